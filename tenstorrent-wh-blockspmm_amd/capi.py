@@ -1,0 +1,297 @@
+"""ctypes binding of libbsparse (include/bsparse.h).
+
+This is plumbing for Python callers (tests, bench.py): every compute call goes
+to the HIP kernels in libbsparse.so.  There is no fallback: if the library is
+missing, load() raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_int, c_int32, c_int64, c_void_p, c_char_p
+from pathlib import Path
+from typing import Optional
+
+import numpy as np
+
+PKG_DIR = Path(__file__).resolve().parent
+LIB_PATH = PKG_DIR / "libbsparse.so"
+
+BSP_OK = 0
+BSP_ERR_INVALID_ARGUMENT = 1
+BSP_ERR_BAD_STRUCTURE = 2
+BSP_ERR_UNSUPPORTED = 3
+BSP_ERR_DEVICE = 4
+BSP_ERR_OUT_OF_MEMORY = 5
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+ROW_MAJOR = 0
+COL_MAJOR = 1
+
+# Every symbol include/bsparse.h declares, with (restype, argtypes).
+_I32P = POINTER(c_int32)
+_I64P = POINTER(c_int64)
+
+
+class BsrDesc(ctypes.Structure):
+    _fields_ = [
+        ("H", c_int64),
+        ("W", c_int64),
+        ("R", c_int64),
+        ("C", c_int64),
+        ("nblocks", c_int64),
+        ("indptr", _I32P),
+        ("indices", _I32P),
+    ]
+
+
+class PlanInfo(ctypes.Structure):
+    _fields_ = [
+        ("kind", c_int32),
+        ("tile_n", c_int32),
+        ("n_tiles", c_int32),
+        ("n_items", c_int32),
+        ("n_entries", c_int32),
+        ("n_split_rows", c_int32),
+        ("n_slots", c_int32),
+        ("grid", c_int32),
+        ("max_item_entries", c_int32),
+        ("reserved", c_int32),
+        ("workspace_bytes", c_int64),
+    ]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_ if name != "reserved"}
+
+
+_DESC_P = POINTER(BsrDesc)
+_INFO_P = POINTER(PlanInfo)
+
+SIGNATURES = {
+    "bsp_abi_version": (c_int, []),
+    "bsp_status_string": (c_char_p, [c_int]),
+    "bsp_last_error": (c_char_p, []),
+    "bsp_validate_bsr": (c_int, [_DESC_P]),
+    "bsp_spmm_plan_create": (c_int, [POINTER(c_void_p), _DESC_P, c_int64, c_int, c_int, c_int]),
+    "bsp_spmm": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p]),
+    "bsp_sddmm_plan_create": (c_int, [POINTER(c_void_p), _DESC_P, c_int64, c_int, c_int, c_int]),
+    "bsp_sddmm": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p]),
+    "bsp_plan_info_get": (c_int, [c_void_p, _INFO_P]),
+    "bsp_plan_destroy": (c_int, [c_void_p]),
+    "bsp_spmm_schedule": (c_int, [_DESC_P, c_int64, c_int, _INFO_P, _I32P, _I32P, _I64P, _I32P]),
+    "bsp_sddmm_schedule": (c_int, [_DESC_P, c_int64, c_int, _INFO_P, _I32P, _I32P, _I64P, _I32P]),
+    "bsp_host_spmm": (c_int, [_DESC_P, c_void_p, c_void_p, c_int64, c_void_p, c_int, c_int]),
+    "bsp_host_sddmm": (c_int, [_DESC_P, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int, c_int]),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+class BsparseError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"bsparse status {status}: {message}")
+        self.status = status
+        self.message = message
+
+
+def load(path: Optional[Path] = None, force_reload: bool = False) -> ctypes.CDLL:
+    """Loads libbsparse.so and declares every entry point; raises if absent."""
+    global _lib
+    if _lib is not None and path is None and not force_reload:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise ImportError(
+            f"{p} not found: build it with __graft_entry__.build() "
+            "(the HIP kernels are the only implementation)")
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)  # AttributeError if a declared symbol is missing
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    return load().bsp_last_error().decode()
+
+
+def check(status: int) -> None:
+    if status != BSP_OK:
+        raise BsparseError(status, last_error())
+
+
+def _i32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.int32)
+
+
+class Bsr:
+    """BSR structure (the index half of bsr_matrix<T>,
+    sparse_common/bsr_matrix.hpp:205-213)."""
+
+    def __init__(self, H: int, W: int, R: int, C: int, indptr, indices):
+        self.H, self.W, self.R, self.C = int(H), int(W), int(R), int(C)
+        self.indptr = _i32(indptr)
+        self.indices = _i32(indices)
+
+    @property
+    def nblocks(self) -> int:
+        return int(self.indices.size)
+
+    @property
+    def nbrows(self) -> int:
+        return self.H // self.R
+
+    def desc(self, nblocks: Optional[int] = None) -> BsrDesc:
+        d = BsrDesc()
+        d.H, d.W, d.R, d.C = self.H, self.W, self.R, self.C
+        d.nblocks = self.nblocks if nblocks is None else nblocks
+        d.indptr = self.indptr.ctypes.data_as(_I32P)
+        d.indices = self.indices.ctypes.data_as(_I32P) if self.indices.size else ctypes.cast(None, _I32P)
+        return d
+
+
+def validate(bsr: Bsr) -> int:
+    d = bsr.desc()
+    return load().bsp_validate_bsr(ctypes.byref(d))
+
+
+def _ptr(x) -> Optional[int]:
+    """Device/host address of a torch tensor or numpy array (or an int)."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    if isinstance(x, np.ndarray):
+        return x.ctypes.data
+    return x.data_ptr()
+
+
+def _dtype_code(out_dtype) -> int:
+    if out_dtype in ("f32", "float32", DTYPE_F32):
+        return DTYPE_F32
+    if out_dtype in ("bf16", "bfloat16", DTYPE_BF16):
+        return DTYPE_BF16
+    raise ValueError(f"unsupported output dtype {out_dtype!r}")
+
+
+class _Plan:
+    def __init__(self):
+        self._h = c_void_p()
+
+    @property
+    def handle(self) -> c_void_p:
+        if not self._h:
+            raise RuntimeError("plan is destroyed")
+        return self._h
+
+    def info(self) -> dict:
+        inf = PlanInfo()
+        check(load().bsp_plan_info_get(self.handle, ctypes.byref(inf)))
+        return inf.as_dict()
+
+    def close(self) -> None:
+        if self._h:
+            load().bsp_plan_destroy(self._h)
+            self._h = c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class SpmmPlan(_Plan):
+    """Plan for C[M x N] = A (BSR) * B[K x N] on one device."""
+
+    def __init__(self, bsr: Bsr, N: int, out_dtype="f32", device: int = 0):
+        super().__init__()
+        self.bsr, self.N, self.out_dtype = bsr, int(N), _dtype_code(out_dtype)
+        d = bsr.desc()
+        check(load().bsp_spmm_plan_create(ctypes.byref(self._h), ctypes.byref(d), self.N, ROW_MAJOR,
+                                          self.out_dtype, device))
+
+    def run(self, a_vals, b, c, ldb: Optional[int] = None, ldc: Optional[int] = None,
+            stream: Optional[int] = None) -> None:
+        check(load().bsp_spmm(self.handle, _ptr(a_vals), _ptr(b), ldb or self.N, _ptr(c),
+                              ldc or self.N, stream))
+
+
+class SddmmPlan(_Plan):
+    """Plan for out = mask (.) (X[M x K] * Y[K x N]) at the mask's blocks."""
+
+    def __init__(self, mask: Bsr, K: int, y_layout: int = ROW_MAJOR, out_dtype="f32", device: int = 0):
+        super().__init__()
+        self.mask, self.K, self.y_layout = mask, int(K), int(y_layout)
+        self.out_dtype = _dtype_code(out_dtype)
+        d = mask.desc()
+        check(load().bsp_sddmm_plan_create(ctypes.byref(self._h), ctypes.byref(d), self.K, self.y_layout,
+                                           self.out_dtype, device))
+
+    def run(self, mask_vals, x, y, out_vals, ldx: Optional[int] = None, ldy: Optional[int] = None,
+            stream: Optional[int] = None) -> None:
+        if ldy is None:
+            ldy = self.mask.W if self.y_layout == ROW_MAJOR else self.K
+        check(load().bsp_sddmm(self.handle, _ptr(mask_vals), _ptr(x), ldx or self.K, _ptr(y), ldy,
+                               _ptr(out_vals), stream))
+
+
+def _schedule(fn_name: str, bsr: Bsr, n: int, num_cus: int) -> dict:
+    lib = load()
+    fn = getattr(lib, fn_name)
+    d = bsr.desc()
+    inf = PlanInfo()
+    null32, null64 = ctypes.cast(None, _I32P), ctypes.cast(None, _I64P)
+    check(fn(ctypes.byref(d), n, num_cus, ctypes.byref(inf), null32, null32, null64, null32))
+    items = np.zeros((max(inf.n_items, 1), 6), np.int32)
+    ent_row = np.zeros(max(inf.n_entries, 1), np.int32)
+    ent_off = np.zeros(max(inf.n_entries, 1), np.int64)
+    wgmap = np.zeros(max(inf.grid, 1), np.int32)
+    check(fn(ctypes.byref(d), n, num_cus, ctypes.byref(inf), items.ctypes.data_as(_I32P),
+             ent_row.ctypes.data_as(_I32P), ent_off.ctypes.data_as(_I64P), wgmap.ctypes.data_as(_I32P)))
+    return {
+        "info": inf.as_dict(),
+        "items": items[: inf.n_items],
+        "ent_row": ent_row[: inf.n_entries],
+        "ent_off": ent_off[: inf.n_entries],
+        "wgmap": wgmap[: inf.grid],
+    }
+
+
+def spmm_schedule(bsr: Bsr, N: int, num_cus: int = 256) -> dict:
+    return _schedule("bsp_spmm_schedule", bsr, N, num_cus)
+
+
+def sddmm_schedule(mask: Bsr, K: int, num_cus: int = 256) -> dict:
+    return _schedule("bsp_sddmm_schedule", mask, K, num_cus)
+
+
+def host_spmm(bsr: Bsr, a_vals: np.ndarray, b: np.ndarray, out_dtype="f32", device: int = 0) -> np.ndarray:
+    """Blocking host-buffer SpMM (the HostCodeFunctionPtr shape)."""
+    code = _dtype_code(out_dtype)
+    a_vals = np.ascontiguousarray(a_vals, dtype=np.uint16)
+    b = np.ascontiguousarray(b, dtype=np.uint16)
+    N = b.shape[1]
+    out = np.empty((bsr.H, N), np.float32 if code == DTYPE_F32 else np.uint16)
+    d = bsr.desc()
+    check(load().bsp_host_spmm(ctypes.byref(d), a_vals.ctypes.data, b.ctypes.data, N, out.ctypes.data,
+                               code, device))
+    return out
+
+
+def host_sddmm(mask: Bsr, mask_vals: np.ndarray, x: np.ndarray, y: np.ndarray, out_dtype="f32",
+               device: int = 0) -> np.ndarray:
+    """Blocking host-buffer SDDMM (the SDDMMHostCodeFunctionPtr shape); returns block values."""
+    code = _dtype_code(out_dtype)
+    mask_vals = np.ascontiguousarray(mask_vals, dtype=np.uint16)
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    y = np.ascontiguousarray(y, dtype=np.uint16)
+    K = x.shape[1]
+    out = np.empty(mask.nblocks * mask.R * mask.C, np.float32 if code == DTYPE_F32 else np.uint16)
+    d = mask.desc()
+    check(load().bsp_host_sddmm(ctypes.byref(d), mask_vals.ctypes.data, x.ctypes.data, y.ctypes.data, K,
+                                out.ctypes.data, code, device))
+    return out

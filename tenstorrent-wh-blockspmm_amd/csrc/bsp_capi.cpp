@@ -1,0 +1,457 @@
+// C ABI of libbsparse: plans, launches and the blocking host-buffer entry
+// points.  See include/bsparse.h for the contract of each function.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "bsp_kernels.hpp"
+#include "bsp_schedule.hpp"
+#include "bsparse.h"
+
+struct bsp_plan {
+    int kind = 0;  // 1 SpMM, 2 SDDMM
+    int device = 0;
+    int out_dtype = BSP_DTYPE_F32;
+    int layout = BSP_ROW_MAJOR;
+    int64_t M = 0, K = 0, N = 0, R = 0, C = 0, nblocks = 0;
+    bsp_plan_info info{};
+    void* d_items = nullptr;
+    int32_t* d_ent_row = nullptr;
+    int64_t* d_ent_off = nullptr;
+    int32_t* d_wgmap = nullptr;
+    float* d_ws = nullptr;
+    int32_t* d_cnt = nullptr;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const std::string& msg) {
+    g_last_error = msg;
+    return status;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    std::string m = std::string(what) + ": " + hipGetErrorString(e);
+    return fail(e == hipErrorOutOfMemory ? BSP_ERR_OUT_OF_MEMORY : BSP_ERR_DEVICE, m);
+}
+
+// Makes `device` current for the lifetime of the guard.
+struct DeviceGuard {
+    int prev = -1;
+    hipError_t err = hipSuccess;
+    explicit DeviceGuard(int device) {
+        err = hipGetDevice(&prev);
+        if (err == hipSuccess && prev != device) err = hipSetDevice(device);
+    }
+    ~DeviceGuard() {
+        if (prev >= 0) (void)hipSetDevice(prev);
+    }
+};
+
+template <typename T>
+hipError_t upload(T** dst, const std::vector<T>& src) {
+    size_t bytes = std::max<size_t>(1, src.size()) * sizeof(T);
+    hipError_t e = hipMalloc((void**)dst, bytes);
+    if (e != hipSuccess) return e;
+    if (!src.empty()) e = hipMemcpy(*dst, src.data(), src.size() * sizeof(T), hipMemcpyHostToDevice);
+    return e;
+}
+
+void free_plan_buffers(bsp_plan* p) {
+    if (p->d_items) (void)hipFree(p->d_items);
+    if (p->d_ent_row) (void)hipFree(p->d_ent_row);
+    if (p->d_ent_off) (void)hipFree(p->d_ent_off);
+    if (p->d_wgmap) (void)hipFree(p->d_wgmap);
+    if (p->d_ws) (void)hipFree(p->d_ws);
+    if (p->d_cnt) (void)hipFree(p->d_cnt);
+    p->d_items = nullptr;
+    p->d_ent_row = nullptr;
+    p->d_ent_off = nullptr;
+    p->d_wgmap = nullptr;
+    p->d_ws = nullptr;
+    p->d_cnt = nullptr;
+}
+
+int device_cus(int device, int* cus) {
+    int n = 0;
+    hipError_t e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device);
+    if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute(CU count)");
+    *cus = n > 0 ? n : 256;
+    return BSP_OK;
+}
+
+int check_device(int device) {
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count <= 0) return fail(BSP_ERR_DEVICE, "no HIP device available");
+    if (device < 0 || device >= count)
+        return fail(BSP_ERR_INVALID_ARGUMENT, "device " + std::to_string(device) + " out of range");
+    return BSP_OK;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+void fill_info_spmm(const bsp::SpmmSchedule& s, bsp_plan_info* info) {
+    std::memset(info, 0, sizeof(*info));
+    info->kind = 1;
+    info->tile_n = s.tile_n;
+    info->n_tiles = s.n_tiles;
+    info->n_items = (int32_t)s.items.size();
+    info->n_entries = (int32_t)s.ent_row.size();
+    info->n_split_rows = s.n_split_rows;
+    info->n_slots = s.n_slots;
+    info->grid = (int32_t)s.wgmap.size();
+    info->max_item_entries = s.max_item_entries;
+    info->workspace_bytes =
+        (int64_t)s.n_slots * s.n_tiles * bsp::spmm_partial_floats(s.tile_n) * (int64_t)sizeof(float) +
+        (int64_t)s.n_slots * s.n_tiles * (int64_t)sizeof(int32_t);
+}
+
+void fill_info_sddmm(const bsp::SddmmSchedule& s, bsp_plan_info* info) {
+    std::memset(info, 0, sizeof(*info));
+    info->kind = 2;
+    info->n_items = (int32_t)s.items.size();
+    info->n_entries = (int32_t)s.ent_col.size();
+    info->grid = (int32_t)s.wgmap.size();
+    info->max_item_entries = s.max_item_entries;
+}
+
+}  // namespace
+
+extern "C" {
+
+int bsp_abi_version(void) { return BSP_ABI_VERSION; }
+
+const char* bsp_status_string(int status) {
+    switch (status) {
+        case BSP_OK: return "ok";
+        case BSP_ERR_INVALID_ARGUMENT: return "invalid argument";
+        case BSP_ERR_BAD_STRUCTURE: return "malformed BSR structure";
+        case BSP_ERR_UNSUPPORTED: return "unsupported";
+        case BSP_ERR_DEVICE: return "device error";
+        case BSP_ERR_OUT_OF_MEMORY: return "out of memory";
+        default: return "unknown status";
+    }
+}
+
+const char* bsp_last_error(void) { return g_last_error.c_str(); }
+
+int bsp_validate_bsr(const bsp_bsr_desc* desc) {
+    std::string msg;
+    int st = bsp::validate_bsr(desc, msg);
+    if (st != BSP_OK) return fail(st, msg);
+    return BSP_OK;
+}
+
+int bsp_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, bsp_plan_info* info,
+                      int32_t* items, int32_t* ent_row, int64_t* ent_off, int32_t* wgmap) {
+    if (!info) return fail(BSP_ERR_INVALID_ARGUMENT, "info is null");
+    bsp::SpmmSchedule s;
+    std::string msg;
+    int st = bsp::build_spmm_schedule(a, N, num_cus, s, msg);
+    if (st != BSP_OK) return fail(st, msg);
+    fill_info_spmm(s, info);
+    if (items)
+        for (size_t i = 0; i < s.items.size(); ++i) {
+            const bsp::SpmmItem& t = s.items[i];
+            int32_t* o = items + 6 * i;
+            o[0] = t.row; o[1] = t.e_begin; o[2] = t.e_end; o[3] = t.slot; o[4] = t.base; o[5] = t.npieces;
+        }
+    if (ent_row && !s.ent_row.empty()) std::memcpy(ent_row, s.ent_row.data(), s.ent_row.size() * 4);
+    if (ent_off && !s.ent_off.empty()) std::memcpy(ent_off, s.ent_off.data(), s.ent_off.size() * 8);
+    if (wgmap && !s.wgmap.empty()) std::memcpy(wgmap, s.wgmap.data(), s.wgmap.size() * 4);
+    return BSP_OK;
+}
+
+int bsp_sddmm_schedule(const bsp_bsr_desc* m, int64_t K, int num_cus, bsp_plan_info* info,
+                       int32_t* items, int32_t* ent_row, int64_t* ent_off, int32_t* wgmap) {
+    if (!info) return fail(BSP_ERR_INVALID_ARGUMENT, "info is null");
+    bsp::SddmmSchedule s;
+    std::string msg;
+    int st = bsp::build_sddmm_schedule(m, K, num_cus, s, msg);
+    if (st != BSP_OK) return fail(st, msg);
+    fill_info_sddmm(s, info);
+    if (items)
+        for (size_t i = 0; i < s.items.size(); ++i) {
+            const bsp::SddmmItem& t = s.items[i];
+            int32_t* o = items + 6 * i;
+            o[0] = t.x_row0; o[1] = t.e_begin; o[2] = t.e_end; o[3] = 0; o[4] = 0; o[5] = 0;
+        }
+    if (ent_row && !s.ent_col.empty()) std::memcpy(ent_row, s.ent_col.data(), s.ent_col.size() * 4);
+    if (ent_off && !s.ent_off.empty()) std::memcpy(ent_off, s.ent_off.data(), s.ent_off.size() * 8);
+    if (wgmap && !s.wgmap.empty()) std::memcpy(wgmap, s.wgmap.data(), s.wgmap.size() * 4);
+    return BSP_OK;
+}
+
+int bsp_spmm_plan_create(bsp_plan** out, const bsp_bsr_desc* a, int64_t N, int b_layout,
+                         int out_dtype, int device) {
+    if (!out) return fail(BSP_ERR_INVALID_ARGUMENT, "plan output pointer is null");
+    *out = nullptr;
+    if (out_dtype != BSP_DTYPE_F32 && out_dtype != BSP_DTYPE_BF16)
+        return fail(BSP_ERR_INVALID_ARGUMENT, "out_dtype must be BSP_DTYPE_F32 or BSP_DTYPE_BF16");
+    if (b_layout != BSP_ROW_MAJOR && b_layout != BSP_COL_MAJOR)
+        return fail(BSP_ERR_INVALID_ARGUMENT, "b_layout must be BSP_ROW_MAJOR or BSP_COL_MAJOR");
+    if (b_layout != BSP_ROW_MAJOR)
+        return fail(BSP_ERR_UNSUPPORTED, "SpMM takes B row-major (the reference's layout)");
+    std::string msg;
+    int st = bsp::validate_bsr(a, msg);
+    if (st != BSP_OK) return fail(st, msg);
+    st = check_device(device);
+    if (st != BSP_OK) return st;
+    int cus = 256;
+    st = device_cus(device, &cus);
+    if (st != BSP_OK) return st;
+    bsp::SpmmSchedule s;
+    st = bsp::build_spmm_schedule(a, N, cus, s, msg);
+    if (st != BSP_OK) return fail(st, msg);
+
+    DeviceGuard g(device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    bsp_plan* p = new bsp_plan();
+    p->kind = 1;
+    p->device = device;
+    p->out_dtype = out_dtype;
+    p->layout = b_layout;
+    p->M = a->H;
+    p->K = a->W;
+    p->N = N;
+    p->R = a->R;
+    p->C = a->C;
+    p->nblocks = a->nblocks;
+    fill_info_spmm(s, &p->info);
+    hipError_t e = upload((bsp::SpmmItem**)&p->d_items, s.items);
+    if (e == hipSuccess) e = upload(&p->d_ent_row, s.ent_row);
+    if (e == hipSuccess) e = upload(&p->d_ent_off, s.ent_off);
+    if (e == hipSuccess) e = upload(&p->d_wgmap, s.wgmap);
+    if (e == hipSuccess && s.n_slots > 0) {
+        const size_t nf = (size_t)s.n_slots * s.n_tiles * bsp::spmm_partial_floats(s.tile_n);
+        e = hipMalloc((void**)&p->d_ws, nf * sizeof(float));
+        if (e == hipSuccess) e = hipMalloc((void**)&p->d_cnt, (size_t)s.n_slots * s.n_tiles * 4);
+        if (e == hipSuccess) e = hipMemset(p->d_cnt, 0, (size_t)s.n_slots * s.n_tiles * 4);
+    }
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        free_plan_buffers(p);
+        delete p;
+        return hip_fail(e, "SpMM plan upload");
+    }
+    *out = p;
+    return BSP_OK;
+}
+
+int bsp_spmm(const bsp_plan* p, const uint16_t* a_vals, const uint16_t* b, int64_t ldb, void* c,
+             int64_t ldc, void* stream) {
+    if (!p || p->kind != 1) return fail(BSP_ERR_INVALID_ARGUMENT, "not an SpMM plan");
+    if (!b || !c || (p->nblocks > 0 && !a_vals))
+        return fail(BSP_ERR_INVALID_ARGUMENT, "null device pointer");
+    if (ldb < p->N || ldc < p->N) return fail(BSP_ERR_INVALID_ARGUMENT, "ldb and ldc must be >= N");
+    if (ldb % 8 != 0) return fail(BSP_ERR_INVALID_ARGUMENT, "ldb must be a multiple of 8");
+    if (!aligned16(b) || (a_vals && !aligned16(a_vals)))
+        return fail(BSP_ERR_INVALID_ARGUMENT, "A values and B must be 16-byte aligned");
+    const size_t esz = p->out_dtype == BSP_DTYPE_BF16 ? 2 : 4;
+    if (((uintptr_t)c % esz) != 0) return fail(BSP_ERR_INVALID_ARGUMENT, "C is misaligned");
+    DeviceGuard g(p->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    bsp::SpmmArgs args{};
+    args.a = a_vals;
+    args.b = b;
+    args.c = c;
+    args.items = (const bsp::SpmmItem*)p->d_items;
+    args.ent_row = p->d_ent_row;
+    args.ent_off = p->d_ent_off;
+    args.wgmap = p->d_wgmap;
+    args.ws = p->d_ws;
+    args.cnt = p->d_cnt;
+    args.ldb = ldb;
+    args.ldc = ldc;
+    args.lda = (int32_t)p->C;
+    args.n_tiles = p->info.n_tiles;
+    hipError_t e = bsp::launch_spmm(args, p->info.tile_n, p->out_dtype == BSP_DTYPE_BF16,
+                                    p->info.grid, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "SpMM launch");
+    return BSP_OK;
+}
+
+int bsp_sddmm_plan_create(bsp_plan** out, const bsp_bsr_desc* mask, int64_t K, int y_layout,
+                          int out_dtype, int device) {
+    if (!out) return fail(BSP_ERR_INVALID_ARGUMENT, "plan output pointer is null");
+    *out = nullptr;
+    if (out_dtype != BSP_DTYPE_F32 && out_dtype != BSP_DTYPE_BF16)
+        return fail(BSP_ERR_INVALID_ARGUMENT, "out_dtype must be BSP_DTYPE_F32 or BSP_DTYPE_BF16");
+    if (y_layout != BSP_ROW_MAJOR && y_layout != BSP_COL_MAJOR)
+        return fail(BSP_ERR_INVALID_ARGUMENT, "y_layout must be BSP_ROW_MAJOR or BSP_COL_MAJOR");
+    std::string msg;
+    int st = bsp::validate_bsr(mask, msg);
+    if (st != BSP_OK) return fail(st, msg);
+    st = check_device(device);
+    if (st != BSP_OK) return st;
+    int cus = 256;
+    st = device_cus(device, &cus);
+    if (st != BSP_OK) return st;
+    bsp::SddmmSchedule s;
+    st = bsp::build_sddmm_schedule(mask, K, cus, s, msg);
+    if (st != BSP_OK) return fail(st, msg);
+
+    DeviceGuard g(device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    bsp_plan* p = new bsp_plan();
+    p->kind = 2;
+    p->device = device;
+    p->out_dtype = out_dtype;
+    p->layout = y_layout;
+    p->M = mask->H;
+    p->N = mask->W;
+    p->K = K;
+    p->R = mask->R;
+    p->C = mask->C;
+    p->nblocks = mask->nblocks;
+    fill_info_sddmm(s, &p->info);
+    hipError_t e = upload((bsp::SddmmItem**)&p->d_items, s.items);
+    if (e == hipSuccess) e = upload(&p->d_ent_row, s.ent_col);
+    if (e == hipSuccess) e = upload(&p->d_ent_off, s.ent_off);
+    if (e == hipSuccess) e = upload(&p->d_wgmap, s.wgmap);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        free_plan_buffers(p);
+        delete p;
+        return hip_fail(e, "SDDMM plan upload");
+    }
+    *out = p;
+    return BSP_OK;
+}
+
+int bsp_sddmm(const bsp_plan* p, const uint16_t* mask_vals, const uint16_t* x, int64_t ldx,
+              const uint16_t* y, int64_t ldy, void* out_vals, void* stream) {
+    if (!p || p->kind != 2) return fail(BSP_ERR_INVALID_ARGUMENT, "not an SDDMM plan");
+    if (p->nblocks == 0) return BSP_OK;
+    if (!mask_vals || !x || !y || !out_vals) return fail(BSP_ERR_INVALID_ARGUMENT, "null device pointer");
+    if (ldx < p->K) return fail(BSP_ERR_INVALID_ARGUMENT, "ldx must be >= K");
+    if (p->layout == BSP_ROW_MAJOR ? ldy < p->N : ldy < p->K)
+        return fail(BSP_ERR_INVALID_ARGUMENT, "ldy too small for Y's layout");
+    if (ldx % 8 != 0 || ldy % 8 != 0)
+        return fail(BSP_ERR_INVALID_ARGUMENT, "ldx and ldy must be multiples of 8");
+    if (!aligned16(x) || !aligned16(y))
+        return fail(BSP_ERR_INVALID_ARGUMENT, "X and Y must be 16-byte aligned");
+    const size_t esz = p->out_dtype == BSP_DTYPE_BF16 ? 2 : 4;
+    if (((uintptr_t)out_vals % esz) != 0 || ((uintptr_t)mask_vals % 2) != 0)
+        return fail(BSP_ERR_INVALID_ARGUMENT, "output or mask values misaligned");
+    DeviceGuard g(p->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    bsp::SddmmArgs args{};
+    args.mask = mask_vals;
+    args.x = x;
+    args.y = y;
+    args.out = out_vals;
+    args.items = (const bsp::SddmmItem*)p->d_items;
+    args.ent_col = p->d_ent_row;
+    args.ent_off = p->d_ent_off;
+    args.wgmap = p->d_wgmap;
+    args.ldx = ldx;
+    args.ldy = ldy;
+    args.ldo = (int32_t)p->C;
+    args.K = (int32_t)p->K;
+    hipError_t e = bsp::launch_sddmm(args, p->layout == BSP_COL_MAJOR,
+                                     p->out_dtype == BSP_DTYPE_BF16, p->info.grid,
+                                     (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "SDDMM launch");
+    return BSP_OK;
+}
+
+int bsp_plan_info_get(const bsp_plan* p, bsp_plan_info* info) {
+    if (!p || !info) return fail(BSP_ERR_INVALID_ARGUMENT, "null plan or info");
+    *info = p->info;
+    return BSP_OK;
+}
+
+int bsp_plan_destroy(bsp_plan* p) {
+    if (!p) return BSP_OK;
+    DeviceGuard g(p->device);
+    free_plan_buffers(p);
+    delete p;
+    return BSP_OK;
+}
+
+int bsp_host_spmm(const bsp_bsr_desc* a, const uint16_t* a_vals, const uint16_t* b, int64_t N,
+                  void* out, int out_dtype, int device) {
+    if (!b || !out || (a && a->nblocks > 0 && !a_vals))
+        return fail(BSP_ERR_INVALID_ARGUMENT, "null host pointer");
+    bsp_plan* p = nullptr;
+    int st = bsp_spmm_plan_create(&p, a, N, BSP_ROW_MAJOR, out_dtype, device);
+    if (st != BSP_OK) return st;
+    DeviceGuard g(device);
+    const size_t esz = out_dtype == BSP_DTYPE_BF16 ? 2 : 4;
+    const size_t a_bytes = std::max<size_t>(16, (size_t)a->nblocks * a->R * a->C * 2);
+    const size_t b_bytes = (size_t)a->W * N * 2;
+    const size_t c_bytes = (size_t)a->H * N * esz;
+    uint16_t *da = nullptr, *db = nullptr;
+    void* dc = nullptr;
+    hipError_t e = hipMalloc((void**)&da, a_bytes);
+    if (e == hipSuccess) e = hipMalloc((void**)&db, b_bytes);
+    if (e == hipSuccess) e = hipMalloc(&dc, c_bytes);
+    if (e == hipSuccess && a->nblocks > 0)
+        e = hipMemcpy(da, a_vals, (size_t)a->nblocks * a->R * a->C * 2, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(db, b, b_bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+        st = bsp_spmm(p, da, db, N, dc, N, nullptr);
+        if (st == BSP_OK) {
+            e = hipDeviceSynchronize();
+            if (e == hipSuccess) e = hipMemcpy(out, dc, c_bytes, hipMemcpyDeviceToHost);
+        }
+    }
+    if (da) (void)hipFree(da);
+    if (db) (void)hipFree(db);
+    if (dc) (void)hipFree(dc);
+    bsp_plan_destroy(p);
+    if (st != BSP_OK) return st;
+    if (e != hipSuccess) return hip_fail(e, "bsp_host_spmm");
+    return BSP_OK;
+}
+
+int bsp_host_sddmm(const bsp_bsr_desc* mask, const uint16_t* mask_vals, const uint16_t* x,
+                   const uint16_t* y, int64_t K, void* out_vals, int out_dtype, int device) {
+    if (!x || !y || (mask && mask->nblocks > 0 && (!mask_vals || !out_vals)))
+        return fail(BSP_ERR_INVALID_ARGUMENT, "null host pointer");
+    bsp_plan* p = nullptr;
+    int st = bsp_sddmm_plan_create(&p, mask, K, BSP_ROW_MAJOR, out_dtype, device);
+    if (st != BSP_OK) return st;
+    if (mask->nblocks == 0) {
+        bsp_plan_destroy(p);
+        return BSP_OK;
+    }
+    DeviceGuard g(device);
+    const size_t esz = out_dtype == BSP_DTYPE_BF16 ? 2 : 4;
+    const size_t nv = (size_t)mask->nblocks * mask->R * mask->C;
+    const size_t x_bytes = (size_t)mask->H * K * 2;
+    const size_t y_bytes = (size_t)K * mask->W * 2;
+    uint16_t *dm = nullptr, *dx = nullptr, *dy = nullptr;
+    void* dout = nullptr;
+    hipError_t e = hipMalloc((void**)&dm, nv * 2);
+    if (e == hipSuccess) e = hipMalloc((void**)&dx, x_bytes);
+    if (e == hipSuccess) e = hipMalloc((void**)&dy, y_bytes);
+    if (e == hipSuccess) e = hipMalloc(&dout, nv * esz);
+    if (e == hipSuccess) e = hipMemcpy(dm, mask_vals, nv * 2, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(dx, x, x_bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(dy, y, y_bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+        st = bsp_sddmm(p, dm, dx, K, dy, mask->W, dout, nullptr);
+        if (st == BSP_OK) {
+            e = hipDeviceSynchronize();
+            if (e == hipSuccess) e = hipMemcpy(out_vals, dout, nv * esz, hipMemcpyDeviceToHost);
+        }
+    }
+    if (dm) (void)hipFree(dm);
+    if (dx) (void)hipFree(dx);
+    if (dy) (void)hipFree(dy);
+    if (dout) (void)hipFree(dout);
+    bsp_plan_destroy(p);
+    if (st != BSP_OK) return st;
+    if (e != hipSuccess) return hip_fail(e, "bsp_host_sddmm");
+    return BSP_OK;
+}
+
+}  // extern "C"

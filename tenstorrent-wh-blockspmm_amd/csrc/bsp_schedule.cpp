@@ -1,0 +1,269 @@
+// Host-side schedule construction for the SpMM and SDDMM kernels.
+//
+// Replaces the reference's per-call host analysis: folding of empty block
+// rows and serpentine assignment of rows to Tensix core rows
+// (block_spmm/inc/host_code/bsr_spmm_multicore_load_balanced_new_DM.cpp:50-61,
+// :339-393), and the SDDMM flat block split / first-fit packing
+// (block_sddmm/inc/host_code/bsr_sddmm_multicore_naive.cpp:154-166, :267-310;
+// bsr_sddmm_multicore_CDA.cpp:95-187).  Here the unit of work is a run of
+// 32x32 sub-block products of one 32-row output stripe; rows longer than a
+// limit derived from the nnz prefix are cut into pieces, and the pieces are
+// spread over the GPU's XCDs longest-first.
+#include "bsp_schedule.hpp"
+
+#include <algorithm>
+#include <cstdlib>
+#include <numeric>
+#include <queue>
+
+namespace bsp {
+
+namespace {
+
+int64_t env_int(const char* name, int64_t dflt) {
+    const char* v = std::getenv(name);
+    if (!v || !*v) return dflt;
+    char* end = nullptr;
+    long long x = std::strtoll(v, &end, 10);
+    return (end && *end == 0) ? (int64_t)x : dflt;
+}
+
+}  // namespace
+
+int validate_bsr(const bsp_bsr_desc* d, std::string& msg) {
+    if (!d) {
+        msg = "null BSR descriptor";
+        return BSP_ERR_INVALID_ARGUMENT;
+    }
+    if (d->R <= 0 || d->C <= 0 || d->H <= 0 || d->W <= 0) {
+        msg = "H, W, R, C must be positive";
+        return BSP_ERR_BAD_STRUCTURE;
+    }
+    if (d->H % d->R != 0 || d->W % d->C != 0) {
+        msg = "H must be a multiple of R and W a multiple of C";
+        return BSP_ERR_BAD_STRUCTURE;
+    }
+    if (d->nblocks < 0 || d->nblocks * d->R * d->C > d->H * d->W) {
+        msg = "nblocks must satisfy 0 <= nblocks*R*C <= H*W";
+        return BSP_ERR_BAD_STRUCTURE;
+    }
+    if (d->H / d->R > INT32_MAX - 1 || d->nblocks > INT32_MAX) {
+        msg = "structure too large for int32 indices";
+        return BSP_ERR_UNSUPPORTED;
+    }
+    if (!d->indptr) {
+        msg = "indptr is null";
+        return BSP_ERR_INVALID_ARGUMENT;
+    }
+    if (d->nblocks > 0 && !d->indices) {
+        msg = "indices is null";
+        return BSP_ERR_INVALID_ARGUMENT;
+    }
+    const int64_t nbr = d->H / d->R, nbc = d->W / d->C;
+    if (d->indptr[0] != 0) {
+        msg = "indptr[0] must be 0";
+        return BSP_ERR_BAD_STRUCTURE;
+    }
+    for (int64_t i = 0; i < nbr; ++i) {
+        if (d->indptr[i + 1] < d->indptr[i]) {
+            msg = "indptr must be non-decreasing (row " + std::to_string(i) + ")";
+            return BSP_ERR_BAD_STRUCTURE;
+        }
+    }
+    if ((int64_t)d->indptr[nbr] != d->nblocks) {
+        msg = "indptr[H/R] = " + std::to_string(d->indptr[nbr]) + " but nblocks = " +
+              std::to_string(d->nblocks);
+        return BSP_ERR_BAD_STRUCTURE;
+    }
+    for (int64_t e = 0; e < d->nblocks; ++e) {
+        if (d->indices[e] < 0 || d->indices[e] >= nbc) {
+            msg = "indices[" + std::to_string(e) + "] = " + std::to_string(d->indices[e]) +
+                  " outside [0, W/C = " + std::to_string(nbc) + ")";
+            return BSP_ERR_BAD_STRUCTURE;
+        }
+    }
+    return BSP_OK;
+}
+
+std::vector<int32_t> xcd_lpt_map(const std::vector<int64_t>& unit_cost, int width) {
+    const int64_t nunits = (int64_t)unit_cost.size();
+    std::vector<int32_t> order(nunits);
+    std::iota(order.begin(), order.end(), 0);
+    // Longest first; ties by index so the map is deterministic.
+    std::stable_sort(order.begin(), order.end(),
+                     [&](int32_t a, int32_t b) { return unit_cost[a] > unit_cost[b]; });
+    std::vector<std::vector<int32_t>> bins(kNumXcd);
+    using Load = std::pair<int64_t, int>;  // (load, xcd)
+    std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
+    for (int x = 0; x < kNumXcd; ++x) heap.push({0, x});
+    for (int32_t u : order) {
+        Load l = heap.top();
+        heap.pop();
+        for (int t = 0; t < width; ++t) bins[l.second].push_back(u * width + t);
+        heap.push({l.first + unit_cost[u] * width, l.second});
+    }
+    size_t maxlen = 0;
+    for (auto& b : bins) maxlen = std::max(maxlen, b.size());
+    std::vector<int32_t> map(maxlen * kNumXcd, -1);
+    for (int x = 0; x < kNumXcd; ++x)
+        for (size_t j = 0; j < bins[x].size(); ++j) map[j * kNumXcd + x] = bins[x][j];
+    return map;
+}
+
+int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSchedule& s,
+                        std::string& msg) {
+    int st = validate_bsr(a, msg);
+    if (st != BSP_OK) return st;
+    if (N <= 0) {
+        msg = "N must be positive";
+        return BSP_ERR_INVALID_ARGUMENT;
+    }
+    if (a->R % kSub || a->C % kSub || N % kSub) {
+        msg = "R, C and N must be multiples of 32";
+        return BSP_ERR_UNSUPPORTED;
+    }
+    if (num_cus <= 0) num_cus = 256;
+    const int64_t RS = a->R / kSub, CS = a->C / kSub;
+    const int64_t nbr = a->H / a->R;
+    const int64_t nsr = a->H / kSub;
+    const int64_t total = a->nblocks * RS * CS;
+    if (total > INT32_MAX || a->W > INT32_MAX || nsr > INT32_MAX) {
+        msg = "problem too large for int32 schedule fields";
+        return BSP_ERR_UNSUPPORTED;
+    }
+
+    // Output tile width: the widest of 256/128/64/32 dividing N that still
+    // leaves at least two workgroups per compute unit; else the narrowest.
+    int64_t tn = env_int("BSP_SPMM_TILE_N", 0);
+    if (tn != 0 && (tn != 32 && tn != 64 && tn != 128 && tn != 256)) tn = 0;
+    if (tn != 0 && N % tn != 0) tn = 0;
+    if (tn == 0) {
+        const int64_t cands[] = {256, 128, 64, 32};
+        for (int64_t c : cands) {
+            if (N % c) continue;
+            tn = c;
+            if (nsr * (N / c) >= 2 * (int64_t)num_cus) break;
+        }
+    }
+    s.tile_n = (int32_t)tn;
+    s.n_tiles = (int32_t)(N / tn);
+
+    // Split limit: a piece holds at most L entries.  L is the larger of twice
+    // the mean length of non-empty rows (uniform rows stay whole) and half of
+    // one compute unit's fair share of the total (skewed rows are cut so no
+    // workgroup dwarfs the rest), and at least 32.
+    int64_t nonempty = 0;
+    for (int64_t i = 0; i < nbr; ++i) nonempty += (a->indptr[i + 1] > a->indptr[i]) ? RS : 0;
+    const int64_t mean = nonempty ? (total + nonempty - 1) / nonempty : 0;
+    const int64_t fair = (total * s.n_tiles + num_cus - 1) / num_cus;
+    int64_t L = std::max<int64_t>({32, 2 * mean, (fair + 1) / 2});
+    L = env_int("BSP_SPMM_SPLIT", L);
+    if (L < 1) L = 1;
+    s.split_limit = (int32_t)L;
+
+    s.items.clear();
+    s.ent_row.clear();
+    s.ent_off.clear();
+    s.ent_row.reserve(total);
+    s.ent_off.reserve(total);
+    s.n_slots = 0;
+    s.n_split_rows = 0;
+    s.max_item_entries = 0;
+    std::vector<int64_t> cost;
+    for (int64_t sr = 0; sr < nsr; ++sr) {
+        const int64_t i = sr / RS, sub = sr % RS;
+        const int32_t e0 = (int32_t)s.ent_row.size();
+        for (int64_t blk = a->indptr[i]; blk < a->indptr[i + 1]; ++blk) {
+            for (int64_t t = 0; t < CS; ++t) {
+                s.ent_row.push_back((int32_t)((int64_t)a->indices[blk] * a->C + kSub * t));
+                s.ent_off.push_back(blk * a->R * a->C + kSub * sub * a->C + kSub * t);
+            }
+        }
+        const int32_t e1 = (int32_t)s.ent_row.size();
+        const int64_t cnt = e1 - e0;
+        // Cost model: one unit per 32x32 product plus a fixed share for the
+        // stripe's output store (split pieces add a partial round trip).
+        if (cnt <= L) {
+            s.items.push_back({(int32_t)sr, e0, e1, -1, -1, 0});
+            cost.push_back(cnt + 2);
+            s.max_item_entries = std::max<int32_t>(s.max_item_entries, (int32_t)cnt);
+        } else {
+            const int64_t np = (cnt + L - 1) / L;
+            const int32_t base = s.n_slots;
+            s.n_slots += (int32_t)np;
+            s.n_split_rows += 1;
+            for (int64_t p = 0; p < np; ++p) {
+                const int32_t b0 = e0 + (int32_t)(cnt * p / np);
+                const int32_t b1 = e0 + (int32_t)(cnt * (p + 1) / np);
+                s.items.push_back({(int32_t)sr, b0, b1, base + (int32_t)p, base, (int32_t)np});
+                cost.push_back((b1 - b0) + 4);
+                s.max_item_entries = std::max<int32_t>(s.max_item_entries, b1 - b0);
+            }
+        }
+    }
+    if ((int64_t)s.items.size() * s.n_tiles > INT32_MAX / 2) {
+        msg = "too many work items";
+        return BSP_ERR_UNSUPPORTED;
+    }
+    s.wgmap = xcd_lpt_map(cost, s.n_tiles);
+    return BSP_OK;
+}
+
+int build_sddmm_schedule(const bsp_bsr_desc* m, int64_t K, int num_cus, SddmmSchedule& s,
+                         std::string& msg) {
+    int st = validate_bsr(m, msg);
+    if (st != BSP_OK) return st;
+    if (K <= 0) {
+        msg = "K must be positive";
+        return BSP_ERR_INVALID_ARGUMENT;
+    }
+    if (m->R % kSub || m->C % kSub || K % kSub) {
+        msg = "R, C and K must be multiples of 32";
+        return BSP_ERR_UNSUPPORTED;
+    }
+    if (num_cus <= 0) num_cus = 256;
+    const int64_t RS = m->R / kSub, CS = m->C / kSub;
+    const int64_t nsr = m->H / kSub;
+    const int64_t total = m->nblocks * RS * CS;
+    if (total > INT32_MAX || m->W > INT32_MAX || m->H > INT32_MAX) {
+        msg = "problem too large for int32 schedule fields";
+        return BSP_ERR_UNSUPPORTED;
+    }
+    // Entries per item: a multiple of 4 (one per wave), sized for about two
+    // workgroups per compute unit, between 4 and 32.
+    int64_t q = (total + 2 * num_cus - 1) / (2 * (int64_t)num_cus);
+    q = std::min<int64_t>(32, std::max<int64_t>(4, (q + 3) / 4 * 4));
+    q = env_int("BSP_SDDMM_CHUNK", q);
+    if (q < 1) q = 1;
+    s.chunk = (int32_t)q;
+
+    s.items.clear();
+    s.ent_col.clear();
+    s.ent_off.clear();
+    s.ent_col.reserve(total);
+    s.ent_off.reserve(total);
+    s.max_item_entries = 0;
+    std::vector<int64_t> cost;
+    for (int64_t sr = 0; sr < nsr; ++sr) {
+        const int64_t i = sr / RS, sub = sr % RS;
+        const int32_t e0 = (int32_t)s.ent_col.size();
+        for (int64_t blk = m->indptr[i]; blk < m->indptr[i + 1]; ++blk) {
+            for (int64_t t = 0; t < CS; ++t) {
+                s.ent_col.push_back((int32_t)((int64_t)m->indices[blk] * m->C + kSub * t));
+                s.ent_off.push_back(blk * m->R * m->C + kSub * sub * m->C + kSub * t);
+            }
+        }
+        const int32_t e1 = (int32_t)s.ent_col.size();
+        for (int32_t b = e0; b < e1; b += (int32_t)q) {
+            const int32_t b1 = std::min<int32_t>(e1, b + (int32_t)q);
+            s.items.push_back({(int32_t)(sr * kSub), b, b1, 0});
+            // Four waves share an item: its time is the longest wave's share.
+            cost.push_back((b1 - b + 3) / 4 + 1);
+            s.max_item_entries = std::max<int32_t>(s.max_item_entries, b1 - b);
+        }
+    }
+    s.wgmap = xcd_lpt_map(cost, 1);
+    return BSP_OK;
+}
+
+}  // namespace bsp

@@ -1,0 +1,79 @@
+// Host-side analysis of a BSR structure into the work lists the HIP kernels
+// walk.  Pure C++ (no HIP), so it runs and is tested without a device.
+#pragma once
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "bsparse.h"
+
+namespace bsp {
+
+// Width of the sub-block every kernel works in: R x C blocks are cut into
+// (R/32) x (C/32) sub-blocks of 32 x 32 (the reference's TILE_SIZE,
+// sparse_common/bsr_matrix.hpp:22).
+constexpr int kSub = 32;
+// MI355X has 8 XCDs; workgroups are handed to XCDs round-robin by workgroup id.
+constexpr int kNumXcd = 8;
+
+// One unit of SpMM work: a contiguous range of a sub-row's entries.
+struct SpmmItem {
+    int32_t row;      // sub-row (32 output rows)
+    int32_t e_begin;  // entries [e_begin, e_end) of the entry arrays
+    int32_t e_end;
+    int32_t slot;     // -1: whole row; else partial-result slot of this piece
+    int32_t base;     // first slot of the row's pieces (also its counter index)
+    int32_t npieces;  // pieces the row is split into (0 for a whole row)
+};
+static_assert(sizeof(SpmmItem) == 24, "SpmmItem layout is shared with the kernels");
+
+struct SpmmSchedule {
+    int32_t tile_n = 0;
+    int32_t n_tiles = 0;
+    int32_t split_limit = 0;  // max entries per piece
+    int32_t n_slots = 0;
+    int32_t n_split_rows = 0;
+    int32_t max_item_entries = 0;
+    std::vector<SpmmItem> items;
+    std::vector<int32_t> ent_row;  // first row of B for the entry
+    std::vector<int64_t> ent_off;  // element offset of the 32x32 A sub-block
+    std::vector<int32_t> wgmap;    // workgroup id -> item * n_tiles + tile, or -1
+};
+
+// One unit of SDDMM work: a run of output sub-blocks that share 32 rows of X.
+struct SddmmItem {
+    int32_t x_row0;
+    int32_t e_begin;
+    int32_t e_end;
+    int32_t pad;
+};
+static_assert(sizeof(SddmmItem) == 16, "SddmmItem layout is shared with the kernels");
+
+struct SddmmSchedule {
+    int32_t chunk = 0;  // max entries per item
+    int32_t max_item_entries = 0;
+    std::vector<SddmmItem> items;
+    std::vector<int32_t> ent_col;  // first column of Y for the entry
+    std::vector<int64_t> ent_off;  // element offset of the 32x32 output sub-block
+    std::vector<int32_t> wgmap;    // workgroup id -> item, or -1
+};
+
+// Structural checks of sparse_common/bsr_matrix.hpp:246-252 / :610-616 plus
+// the CSR invariants the golden relies on implicitly.  On failure returns a
+// bsp_status and fills `msg`.
+int validate_bsr(const bsp_bsr_desc* d, std::string& msg);
+
+int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSchedule& out,
+                        std::string& msg);
+int build_sddmm_schedule(const bsp_bsr_desc* mask, int64_t K, int num_cus, SddmmSchedule& out,
+                         std::string& msg);
+
+// Spreads weighted units over the XCDs (longest first onto the least-loaded
+// XCD), then lays them out so that workgroup id g runs on XCD g % kNumXcd in
+// each XCD's longest-first order.  Unit u expands to `width` consecutive
+// workgroups (the N tiles of one SpMM item stay on one XCD, so the A blocks
+// they share are read into one L2).  Returns the workgroup map; -1 = idle.
+std::vector<int32_t> xcd_lpt_map(const std::vector<int64_t>& unit_cost, int width);
+
+}  // namespace bsp

@@ -1,0 +1,145 @@
+"""Shared test helpers: package/oracle loading, device runners through the C
+ABI, and the parity criterion."""
+from __future__ import annotations
+
+import os
+import sys
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent.parent
+sys.path.insert(0, str(REPO))
+import __graft_entry__ as entry  # noqa: E402
+
+pkg = entry.load_package()
+capi = pkg.capi
+W = pkg.workloads
+orc = entry._load_oracle()
+
+# Host threads for the oracle: the GPU box gives one GPU's share (16 cores).
+ORACLE_THREADS = min(16, os.cpu_count() or 1)
+
+
+def bsr_of(a) -> "capi.Bsr":
+    return capi.Bsr(a.H, a.W, a.R, a.C, a.indptr, a.indices)
+
+
+# ---------------------------------------------------------------------------
+# Parity criterion.
+def tolerance(golden: np.ndarray, k_eff) -> np.ndarray:
+    """Elementwise bound |y - g| <= 1e-2 * sqrt(K_e / 32) * max(1, |g|), with
+    K_e the reduction length of the element (SpMM: stored blocks in the row
+    times C; SDDMM: K)."""
+    k = np.maximum(np.asarray(k_eff, dtype=np.float64), 32.0)
+    return 1e-2 * np.sqrt(k / 32.0) * np.maximum(1.0, np.abs(golden.astype(np.float64)))
+
+
+def spmm_k_eff(a) -> np.ndarray:
+    """Reduction length per output row: C times the blocks stored in its block row."""
+    return np.repeat(np.diff(a.indptr).astype(np.int64) * a.C, a.R)[:, None]
+
+
+def compare(got: np.ndarray, golden: np.ndarray, k_eff) -> dict:
+    got = np.asarray(got, dtype=np.float64)
+    g = np.asarray(golden, dtype=np.float64)
+    err = np.abs(got - g)
+    bound = tolerance(g, k_eff)
+    finite = np.isfinite(got).all()
+    rel = err / np.maximum(np.abs(g), 1e-30)
+    res = {
+        "ok": bool(finite and np.all(err <= bound)),
+        "max_abs": float(err.max()) if err.size else 0.0,
+        "max_rel_over_1": float((err / np.maximum(1.0, np.abs(g))).max()) if err.size else 0.0,
+        "max_rel": float(rel[np.abs(g) > 1e-3].max()) if (np.abs(g) > 1e-3).any() else 0.0,
+        "worst_ratio": float((err / bound).max()) if err.size else 0.0,
+        "finite": bool(finite),
+    }
+    if g.size > 1 and np.std(g) > 0:
+        res["pcc"] = orc.pcc(got.astype(np.float32), g.astype(np.float32))
+    return res
+
+
+def assert_parity(got, golden, k_eff, what=""):
+    res = compare(got, golden, k_eff)
+    assert res["ok"], f"{what}: parity failed {res}"
+    return res
+
+
+# ---------------------------------------------------------------------------
+# Device runners (C ABI, device pointers on torch's current stream).
+def _dev_u16(arr: np.ndarray):
+    import torch
+    arr = np.ascontiguousarray(arr, dtype=np.uint16)
+    if arr.size == 0:
+        return torch.zeros(8, dtype=torch.int16, device="cuda")
+    return torch.from_numpy(arr.view(np.int16)).to("cuda")
+
+
+def run_spmm(a, b: np.ndarray, out_dtype="f32", plan=None, poison=True) -> np.ndarray:
+    """C = A*B on the GPU; returns fp32 (bf16 outputs widened exactly)."""
+    import torch
+    M, N = a.H, b.shape[1]
+    own = plan is None
+    if own:
+        plan = capi.SpmmPlan(bsr_of(a), N, out_dtype)
+    da = _dev_u16(a.data if a.data is not None else np.zeros(0, np.uint16))
+    db = _dev_u16(b)
+    if out_dtype == "f32":
+        dc = torch.full((M, N), float("nan") if poison else 0.0, dtype=torch.float32, device="cuda")
+    else:
+        dc = torch.full((M, N), 0x7FC0 if poison else 0, dtype=torch.int16, device="cuda")
+    plan.run(da, db, dc, stream=torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    out = dc.cpu().numpy()
+    if own:
+        plan.close()
+    if out_dtype == "f32":
+        return out
+    return W.bf16_to_f32(out.view(np.uint16))
+
+
+def run_sddmm(mask, x: np.ndarray, y: np.ndarray, out_dtype="f32", y_layout=None, plan=None,
+              poison=True) -> np.ndarray:
+    """mask (.) (X*Y) block values on the GPU; y is passed as given (K x N for
+    ROW_MAJOR, N x K for COL_MAJOR)."""
+    import torch
+    if y_layout is None:
+        y_layout = capi.ROW_MAJOR
+    K = x.shape[1]
+    own = plan is None
+    if own:
+        plan = capi.SddmmPlan(bsr_of(mask), K, y_layout, out_dtype)
+    nv = mask.nblocks * mask.R * mask.C
+    dm = _dev_u16(mask.data)
+    dx = _dev_u16(x)
+    dy = _dev_u16(y)
+    if out_dtype == "f32":
+        do = torch.full((max(nv, 1),), float("nan") if poison else 0.0, dtype=torch.float32, device="cuda")
+    else:
+        do = torch.full((max(nv, 1),), 0x7FC0 if poison else 0, dtype=torch.int16, device="cuda")
+    ldy = mask.W if y_layout == capi.ROW_MAJOR else K
+    plan.run(dm, dx, dy, do, ldy=ldy, stream=torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    out = do.cpu().numpy()[:nv]
+    if own:
+        plan.close()
+    if out_dtype == "f32":
+        return out
+    return W.bf16_to_f32(out.view(np.uint16))
+
+
+def golden_spmm(a, b, threads=ORACLE_THREADS) -> np.ndarray:
+    return orc.spmm(a.indptr, a.indices, a.data, a.H, a.W, a.R, a.C, b, threads=threads)
+
+
+def golden_sddmm(mask, x, y, y_colmajor=False, threads=ORACLE_THREADS) -> np.ndarray:
+    return orc.sddmm(mask.indptr, mask.indices, mask.data, mask.H, mask.W, mask.R, mask.C, x, y,
+                     y_colmajor=y_colmajor, threads=threads)
+
+
+def with_values(s, content="RAND", seed=0):
+    """Attaches block values of a content type to a structure."""
+    rng = np.random.default_rng(seed)
+    s.data = W.block_content(s.nblocks, s.R, s.C, content, rng)
+    return s
