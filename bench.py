@@ -1,0 +1,330 @@
+"""Benchmark: effective TFLOP/s of block-sparse SpMM on one MI355X.
+
+Workload (the headline): C = A*B with A 4096x4096 in 32x32 bf16 blocks at 25%
+uniform-random block density, B 4096x512 bf16, fp32 accumulation and fp32
+output.  The same run reports the whole density sweep {1, 5, 25, 50}% (fp32
+and bf16 outputs), and one line each for the SDDMM, skewed-SpMM and
+attention-pair workloads.
+
+A step is one SpMM launch over the whole workload.  Inputs are resident in
+HBM: the timed loop cycles through enough copies of A, B and C (> 512 MB) that
+no launch finds its operands in the 256 MB Infinity Cache.  Effective
+TFLOP/s counts only nonzero-block FLOPs, 2*nnzb*R*C*N (the reference's formula,
+GEMM_profiling/read_spmm_profiler.py:73).
+
+Per-launch kernel time is measured with HIP events recorded on the stream the
+kernel is launched on, around each launch; the whole-job figure (`value`) is
+total FLOPs over the wall time of the K timed steps between device
+synchronisations.
+
+The CPU baseline is the oracle (the C restatement of the reference's golden,
+oracle/bsp_oracle.c) on this host: all cores on the whole 25% workload, and
+one core on a 32-block-row sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (AMD Instinct MI355X datasheet)
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+ROTATE_BYTES = 600 << 20   # > 2 x the 256 MB Infinity Cache
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="first run one 256 MiB device-to-device copy (a kernel of known traffic, "
+                        "for scaling FETCH_SIZE / WRITE_SIZE counters)")
+    p.add_argument("--only", default="", help="comma list of sections to run: head (25%% fp32 only), sweep, sddmm, skewed, attention")
+    return p.parse_args()
+
+
+class Timer:
+    """HIP events on the launch stream: per-launch kernel time and the wall
+    time of the whole timed region."""
+
+    def __init__(self, torch, steps):
+        self.torch = torch
+        self.ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                   for _ in range(steps)]
+
+    def run(self, launch, steps, warmup):
+        torch = self.torch
+        for i in range(warmup):
+            launch(i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            s, e = self.ev[i]
+            s.record()
+            launch(warmup + i)
+            e.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        per = [s.elapsed_time(e) for s, e in self.ev[:steps]]  # ms
+        return {"wall_s": wall, "kernel_ms_mean": float(np.mean(per)),
+                "kernel_ms_median": float(np.median(per)), "kernel_ms_min": float(np.min(per))}
+
+
+def dev_u16(torch, arr):
+    arr = np.ascontiguousarray(arr, dtype=np.uint16)
+    return torch.from_numpy(arr.view(np.int16)).to("cuda")
+
+
+def bench_spmm(torch, capi, W, a, b, out_dtype, steps, warmup, rotate=True):
+    """Times SpMM on (a, b); returns timings, FLOPs and algorithmic bytes."""
+    M, K, N = a.H, a.W, b.shape[1]
+    plan = capi.SpmmPlan(capi.Bsr(a.H, a.W, a.R, a.C, a.indptr, a.indices), N, out_dtype)
+    out_bytes = 4 if out_dtype == "f32" else 2
+    per_copy = a.data.nbytes + b.nbytes + M * N * out_bytes
+    ncopy = max(1, -(-ROTATE_BYTES // per_copy)) if rotate else 1
+    da0, db0 = dev_u16(torch, a.data), dev_u16(torch, b)
+    copies = []
+    for _ in range(ncopy):
+        dc = torch.empty((M, N), dtype=torch.float32 if out_dtype == "f32" else torch.int16, device="cuda")
+        copies.append((da0.clone(), db0.clone(), dc))
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def launch(i):
+        da, db, dc = copies[i % ncopy]
+        plan.run(da, db, dc, stream=stream)
+
+    t = Timer(torch, steps).run(launch, steps, warmup)
+    info = plan.info()
+    plan.close()
+    del copies
+    flops = W.spmm_flops(a.nblocks, a.R, a.C, N)
+    nbytes = W.spmm_bytes(a, N, out_bytes)
+    return t, flops, nbytes, info, ncopy
+
+
+def bench_sddmm(torch, capi, W, mask, x, y, y_layout, out_dtype, steps, warmup):
+    K = x.shape[1]
+    plan = capi.SddmmPlan(capi.Bsr(mask.H, mask.W, mask.R, mask.C, mask.indptr, mask.indices), K,
+                          y_layout, out_dtype)
+    nv = mask.nblocks * mask.R * mask.C
+    out_bytes = 4 if out_dtype == "f32" else 2
+    per_copy = mask.data.nbytes + x.nbytes + y.nbytes + nv * out_bytes
+    ncopy = max(1, -(-ROTATE_BYTES // per_copy))
+    dm0, dx0, dy0 = dev_u16(torch, mask.data), dev_u16(torch, x), dev_u16(torch, y)
+    copies = []
+    for _ in range(ncopy):
+        do = torch.empty(nv, dtype=torch.float32 if out_dtype == "f32" else torch.int16, device="cuda")
+        copies.append((dm0.clone(), dx0.clone(), dy0.clone(), do))
+    stream = torch.cuda.current_stream().cuda_stream
+    ldy = mask.W if y_layout == capi.ROW_MAJOR else K
+
+    def launch(i):
+        dm, dx, dy, do = copies[i % ncopy]
+        plan.run(dm, dx, dy, do, ldy=ldy, stream=stream)
+
+    t = Timer(torch, steps).run(launch, steps, warmup)
+    plan.close()
+    del copies
+    flops = W.sddmm_flops(mask.nblocks, mask.R, mask.C, K)
+    nbytes = W.sddmm_bytes(mask, K, out_bytes)
+    return t, flops, nbytes
+
+
+def summarize(t, flops, nbytes, steps):
+    k_s = t["kernel_ms_mean"] * 1e-3
+    return {
+        "kernel_us": round(t["kernel_ms_mean"] * 1e3, 3),
+        "kernel_us_median": round(t["kernel_ms_median"] * 1e3, 3),
+        "tflops": round(flops / k_s / 1e12, 3),
+        "frac_mfma_peak": round(flops / k_s / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "gbs": round(nbytes / k_s / 1e9, 1),
+        "frac_hbm_peak": round(nbytes / k_s / 1e9 / PEAK_HBM_GBS, 4),
+        "wall_tflops": round(flops * steps / t["wall_s"] / 1e12, 3),
+        "flops": flops,
+        "bytes": nbytes,
+    }
+
+
+KERNEL_NAMES = {256: "spmm_kernel<4,2,false>", 128: "spmm_kernel<4,1,false>",
+                64: "spmm_kernel<2,1,false>", 32: "spmm_kernel<1,1,false>"}
+
+
+def roofline(flops, nbytes, k_s, row):
+    """The bound is the lower roof for the kernel's algorithmic intensity:
+    MFMA when FLOP/byte >= peak FLOP/s / peak bytes/s (312.5), else HBM."""
+    ai = flops / nbytes
+    ridge = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+    tflops = flops / k_s / 1e12
+    gbs = nbytes / k_s / 1e9
+    r = {"kernel": KERNEL_NAMES.get(row["tile_n"], "spmm_kernel"), "kernel_us": row["kernel_us"],
+         "algorithmic_flop_per_launch": flops, "algorithmic_bytes_per_launch": nbytes,
+         "intensity_flop_per_byte": round(ai, 1), "traffic": None,
+         "mfma_tflops": round(tflops, 3), "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+         "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)}
+    if ai >= ridge:
+        r.update({"bound": "mfma", "achieved": round(tflops, 3), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                  "frac": round(tflops / PEAK_BF16_TFLOPS, 4)})
+    else:
+        r.update({"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                  "frac": round(gbs / PEAK_HBM_GBS, 4)})
+    return r
+
+
+def cpu_baseline(W, orc):
+    """The oracle on this host: all cores on the whole 25% workload (median of
+    3 after one warm-up), one core on a 32-block-row sample."""
+    w = W.workload_spmm_sweep(0.25)
+    a, b = w["a"], w["b"]
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    cores = max(1, min(cores, int(os.environ.get("OMP_NUM_THREADS", cores))))
+
+    def timed(fn, reps=3):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts))
+
+    flops = W.spmm_flops(a.nblocks, 32, 32, 512)
+    t_all = timed(lambda: orc.spmm(a.indptr, a.indices, a.data, a.H, a.W, 32, 32, b, threads=cores))
+    rows = 32
+    nb = int(a.indptr[rows])
+    ip = np.ascontiguousarray(a.indptr[:rows + 1])
+    t_one = timed(lambda: orc.spmm(ip, a.indices[:nb], a.data[:nb * 1024], rows * 32, a.W, 32, 32, b,
+                                   threads=1), reps=1)
+    flops_one = W.spmm_flops(nb, 32, 32, 512)
+    return {
+        "value": round(flops / t_all / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"whole 25% workload ({a.nblocks} blocks, N=512), fp32 out, OpenMP over block rows; "
+                  f"median of 3 runs after 1 warm-up: {t_all:.3f} s",
+        "single_core": {"value": round(flops_one / t_one / 1e12, 6), "cores": 1,
+                        "sample": f"block rows 0..{rows - 1} ({nb} blocks), N=512: {t_one:.3f} s"},
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1 "
+                                   "(the multi-GPU sharding is a design note, not built)"}))
+        sys.exit(2)
+    import torch
+    import __graft_entry__ as entry
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(1)
+    pkg = entry.load_package()
+    capi, W = pkg.capi, pkg.workloads
+    capi.load()
+    only = set(filter(None, args.only.split(",")))
+    steps, warmup = args.steps, args.warmup
+    if args.copy_calibration:
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")  # 256 MiB
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    out = {}
+    sweep = []
+    head = None
+    if not only or "sweep" in only or "head" in only:
+        head_only = "head" in only and "sweep" not in only
+        for d in W.SPMM_SWEEP_DENSITIES:
+            if head_only and d != 0.25:
+                continue
+            w = W.workload_spmm_sweep(d)
+            for od in ("f32", "bf16"):
+                if head_only and od != "f32":
+                    continue
+                t, fl, nbytes, info, ncopy = bench_spmm(torch, capi, W, w["a"], w["b"], od, steps, warmup)
+                row = {"density": d, "out": od, "nnzb": w["a"].nblocks, **summarize(t, fl, nbytes, steps),
+                       "tile_n": info["tile_n"], "grid": info["grid"], "copies": ncopy}
+                sweep.append(row)
+                if d == 0.25 and od == "f32":
+                    head = (t, fl, nbytes, row)
+            if head_only:
+                continue
+            # warm (cache-resident) figure for the same launch, for reference
+            t, fl, nbytes, info, _ = bench_spmm(torch, capi, W, w["a"], w["b"], "f32", steps, warmup,
+                                                rotate=False)
+            sweep.append({"density": d, "out": "f32", "warm_cache": True, **summarize(t, fl, nbytes, steps)})
+        out["sweep"] = sweep
+    if not only or "sddmm" in only:
+        s = W.workload_sddmm()
+        t, fl, nb = bench_sddmm(torch, capi, W, s["mask"], s["x"], s["y"], capi.ROW_MAJOR, "f32", steps, warmup)
+        out["sddmm"] = {"workload": "SDDMM mask 4096x4096 32x32 blocks d=10%, X 4096x256, Y 256x4096, fp32 out",
+                        "nnzb": s["mask"].nblocks, **summarize(t, fl, nb, steps)}
+    if not only or "skewed" in only:
+        w = W.workload_spmm_skewed()
+        t, fl, nb, info, _ = bench_spmm(torch, capi, W, w["a"], w["b"], "f32", steps, warmup)
+        out["skewed"] = {"workload": "SpMM A 16384x16384 Zipf(1.2) rows, 2% mean density, B 16384x1024, fp32 out",
+                         "nnzb": w["a"].nblocks, "split_rows": info["n_split_rows"],
+                         **summarize(t, fl, nb, steps)}
+    if not only or "attention" in only:
+        w = W.workload_attention()
+        m = w["mask"]
+        t1, f1, b1 = bench_sddmm(torch, capi, W, m, w["q"], w["k"], capi.COL_MAJOR, "bf16", steps, warmup)
+        a = W.BsrArrays(m.H, m.W, 32, 32, m.indptr, m.indices, m.data)
+        t2, f2, b2, _, _ = bench_spmm(torch, capi, W, a, w["v"], "f32", steps, warmup)
+        out["attention"] = {"workload": "seq 8192, d 128, 8 causal block bands + 1% global; S=mask(.)QK^T "
+                                        "(bf16) then O=S*V (fp32)",
+                            "nnzb": m.nblocks, "sddmm": summarize(t1, f1, b1, steps),
+                            "spmm": summarize(t2, f2, b2, steps),
+                            "pair_tflops": round((f1 + f2) / ((t1["kernel_ms_mean"] + t2["kernel_ms_mean"]) * 1e-3)
+                                                 / 1e12, 3)}
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(W, entry._load_oracle())
+
+    if head is None:
+        print(json.dumps(out))
+        return
+    t, fl, nbytes, row = head
+    k_s = t["kernel_ms_mean"] * 1e-3
+    result = {
+        "metric": "effective TFLOP/s on nonzero blocks (SpMM, SDDMM); % bf16 MFMA peak / % HBM BW",
+        "value": round(fl * steps / t["wall_s"] / 1e12, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(t["wall_s"] / steps * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded uniform-random block positions, U[-1,1] bf16 values)",
+        "config": {"workload": "BSR SpMM C=A*B: A 4096x4096, 32x32 blocks, 25% block density (4096 blocks), "
+                               "B 4096x512 bf16, fp32 accumulate, fp32 C",
+                   "M": 4096, "K": 4096, "N": 512, "block": [32, 32], "density": 0.25,
+                   "peaks": {"bf16_mfma_tflops": PEAK_BF16_TFLOPS, "hbm_gbs": PEAK_HBM_GBS,
+                             "source": "AMD Instinct MI355X published dense figures"}},
+        "roofline": roofline(fl, nbytes, k_s, row),
+        "cpu_baseline": cpu,
+    }
+    result.update(out)
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

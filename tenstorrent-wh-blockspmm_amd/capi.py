@@ -56,12 +56,12 @@ class PlanInfo(ctypes.Structure):
         ("n_slots", c_int32),
         ("grid", c_int32),
         ("max_item_entries", c_int32),
-        ("reserved", c_int32),
+        ("stages", c_int32),
         ("workspace_bytes", c_int64),
     ]
 
     def as_dict(self) -> dict:
-        return {name: getattr(self, name) for name, _ in self._fields_ if name != "reserved"}
+        return {name: getattr(self, name) for name, _ in self._fields_}
 
 
 _DESC_P = POINTER(BsrDesc)

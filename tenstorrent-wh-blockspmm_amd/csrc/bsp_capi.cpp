@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -18,12 +19,11 @@ struct bsp_plan {
     int layout = BSP_ROW_MAJOR;
     int64_t M = 0, K = 0, N = 0, R = 0, C = 0, nblocks = 0;
     bsp_plan_info info{};
-    void* d_items = nullptr;
-    int32_t* d_ent_row = nullptr;
-    int64_t* d_ent_off = nullptr;
-    int32_t* d_wgmap = nullptr;
+    void* d_wgs = nullptr;  // per-workgroup records (SpmmWg / SddmmItem)
+    int32_t* d_ent_row = nullptr;   // SDDMM: first column of Y per entry
+    int64_t* d_ent_off = nullptr;   // SDDMM: output offset per entry; SpMM: packed entries
+    bsp::SpmmSplit* d_splits = nullptr;
     float* d_ws = nullptr;
-    int32_t* d_cnt = nullptr;
 };
 
 namespace {
@@ -63,18 +63,16 @@ hipError_t upload(T** dst, const std::vector<T>& src) {
 }
 
 void free_plan_buffers(bsp_plan* p) {
-    if (p->d_items) (void)hipFree(p->d_items);
+    if (p->d_wgs) (void)hipFree(p->d_wgs);
     if (p->d_ent_row) (void)hipFree(p->d_ent_row);
     if (p->d_ent_off) (void)hipFree(p->d_ent_off);
-    if (p->d_wgmap) (void)hipFree(p->d_wgmap);
+    if (p->d_splits) (void)hipFree(p->d_splits);
     if (p->d_ws) (void)hipFree(p->d_ws);
-    if (p->d_cnt) (void)hipFree(p->d_cnt);
-    p->d_items = nullptr;
+    p->d_wgs = nullptr;
     p->d_ent_row = nullptr;
     p->d_ent_off = nullptr;
-    p->d_wgmap = nullptr;
+    p->d_splits = nullptr;
     p->d_ws = nullptr;
-    p->d_cnt = nullptr;
 }
 
 int device_cus(int device, int* cus) {
@@ -107,9 +105,13 @@ void fill_info_spmm(const bsp::SpmmSchedule& s, bsp_plan_info* info) {
     info->n_slots = s.n_slots;
     info->grid = (int32_t)s.wgmap.size();
     info->max_item_entries = s.max_item_entries;
+    info->stages = bsp::spmm_default_stages(s.tile_n);
+    if (const char* v = std::getenv("BSP_SPMM_STAGES")) {
+        const int st = std::atoi(v);
+        if (bsp::spmm_stages_supported(s.tile_n, st)) info->stages = st;
+    }
     info->workspace_bytes =
-        (int64_t)s.n_slots * s.n_tiles * bsp::spmm_partial_floats(s.tile_n) * (int64_t)sizeof(float) +
-        (int64_t)s.n_slots * s.n_tiles * (int64_t)sizeof(int32_t);
+        (int64_t)s.n_slots * s.n_tiles * bsp::spmm_partial_floats(s.tile_n) * (int64_t)sizeof(float);
 }
 
 void fill_info_sddmm(const bsp::SddmmSchedule& s, bsp_plan_info* info) {
@@ -224,15 +226,12 @@ int bsp_spmm_plan_create(bsp_plan** out, const bsp_bsr_desc* a, int64_t N, int b
     p->C = a->C;
     p->nblocks = a->nblocks;
     fill_info_spmm(s, &p->info);
-    hipError_t e = upload((bsp::SpmmItem**)&p->d_items, s.items);
-    if (e == hipSuccess) e = upload(&p->d_ent_row, s.ent_row);
-    if (e == hipSuccess) e = upload(&p->d_ent_off, s.ent_off);
-    if (e == hipSuccess) e = upload(&p->d_wgmap, s.wgmap);
+    hipError_t e = upload((bsp::SpmmWg**)&p->d_wgs, bsp::spmm_wg_records(s));
+    if (e == hipSuccess) e = upload(&p->d_ent_off, bsp::spmm_packed_entries(s));
+    if (e == hipSuccess) e = upload(&p->d_splits, bsp::spmm_splits(s));
     if (e == hipSuccess && s.n_slots > 0) {
         const size_t nf = (size_t)s.n_slots * s.n_tiles * bsp::spmm_partial_floats(s.tile_n);
         e = hipMalloc((void**)&p->d_ws, nf * sizeof(float));
-        if (e == hipSuccess) e = hipMalloc((void**)&p->d_cnt, (size_t)s.n_slots * s.n_tiles * 4);
-        if (e == hipSuccess) e = hipMemset(p->d_cnt, 0, (size_t)s.n_slots * s.n_tiles * 4);
     }
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
@@ -261,18 +260,17 @@ int bsp_spmm(const bsp_plan* p, const uint16_t* a_vals, const uint16_t* b, int64
     args.a = a_vals;
     args.b = b;
     args.c = c;
-    args.items = (const bsp::SpmmItem*)p->d_items;
-    args.ent_row = p->d_ent_row;
-    args.ent_off = p->d_ent_off;
-    args.wgmap = p->d_wgmap;
+    args.wgs = (const bsp::SpmmWg*)p->d_wgs;
+    args.ents = p->d_ent_off;
+    args.splits = p->d_splits;
     args.ws = p->d_ws;
-    args.cnt = p->d_cnt;
     args.ldb = ldb;
     args.ldc = ldc;
     args.lda = (int32_t)p->C;
     args.n_tiles = p->info.n_tiles;
-    hipError_t e = bsp::launch_spmm(args, p->info.tile_n, p->out_dtype == BSP_DTYPE_BF16,
-                                    p->info.grid, (hipStream_t)stream);
+    args.N = (int32_t)p->N;
+    hipError_t e = bsp::launch_spmm(args, p->info.tile_n, p->info.stages, p->out_dtype == BSP_DTYPE_BF16,
+                                    p->info.grid, p->info.n_split_rows, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "SpMM launch");
     return BSP_OK;
 }
@@ -311,10 +309,9 @@ int bsp_sddmm_plan_create(bsp_plan** out, const bsp_bsr_desc* mask, int64_t K, i
     p->C = mask->C;
     p->nblocks = mask->nblocks;
     fill_info_sddmm(s, &p->info);
-    hipError_t e = upload((bsp::SddmmItem**)&p->d_items, s.items);
+    hipError_t e = upload((bsp::SddmmItem**)&p->d_wgs, bsp::sddmm_wg_records(s));
     if (e == hipSuccess) e = upload(&p->d_ent_row, s.ent_col);
     if (e == hipSuccess) e = upload(&p->d_ent_off, s.ent_off);
-    if (e == hipSuccess) e = upload(&p->d_wgmap, s.wgmap);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         free_plan_buffers(p);
@@ -347,10 +344,9 @@ int bsp_sddmm(const bsp_plan* p, const uint16_t* mask_vals, const uint16_t* x, i
     args.x = x;
     args.y = y;
     args.out = out_vals;
-    args.items = (const bsp::SddmmItem*)p->d_items;
+    args.wgs = (const bsp::SddmmItem*)p->d_wgs;
     args.ent_col = p->d_ent_row;
     args.ent_off = p->d_ent_off;
-    args.wgmap = p->d_wgmap;
     args.ldx = ldx;
     args.ldy = ldy;
     args.ldo = (int32_t)p->C;

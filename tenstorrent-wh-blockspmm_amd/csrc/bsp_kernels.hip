@@ -42,6 +42,25 @@ __device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
+}
+
+// Reads plan data (written before the launch, never by a kernel) through the
+// constant address space so that it is fetched with scalar loads.
+template <typename T>
+__device__ __forceinline__ T load_const(const T* ptr) {
+    static_assert(sizeof(T) % 4 == 0, "plan records are whole dwords");
+    const __attribute__((address_space(4))) uint32_t* src =
+        (const __attribute__((address_space(4))) uint32_t*)(uintptr_t)ptr;
+    uint32_t w[sizeof(T) / 4];
+#pragma unroll
+    for (unsigned i = 0; i < sizeof(T) / 4; ++i) w[i] = src[i];
+    T out;
+    __builtin_memcpy(&out, w, sizeof(T));
+    return out;
+}
+
 // Packs rows k (r0) and k+1 (r1), 8 columns each, into 8 k-pair dwords in
 // column order.
 __device__ __forceinline__ void pack_pairs(const u32x4& r0, const u32x4& r1, u32x4& lo,
@@ -57,148 +76,235 @@ __device__ __forceinline__ void pack_pairs(const u32x4& r0, const u32x4& r1, u32
 }
 
 // ---------------------------------------------------------------------------
-// SpMM.  Workgroup = one work item (a run of one 32-row stripe's sub-block
-// products) x one tile of TN output columns; NW waves, each owning NTW 32-col
-// MFMA tiles.  Per entry: the 32x32 A sub-block and the 32 x TN slice of B are
-// loaded (16-byte, coalesced) into registers one entry ahead, then written to
-// a double-buffered LDS stage; one barrier per entry.
-template <int NW, int NTW, bool OUT_BF16>
-__global__ __launch_bounds__(NW * 64) void spmm_kernel(SpmmArgs p) {
-    constexpr int NT = NW * 64;
-    constexpr int TN = NW * NTW * 32;
-    constexpr int A_LD = 40;      // bf16 per LDS row of A (32 + 8 pad)
-    constexpr int B_LD = TN + 8;  // dwords per LDS k-pair row of B
-    constexpr int ACH = (128 + NT - 1) / NT;
-    __shared__ __attribute__((aligned(16))) uint16_t sA[2][32 * A_LD];
-    __shared__ __attribute__((aligned(16))) uint32_t sB[2][16 * B_LD];
-    __shared__ int s_last;
+// SpMM.  Every wave works alone on one 32 x 64 output tile (two 32x32 MFMA
+// tiles) of one work item (a run of one 32-row stripe's sub-block products);
+// a workgroup packs NW waves that cover NW consecutive 64-column tiles of the
+// same item (so they read the same A blocks, through the same L1).  There is
+// no barrier: each wave streams its entries through its own S-stage ring in
+// LDS, filled by direct global->LDS loads (global_load_lds_dwordx4, no
+// register staging), S-1 entries ahead of the one it computes.
+// A stage holds
+//   - the entry's 32x32 A sub-block (2 KB) as 128 16-byte chunks, chunk
+//     64*s + 32*q + r = A[r][16*s + 8*q .. +7], so the A operand of k-step s
+//     is one conflict-free ds_read_b128 at chunk 64*s + lane;
+//   - the 32 x 64 slice of row-major B (4 KB), row k at 128*k bytes, its
+//     16-byte chunk c stored at slot c ^ 4*((k >> 1) & 1) so that the rows a
+//     transpose read touches fall on distinct LDS banks.
+// The B operand (8 consecutive k at one column) is read with two
+// ds_read_b64_tr_b16: in each 16-lane group, source lane 4*j + m addresses
+// row k0+j, columns n+4m..n+4m+3, and output lane i receives rows k0..k0+3 of
+// column n+i.
+namespace spmm_detail {
 
-    const int wg = p.wgmap[blockIdx.x];
-    if (wg < 0) return;
-    const int item_id = wg / p.n_tiles;
-    const int tile = wg - item_id * p.n_tiles;
-    const SpmmItem it = p.items[item_id];
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int l32 = lane & 31, q = lane >> 5;
-    const int n0 = tile * TN;
+constexpr int kA_BYTES = 2048;
+constexpr int kB_BYTES = 4096;  // 32 rows x 64 columns of bf16
+constexpr int kSTAGE = kA_BYTES + kB_BYTES;
+constexpr int kLOADS = 6;       // 16-byte DMA instructions per stage: 2 for A, 4 for B
 
-    f32x16 acc[NTW];
-#pragma unroll
-    for (int i = 0; i < NTW; ++i)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
+// Direct global->LDS load of 16 bytes per lane: lane L's bytes land at
+// lds_wave_base + 16*L (lds_wave_base is wave-uniform).  Issued as inline asm
+// so that the compiler does not track it: its own bookkeeping would otherwise
+// wait for every outstanding load before each LDS read, which serialises the
+// ring.  Completion is awaited explicitly with wait_vmcnt.  Nothing else in
+// these kernels uses M0.
+__device__ __forceinline__ void gl_lds16(const void* g, uint32_t lds_wave_base) {
+    const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_wave_base);
+    __asm__ volatile(
+        "s_mov_b32 m0, %1\n\t"
+        "global_load_lds_dwordx4 %0, off"
+        :
+        : "v"(g), "s"(lds)
+        : "memory");
+}
 
-    u32x4 ra[ACH];
-    u32x4 rb0[NTW], rb1[NTW];
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt[3:0] bits 3:0, expcnt bits 6:4, lgkmcnt bits 11:8, vmcnt[5:4] bits 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt out of range");
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | (((N >> 4) & 0x3) << 14));
+    __asm__ volatile("" ::: "memory");
+}
 
-    auto gload = [&](int e) {
-        const int32_t brow = p.ent_row[e];
-        const uint16_t* ablk = p.a + p.ent_off[e];
-#pragma unroll
-        for (int i = 0; i < ACH; ++i) {
-            const int c = tid + i * NT;
-            if (c < 128)
-                ra[i] = *(const u32x4*)(ablk + (int64_t)(c >> 2) * p.lda + (c & 3) * 8);
+// Waits until at most PER*n vector loads of this wave are outstanding, n <= NMAX.
+template <int PER, int NMAX>
+__device__ __forceinline__ void wait_stages(int n) {
+    if constexpr (NMAX >= 0) {
+        if (n >= NMAX) {
+            wait_vmcnt<PER * NMAX>();
+            return;
         }
-#pragma unroll
-        for (int i = 0; i < NTW; ++i) {
-            const int qq = tid + i * NT;
-            const int pr = qq / (TN / 8), c8 = (qq % (TN / 8)) * 8;
-            const uint16_t* src = p.b + (int64_t)(brow + 2 * pr) * p.ldb + n0 + c8;
-            rb0[i] = *(const u32x4*)src;
-            rb1[i] = *(const u32x4*)(src + p.ldb);
-        }
-    };
-    auto lstore = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < ACH; ++i) {
-            const int c = tid + i * NT;
-            if (c < 128) *(u32x4*)&sA[buf][(c >> 2) * A_LD + (c & 3) * 8] = ra[i];
-        }
-#pragma unroll
-        for (int i = 0; i < NTW; ++i) {
-            const int qq = tid + i * NT;
-            const int pr = qq / (TN / 8), c8 = (qq % (TN / 8)) * 8;
-            u32x4 lo, hi;
-            pack_pairs(rb0[i], rb1[i], lo, hi);
-            *(u32x4*)&sB[buf][pr * B_LD + c8] = lo;
-            *(u32x4*)&sB[buf][pr * B_LD + c8 + 4] = hi;
-        }
-    };
-    auto compute = [&](int buf) {
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const u32x4 av = *(const u32x4*)&sA[buf][l32 * A_LD + 16 * s + 8 * q];
-#pragma unroll
-            for (int nt = 0; nt < NTW; ++nt) {
-                const uint32_t* bp = &sB[buf][(8 * s + 4 * q) * B_LD + wave * (NTW * 32) + nt * 32 + l32];
-                u32x4 bv;
-                bv.x = bp[0];
-                bv.y = bp[B_LD];
-                bv.z = bp[2 * B_LD];
-                bv.w = bp[3 * B_LD];
-                acc[nt] = mfma32(av, bv, acc[nt]);
-            }
-        }
-    };
-
-    const int e_begin = it.e_begin, e_end = it.e_end;
-    if (e_begin < e_end) gload(e_begin);
-    for (int e = e_begin; e < e_end; ++e) {
-        const int buf = (e - e_begin) & 1;
-        lstore(buf);
-        if (e + 1 < e_end) gload(e + 1);
-        __syncthreads();
-        compute(buf);
+        wait_stages<PER, NMAX - 1>(n);
     }
+}
 
-    if (it.slot >= 0) {
-        // Piece of a split row: publish the partial, and let the last piece to
-        // arrive add all partials in piece order (deterministic) and store.
-        constexpr int PER = NTW * 16 * NT;  // floats per (slot, tile)
-        float* mine = p.ws + ((int64_t)it.slot * p.n_tiles + tile) * PER;
-#pragma unroll
-        for (int nt = 0; nt < NTW; ++nt)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) mine[(nt * 16 + v) * NT + tid] = acc[nt][v];
-        __threadfence();
-        __syncthreads();
-        int32_t* counter = p.cnt + (int64_t)it.base * p.n_tiles + tile;
-        if (tid == 0) {
-            const int prev = atomicAdd(counter, 1);
-            s_last = (prev == it.npieces - 1);
-        }
-        __syncthreads();
-        if (!s_last) return;
-        __threadfence();
-#pragma unroll
-        for (int nt = 0; nt < NTW; ++nt)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[nt][v] = 0.0f;
-        for (int pc = 0; pc < it.npieces; ++pc) {
-            const float* src = p.ws + ((int64_t)(it.base + pc) * p.n_tiles + tile) * PER;
-#pragma unroll
-            for (int nt = 0; nt < NTW; ++nt)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) acc[nt][v] += src[(nt * 16 + v) * NT + tid];
-        }
-        if (tid == 0) *counter = 0;  // ready for the next launch
-    }
+__device__ __forceinline__ u32x4 ld_tr_b16(const uint8_t* lds) {
+    typedef short v4i16 __attribute__((ext_vector_type(4)));
+    v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4i16*)(__attribute__((address_space(3))) uint8_t*)lds);
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    u32x2 w = __builtin_bit_cast(u32x2, v);
+    return u32x4{w.x, w.y, 0u, 0u};
+}
 
-    const int64_t r0 = (int64_t)it.row * 32;
+}  // namespace spmm_detail
+
+// Stores the accumulators of one wave's 32 x 64 tile (columns past N skipped).
+template <bool OUT_BF16>
+__device__ __forceinline__ void spmm_store_wave(const SpmmArgs& p, const f32x16 (&acc)[2], int64_t row0,
+                                                int col0, int l32, int q) {
 #pragma unroll
-    for (int nt = 0; nt < NTW; ++nt) {
-        const int64_t col = n0 + wave * (NTW * 32) + nt * 32 + l32;
+    for (int nt = 0; nt < 2; ++nt) {
+        const int64_t col = col0 + nt * 32 + l32;
+        if (col >= p.N) continue;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-            const int64_t row = r0 + 8 * (v >> 2) + 4 * q + (v & 3);
+            const int64_t row = row0 + 8 * (v >> 2) + 4 * q + (v & 3);
             if (OUT_BF16)
                 ((uint16_t*)p.c)[row * p.ldc + col] = f32_to_bf16_rne(acc[nt][v]);
             else
                 ((float*)p.c)[row * p.ldc + col] = acc[nt][v];
         }
     }
+}
+
+template <int NW, int S, bool OUT_BF16>
+__global__ __launch_bounds__(NW * 64) void spmm_kernel(SpmmArgs p) {
+    using namespace spmm_detail;
+    static_assert(kLOADS * (S - 2) < 64, "vmcnt budget");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NW * S * kSTAGE];
+
+    const SpmmWg it = load_const(p.wgs + blockIdx.x);
+    if (it.row < 0) return;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l32 = lane & 31, q = lane >> 5;
+    const int col0 = (it.tile * NW + wave) * 64;  // this wave's first output column
+    if (col0 >= p.N) return;                       // a partial last group
+    const uint32_t ring = lds_address(smem) + wave * S * kSTAGE;
+    const uint8_t* ring_ptr = smem + wave * S * kSTAGE;
+
+    // Per-lane global offsets of this lane's chunks in an entry.
+    // A DMA d (d = 0, 1): chunk 64*d + lane = A[lane % 32][16*d + 8*(lane / 32)].
+    const int a_goff = (lane & 31) * p.lda + 8 * (lane >> 5);
+    // B DMA j (j = 0..3): rows 8*j + lane/8, stored slot lane%8 holds chunk slot ^ f(row).
+    int64_t b_goff[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r = 8 * j + (lane >> 3);
+        const int c = (lane & 7) ^ (4 * ((r >> 1) & 1));
+        // Columns past N (a partial last tile) read a valid chunk; they are not stored.
+        b_goff[j] = (int64_t)r * p.ldb + min(col0 + 8 * c, p.N - 8);
+    }
+
+    auto issue = [&](int64_t ent, int stage) {
+        const int32_t brow = (int32_t)(ent & 0xffffffff);
+        const uint16_t* ablk = p.a + (ent >> 32) * 32;
+        const uint16_t* bpan = p.b + (int64_t)brow * p.ldb;
+        const uint32_t st = ring + (uint32_t)stage * kSTAGE;
+        gl_lds16(ablk + a_goff, st);
+        gl_lds16(ablk + a_goff + 16, st + 1024);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) gl_lds16(bpan + b_goff[j], st + kA_BYTES + j * 1024);
+    };
+
+    // Per-lane LDS offsets of the operand reads (stage-relative).
+    const int a_rd = lane * 16;  // + s * 1024
+    int b_rd[2][2][2];           // [k-step][half][tile]
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const int g = lane >> 4;
+                const int r = 16 * s2 + 8 * (g >> 1) + 4 * h + ((lane & 15) >> 2);
+                const int col = nt * 32 + 16 * (g & 1) + 4 * (lane & 3);
+                const int c = col >> 3;
+                b_rd[s2][h][nt] = kA_BYTES + r * 128 + 16 * (c ^ (4 * ((r >> 1) & 1))) + 2 * (col & 7);
+            }
+
+    f32x16 acc[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
+
+    auto compute = [&](int stage) {
+        const uint8_t* st = ring_ptr + stage * kSTAGE;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            const u32x4 av = *(const u32x4*)(st + s2 * 1024 + a_rd);
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const u32x4 lo = ld_tr_b16(st + b_rd[s2][0][nt]);
+                const u32x4 hi = ld_tr_b16(st + b_rd[s2][1][nt]);
+                acc[nt] = mfma32(av, u32x4{lo.x, lo.y, hi.x, hi.y}, acc[nt]);
+            }
+        }
+    };
+
+    const int e0 = it.e_begin, n = it.e_end - it.e_begin;
+    const int64_t* ents = p.ents + e0;
+#pragma unroll
+    for (int i = 0; i < S - 1; ++i)
+        if (i < n) issue(load_const(ents + i), i);
+    // Main loop: stage k is complete once kLOADS*(S-2) loads (the stages
+    // issued after it) remain.  The slot refilled here was read by the
+    // previous iteration, whose operands the MFMAs have already consumed.
+    int k = 0, stage = 0;
+    int64_t next_ent = (S - 1 < n) ? load_const(ents + S - 1) : 0;
+    for (; k < n - (S - 1); ++k) {
+        wait_vmcnt<kLOADS * (S - 2)>();
+        issue(next_ent, stage == 0 ? S - 1 : stage - 1);
+        next_ent = (k + S < n) ? load_const(ents + k + S) : 0;
+        compute(stage);
+        stage = stage == S - 1 ? 0 : stage + 1;
+    }
+    // Tail: nothing left to issue; fewer stages are in flight.
+    for (; k < n; ++k) {
+        wait_stages<kLOADS, S - 2>(n - 1 - k);
+        compute(stage);
+        stage = stage == S - 1 ? 0 : stage + 1;
+    }
+
+    if (it.slot >= 0) {
+        // Piece of a split row: the partial goes to scratch; spmm_reduce_kernel
+        // adds the pieces in order after this launch.
+        float* mine = p.ws + ((int64_t)it.slot * p.n_tiles + it.tile) * (NW * 64 * 32) + wave * (64 * 32);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) mine[(nt * 16 + v) * 64 + lane] = acc[nt][v];
+        return;
+    }
+    spmm_store_wave<OUT_BF16>(p, acc, (int64_t)it.row * 32, col0, l32, q);
+}
+
+// Adds the partials of each split row in piece order (deterministic) and
+// stores the tile: one workgroup of NW waves per (split row, column group).
+template <int NW, bool OUT_BF16>
+__global__ __launch_bounds__(NW * 64) void spmm_reduce_kernel(SpmmArgs p) {
+    const int tile = blockIdx.x % p.n_tiles;
+    const SpmmSplit sp = load_const(p.splits + blockIdx.x / p.n_tiles);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int col0 = (tile * NW + wave) * 64;
+    if (col0 >= p.N) return;
+    f32x16 acc[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[nt][v] = 0.0f;
+    for (int pc = 0; pc < sp.npieces; ++pc) {
+        const float* src = p.ws + ((int64_t)(sp.base + pc) * p.n_tiles + tile) * (NW * 64 * 32) + wave * (64 * 32);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[nt][v] += src[(nt * 16 + v) * 64 + lane];
+    }
+    spmm_store_wave<OUT_BF16>(p, acc, (int64_t)sp.row * 32, col0, lane & 31, lane >> 5);
 }
 
 // ---------------------------------------------------------------------------
@@ -214,9 +320,7 @@ __global__ __launch_bounds__(256) void sddmm_kernel(SddmmArgs p) {
     constexpr int Y_LD = 40;  // dwords per LDS k-pair row (32 + 8 pad)
     __shared__ __attribute__((aligned(16))) uint32_t sY[4][16 * Y_LD];
 
-    const int wg = p.wgmap[blockIdx.x];
-    if (wg < 0) return;
-    const SddmmItem it = p.items[wg];
+    const SddmmItem it = p.wgs[blockIdx.x];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int l32 = lane & 31, q = lane >> 5;
     const uint16_t* xlane = p.x + (int64_t)(it.x_row0 + l32) * p.ldx + 8 * q;
@@ -281,27 +385,34 @@ __global__ __launch_bounds__(256) void sddmm_kernel(SddmmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-hipError_t launch_spmm(const SpmmArgs& a, int tile_n, bool out_bf16, int grid,
+template <int NW, int S>
+static void launch_spmm_t(const SpmmArgs& a, bool out_bf16, int grid, int n_split, hipStream_t stream) {
+    if (out_bf16)
+        hipLaunchKernelGGL((spmm_kernel<NW, S, true>), dim3(grid), dim3(NW * 64), 0, stream, a);
+    else
+        hipLaunchKernelGGL((spmm_kernel<NW, S, false>), dim3(grid), dim3(NW * 64), 0, stream, a);
+    if (n_split > 0) {
+        const int g = n_split * a.n_tiles;
+        if (out_bf16)
+            hipLaunchKernelGGL((spmm_reduce_kernel<NW, true>), dim3(g), dim3(NW * 64), 0, stream, a);
+        else
+            hipLaunchKernelGGL((spmm_reduce_kernel<NW, false>), dim3(g), dim3(NW * 64), 0, stream, a);
+    }
+}
+
+hipError_t launch_spmm(const SpmmArgs& a, int tile_n, int stages, bool out_bf16, int grid, int n_split,
                        hipStream_t stream) {
     if (grid <= 0) return hipSuccess;
-#define BSP_SPMM_CASE(TN, NW, NTW)                                                        \
-    case TN:                                                                              \
-        if (out_bf16)                                                                     \
-            hipLaunchKernelGGL((spmm_kernel<NW, NTW, true>), dim3(grid), dim3(NW * 64), 0, \
-                               stream, a);                                                \
-        else                                                                              \
-            hipLaunchKernelGGL((spmm_kernel<NW, NTW, false>), dim3(grid), dim3(NW * 64), 0, \
-                               stream, a);                                                \
-        break;
-    switch (tile_n) {
-        BSP_SPMM_CASE(256, 4, 2)
-        BSP_SPMM_CASE(128, 4, 1)
-        BSP_SPMM_CASE(64, 2, 1)
-        BSP_SPMM_CASE(32, 1, 1)
+    switch (tile_n * 100 + stages) {
+        case 25604: launch_spmm_t<4, 4>(a, out_bf16, grid, n_split, stream); break;
+        case 25606: launch_spmm_t<4, 6>(a, out_bf16, grid, n_split, stream); break;
+        case 12806: launch_spmm_t<2, 6>(a, out_bf16, grid, n_split, stream); break;
+        case 12808: launch_spmm_t<2, 8>(a, out_bf16, grid, n_split, stream); break;
+        case 6408: launch_spmm_t<1, 8>(a, out_bf16, grid, n_split, stream); break;
+        case 6412: launch_spmm_t<1, 12>(a, out_bf16, grid, n_split, stream); break;
         default:
             return hipErrorInvalidValue;
     }
-#undef BSP_SPMM_CASE
     return hipGetLastError();
 }
 

@@ -110,6 +110,77 @@ std::vector<int32_t> xcd_lpt_map(const std::vector<int64_t>& unit_cost, int widt
     return map;
 }
 
+std::vector<int32_t> xcd_tile_map(const std::vector<int64_t>& item_cost, int n_tiles, int col_groups) {
+    if (col_groups < 1 || kNumXcd % col_groups != 0 || n_tiles % col_groups != 0) col_groups = 1;
+    const int row_groups = kNumXcd / col_groups;
+    const int64_t nitems = (int64_t)item_cost.size();
+    std::vector<int32_t> order(nitems);
+    std::iota(order.begin(), order.end(), 0);
+    std::stable_sort(order.begin(), order.end(),
+                     [&](int32_t a, int32_t b) { return item_cost[a] > item_cost[b]; });
+    std::vector<std::vector<int32_t>> rows(row_groups);
+    using Load = std::pair<int64_t, int>;
+    std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
+    for (int g = 0; g < row_groups; ++g) heap.push({0, g});
+    for (int32_t u : order) {
+        Load l = heap.top();
+        heap.pop();
+        rows[l.second].push_back(u);
+        heap.push({l.first + item_cost[u], l.second});
+    }
+    const int tpg = n_tiles / col_groups;
+    std::vector<std::vector<int32_t>> bins(kNumXcd);
+    for (int rg = 0; rg < row_groups; ++rg)
+        for (int cg = 0; cg < col_groups; ++cg) {
+            auto& b = bins[rg * col_groups + cg];
+            for (int32_t u : rows[rg])
+                for (int t = cg * tpg; t < (cg + 1) * tpg; ++t) b.push_back(u * n_tiles + t);
+        }
+    size_t maxlen = 0;
+    for (auto& b : bins) maxlen = std::max(maxlen, b.size());
+    std::vector<int32_t> map(maxlen * kNumXcd, -1);
+    for (int x = 0; x < kNumXcd; ++x)
+        for (size_t j = 0; j < bins[x].size(); ++j) map[j * kNumXcd + x] = bins[x][j];
+    return map;
+}
+
+std::vector<SpmmWg> spmm_wg_records(const SpmmSchedule& s) {
+    std::vector<SpmmWg> out(s.wgmap.size());
+    for (size_t g = 0; g < s.wgmap.size(); ++g) {
+        const int32_t u = s.wgmap[g];
+        if (u < 0) {
+            out[g] = {-1, 0, 0, -1, -1, 0, 0, 0};
+            continue;
+        }
+        const SpmmItem& it = s.items[u / s.n_tiles];
+        out[g] = {it.row, it.e_begin, it.e_end, it.slot, it.base, it.npieces, u % s.n_tiles, 0};
+    }
+    return out;
+}
+
+std::vector<int64_t> spmm_packed_entries(const SpmmSchedule& s) {
+    std::vector<int64_t> out(s.ent_row.size());
+    for (size_t e = 0; e < out.size(); ++e)
+        out[e] = (int64_t)(uint32_t)s.ent_row[e] | ((s.ent_off[e] / kSub) << 32);
+    return out;
+}
+
+std::vector<SpmmSplit> spmm_splits(const SpmmSchedule& s) {
+    std::vector<SpmmSplit> out;
+    for (const SpmmItem& it : s.items)
+        if (it.slot >= 0 && it.slot == it.base) out.push_back({it.row, it.base, it.npieces, 0});
+    return out;
+}
+
+std::vector<SddmmItem> sddmm_wg_records(const SddmmSchedule& s) {
+    std::vector<SddmmItem> out(s.wgmap.size());
+    for (size_t g = 0; g < s.wgmap.size(); ++g) {
+        const int32_t u = s.wgmap[g];
+        out[g] = u < 0 ? SddmmItem{0, 0, 0, 0} : s.items[u];
+    }
+    return out;
+}
+
 int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSchedule& s,
                         std::string& msg) {
     int st = validate_bsr(a, msg);
@@ -118,7 +189,7 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
         msg = "N must be positive";
         return BSP_ERR_INVALID_ARGUMENT;
     }
-    if (a->R % kSub || a->C % kSub || N % kSub) {
+    if (a->R % kSub || a->C % kSub || N % kSub || N > INT32_MAX / 2) {
         msg = "R, C and N must be multiples of 32";
         return BSP_ERR_UNSUPPORTED;
     }
@@ -132,21 +203,13 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
         return BSP_ERR_UNSUPPORTED;
     }
 
-    // Output tile width: the widest of 256/128/64/32 dividing N that still
-    // leaves at least two workgroups per compute unit; else the narrowest.
+    // Workgroup width: 256 columns (four waves of 64), or 128 / 64 when N is
+    // narrow; the last group of a row may be partial.
     int64_t tn = env_int("BSP_SPMM_TILE_N", 0);
-    if (tn != 0 && (tn != 32 && tn != 64 && tn != 128 && tn != 256)) tn = 0;
-    if (tn != 0 && N % tn != 0) tn = 0;
-    if (tn == 0) {
-        const int64_t cands[] = {256, 128, 64, 32};
-        for (int64_t c : cands) {
-            if (N % c) continue;
-            tn = c;
-            if (nsr * (N / c) >= 2 * (int64_t)num_cus) break;
-        }
-    }
+    if (tn != 0 && tn != 64 && tn != 128 && tn != 256) tn = 0;
+    if (tn == 0) tn = N >= 256 ? 256 : (N >= 128 ? 128 : 64);
     s.tile_n = (int32_t)tn;
-    s.n_tiles = (int32_t)(N / tn);
+    s.n_tiles = (int32_t)((N + tn - 1) / tn);
 
     // Split limit: a piece holds at most L entries.  L is the larger of twice
     // the mean length of non-empty rows (uniform rows stay whole) and half of
@@ -205,7 +268,15 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
         msg = "too many work items";
         return BSP_ERR_UNSUPPORTED;
     }
-    s.wgmap = xcd_lpt_map(cost, s.n_tiles);
+    // Column groups of the XCD map: the fewest (1, 2, 4, 8) that bring one
+    // XCD's slice of B to at most 2 MiB, limited by the tile count.
+    int64_t cg = 1;
+    const int64_t b_bytes = a->W * N * 2;
+    while (cg < kNumXcd && b_bytes / cg > (2 << 20) && s.n_tiles % (cg * 2) == 0) cg *= 2;
+    cg = env_int("BSP_SPMM_XCD_COLS", cg);
+    if (cg < 1 || kNumXcd % cg != 0 || s.n_tiles % cg != 0) cg = 1;
+    s.xcd_col_groups = (int32_t)cg;
+    s.wgmap = xcd_tile_map(cost, s.n_tiles, (int)cg);
     return BSP_OK;
 }
 

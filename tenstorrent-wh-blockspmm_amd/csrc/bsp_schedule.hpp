@@ -28,6 +28,29 @@ struct SpmmItem {
 };
 static_assert(sizeof(SpmmItem) == 24, "SpmmItem layout is shared with the kernels");
 
+// What one SpMM workgroup reads first: its item and N tile (idle slots of the
+// XCD map have row == -1).
+struct SpmmWg {
+    int32_t row;
+    int32_t e_begin;
+    int32_t e_end;
+    int32_t slot;
+    int32_t base;
+    int32_t npieces;
+    int32_t tile;
+    int32_t pad;
+};
+static_assert(sizeof(SpmmWg) == 32, "SpmmWg layout is shared with the kernels");
+
+// One split row: its sub-row, first partial slot and number of pieces.
+struct SpmmSplit {
+    int32_t row;
+    int32_t base;
+    int32_t npieces;
+    int32_t pad;
+};
+static_assert(sizeof(SpmmSplit) == 16, "SpmmSplit layout is shared with the kernels");
+
 struct SpmmSchedule {
     int32_t tile_n = 0;
     int32_t n_tiles = 0;
@@ -35,11 +58,19 @@ struct SpmmSchedule {
     int32_t n_slots = 0;
     int32_t n_split_rows = 0;
     int32_t max_item_entries = 0;
+    int32_t xcd_col_groups = 1;  // column groups of the XCD map
     std::vector<SpmmItem> items;
     std::vector<int32_t> ent_row;  // first row of B for the entry
     std::vector<int64_t> ent_off;  // element offset of the 32x32 A sub-block
     std::vector<int32_t> wgmap;    // workgroup id -> item * n_tiles + tile, or -1
 };
+
+// Per-workgroup records in launch order (items expanded through wgmap).
+std::vector<SpmmWg> spmm_wg_records(const SpmmSchedule& s);
+// Entries packed for the kernel: first row of B | (A offset / 32) << 32.
+std::vector<int64_t> spmm_packed_entries(const SpmmSchedule& s);
+// The split rows in slot order.
+std::vector<SpmmSplit> spmm_splits(const SpmmSchedule& s);
 
 // One unit of SDDMM work: a run of output sub-blocks that share 32 rows of X.
 struct SddmmItem {
@@ -59,6 +90,9 @@ struct SddmmSchedule {
     std::vector<int32_t> wgmap;    // workgroup id -> item, or -1
 };
 
+// Per-workgroup items in launch order; idle slots get an empty range.
+std::vector<SddmmItem> sddmm_wg_records(const SddmmSchedule& s);
+
 // Structural checks of sparse_common/bsr_matrix.hpp:246-252 / :610-616 plus
 // the CSR invariants the golden relies on implicitly.  On failure returns a
 // bsp_status and fills `msg`.
@@ -68,6 +102,15 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
                         std::string& msg);
 int build_sddmm_schedule(const bsp_bsr_desc* mask, int64_t K, int num_cus, SddmmSchedule& out,
                          std::string& msg);
+
+// SpMM workgroup map over the XCDs in a 2-D split: the N tiles are cut into
+// `col_groups` contiguous groups and the items into kNumXcd / col_groups row
+// groups balanced by cost (longest first onto the least-loaded group); XCD
+// x = row_group * col_groups + col_group runs that row group's items on that
+// column group's tiles, longest first.  Each XCD then reads only its column
+// slice of B, which stays in its L2.  Returns item * n_tiles + tile per
+// workgroup id (workgroup g runs on XCD g % kNumXcd), -1 for idle slots.
+std::vector<int32_t> xcd_tile_map(const std::vector<int64_t>& item_cost, int n_tiles, int col_groups);
 
 // Spreads weighted units over the XCDs (longest first onto the least-loaded
 // XCD), then lays them out so that workgroup id g runs on XCD g % kNumXcd in

@@ -1,0 +1,252 @@
+"""C ABI on the CPU: the library loads and exports every declared entry point,
+malformed input is rejected with the documented status before any device
+work, and the host-side schedule covers every sub-block product exactly once
+with balanced pieces.  No compute call needs a GPU here."""
+import ctypes
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from helpers import REPO, W, capi
+
+HEADER = REPO / "include" / "bsparse.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(bsp_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported():
+    names = _declared_functions()
+    assert len(names) >= 14
+    lib = capi.load()
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(capi.SIGNATURES), "binding and header disagree"
+    nm = subprocess.run(["nm", "-D", "--defined-only", str(capi.LIB_PATH)], capture_output=True, text=True)
+    exported = set(re.findall(r"\bT (bsp_\w+)", nm.stdout))
+    assert set(names) <= exported
+
+
+def test_library_links_hip_and_has_gfx950_code():
+    out = subprocess.run(["ldd", str(capi.LIB_PATH)], capture_output=True, text=True).stdout
+    assert "libamdhip64" in out
+    blob = capi.LIB_PATH.read_bytes()
+    assert b"gfx950" in blob
+    assert b"oracle" not in blob.lower().replace(b"_oracle", b"")  # never linked against the oracle
+
+
+def test_abi_version_and_status_strings():
+    lib = capi.load()
+    assert lib.bsp_abi_version() == 1
+    for code, text in [(0, b"ok"), (2, b"malformed BSR structure"), (3, b"unsupported")]:
+        assert lib.bsp_status_string(code) == text
+
+
+def _bsr(indptr, indices, H=128, Wd=128, R=32, C=32):
+    return capi.Bsr(H, Wd, R, C, np.array(indptr, np.int32), np.array(indices, np.int32))
+
+
+GOOD = dict(indptr=[0, 1, 1, 3, 3], indices=[2, 0, 3])
+
+BAD = [
+    ("indptr0", dict(indptr=[1, 1, 1, 3, 3], indices=[2, 0, 3]), capi.BSP_ERR_BAD_STRUCTURE, "indptr[0]"),
+    ("decreasing", dict(indptr=[0, 2, 1, 3, 3], indices=[2, 0, 3]), capi.BSP_ERR_BAD_STRUCTURE, "non-decreasing"),
+    ("last", dict(indptr=[0, 1, 1, 2, 2], indices=[2, 0, 3]), capi.BSP_ERR_BAD_STRUCTURE, "nblocks"),
+    ("col_range", dict(indptr=[0, 1, 1, 3, 3], indices=[2, 0, 4]), capi.BSP_ERR_BAD_STRUCTURE, "outside"),
+    ("col_negative", dict(indptr=[0, 1, 1, 3, 3], indices=[2, -1, 3]), capi.BSP_ERR_BAD_STRUCTURE, "outside"),
+]
+
+
+def test_validate_accepts_good_and_duplicate_columns():
+    assert capi.validate(_bsr(**GOOD)) == capi.BSP_OK
+    dup = W.fill_col_as_reference(64, 64, 32, 32, 4)
+    assert capi.validate(capi.Bsr(64, 64, 32, 32, dup.indptr, dup.indices)) == capi.BSP_OK
+    assert capi.validate(_bsr([0, 0, 0, 0, 0], [])) == capi.BSP_OK  # no blocks at all
+
+
+@pytest.mark.parametrize("name,kw,status,msg", BAD, ids=[b[0] for b in BAD])
+def test_validate_rejects_malformed(name, kw, status, msg):
+    assert capi.validate(_bsr(**kw)) == status
+    assert msg in capi.last_error()
+
+
+@pytest.mark.parametrize("H,Wd,R,C", [(100, 128, 32, 32), (128, 100, 32, 32), (128, 128, 0, 32),
+                                      (128, 128, 32, -32)])
+def test_validate_rejects_bad_shapes(H, Wd, R, C):
+    nbr = max(1, H // max(R, 1))
+    b = capi.Bsr(H, Wd, R, C, np.zeros(nbr + 1, np.int32), np.zeros(0, np.int32))
+    assert capi.validate(b) == capi.BSP_ERR_BAD_STRUCTURE
+
+
+def test_null_arguments():
+    lib = capi.load()
+    assert lib.bsp_validate_bsr(None) == capi.BSP_ERR_INVALID_ARGUMENT
+    d = _bsr(**GOOD).desc()
+    d.indptr = ctypes.cast(None, ctypes.POINTER(ctypes.c_int32))
+    assert lib.bsp_validate_bsr(ctypes.byref(d)) == capi.BSP_ERR_INVALID_ARGUMENT
+    assert lib.bsp_spmm_plan_create(None, ctypes.byref(_bsr(**GOOD).desc()), 64, 0, 0, 0) == \
+        capi.BSP_ERR_INVALID_ARGUMENT
+    assert lib.bsp_spmm(None, None, None, 0, None, 0, None) == capi.BSP_ERR_INVALID_ARGUMENT
+    assert lib.bsp_sddmm(None, None, None, 0, None, 0, None, None) == capi.BSP_ERR_INVALID_ARGUMENT
+    assert lib.bsp_plan_destroy(None) == capi.BSP_OK
+    g = _bsr(**GOOD)
+    assert lib.bsp_host_spmm(ctypes.byref(g.desc()), None, None, 64, None, 0, 0) == \
+        capi.BSP_ERR_INVALID_ARGUMENT
+
+
+def test_plan_create_rejects_before_touching_a_device():
+    """Argument and structure errors are reported the same with or without a GPU."""
+    lib = capi.load()
+    h = ctypes.c_void_p()
+    good = _bsr(**GOOD)
+    assert lib.bsp_spmm_plan_create(ctypes.byref(h), ctypes.byref(good.desc()), 64, 0, 7, 0) == \
+        capi.BSP_ERR_INVALID_ARGUMENT  # bad dtype
+    assert lib.bsp_spmm_plan_create(ctypes.byref(h), ctypes.byref(good.desc()), 64, 5, 0, 0) == \
+        capi.BSP_ERR_INVALID_ARGUMENT  # bad layout
+    assert lib.bsp_spmm_plan_create(ctypes.byref(h), ctypes.byref(good.desc()), 64, 1, 0, 0) == \
+        capi.BSP_ERR_UNSUPPORTED  # column-major B
+    bad = _bsr(**BAD[0][1])
+    assert lib.bsp_spmm_plan_create(ctypes.byref(h), ctypes.byref(bad.desc()), 64, 0, 0, 0) == \
+        capi.BSP_ERR_BAD_STRUCTURE
+    assert lib.bsp_sddmm_plan_create(ctypes.byref(h), ctypes.byref(bad.desc()), 64, 0, 0, 0) == \
+        capi.BSP_ERR_BAD_STRUCTURE
+    assert not h
+
+
+def test_schedule_rejects_unsupported_sizes():
+    odd = capi.Bsr(96, 96, 48, 48, np.array([0, 1, 1], np.int32), np.array([0], np.int32))
+    with pytest.raises(capi.BsparseError) as e:
+        capi.spmm_schedule(odd, 64)
+    assert e.value.status == capi.BSP_ERR_UNSUPPORTED
+    with pytest.raises(capi.BsparseError) as e:
+        capi.spmm_schedule(_bsr(**GOOD), 48)  # N not a multiple of 32
+    assert e.value.status == capi.BSP_ERR_UNSUPPORTED
+    with pytest.raises(capi.BsparseError) as e:
+        capi.sddmm_schedule(_bsr(**GOOD), 40)
+    assert e.value.status == capi.BSP_ERR_UNSUPPORTED
+
+
+# ---------------------------------------------------------------------------
+# Schedule invariants
+def _expected_entries(s):
+    """{sub_row: [(b_row, a_off), ...]} in CSR order."""
+    RS, CS = s.R // 32, s.C // 32
+    exp = {}
+    for sr in range(s.H // 32):
+        i, sub = divmod(sr, RS)
+        lst = []
+        for blk in range(s.indptr[i], s.indptr[i + 1]):
+            for t in range(CS):
+                lst.append((int(s.indices[blk]) * s.C + 32 * t, blk * s.R * s.C + 32 * sub * s.C + 32 * t))
+        exp[sr] = lst
+    return exp
+
+
+def _check_spmm_schedule(s, N, num_cus, split_env=None, monkeypatch=None):
+    if split_env is not None:
+        monkeypatch.setenv("BSP_SPMM_SPLIT", str(split_env))
+    sch = capi.spmm_schedule(capi.Bsr(s.H, s.W, s.R, s.C, s.indptr, s.indices), N, num_cus)
+    info, items = sch["info"], sch["items"]
+    assert info["tile_n"] in (128, 256) and info["n_tiles"] == -(-N // info["tile_n"])
+    exp = _expected_entries(s)
+    seen = {sr: [] for sr in exp}
+    slots = set()
+    for row, e0, e1, slot, base, npieces in items:
+        seen[row].append((e0, e1, slot, base, npieces))
+    for sr, pieces in seen.items():
+        assert pieces, f"sub-row {sr} has no work item (its output would not be written)"
+        pieces.sort()
+        ents = []
+        for e0, e1, *_ in pieces:
+            ents += list(zip(sch["ent_row"][e0:e1].tolist(), sch["ent_off"][e0:e1].tolist()))
+        assert ents == exp[sr], f"sub-row {sr} entries differ"
+        assert all(pieces[k][1] == pieces[k + 1][0] for k in range(len(pieces) - 1)), "pieces not contiguous"
+        if len(pieces) == 1:
+            assert pieces[0][2] == -1 and pieces[0][4] == 0
+        else:
+            base, npieces = pieces[0][3], pieces[0][4]
+            assert npieces == len(pieces)
+            assert sorted(p[2] for p in pieces) == list(range(base, base + npieces))
+            assert all(p[3] == base and p[4] == npieces for p in pieces)
+            slots.update(p[2] for p in pieces)
+    assert len(slots) == info["n_slots"]
+    assert info["max_item_entries"] == max((e1 - e0) for _, e0, e1, *_ in items)
+    wg = sch["wgmap"]
+    assert info["grid"] == wg.size and wg.size % 8 == 0
+    real = np.sort(wg[wg >= 0])
+    np.testing.assert_array_equal(real, np.arange(len(items) * info["n_tiles"]))
+    # Each XCD (workgroup id modulo 8) covers whole column groups of its items.
+    per_xcd = {}
+    for g, u in enumerate(wg):
+        if u >= 0:
+            per_xcd.setdefault(g % 8, set()).add(u % info["n_tiles"])
+    sizes = {len(t) for t in per_xcd.values()}
+    assert len(sizes) <= 1, "XCDs cover unequal numbers of tiles"
+    return sch
+
+
+@pytest.mark.parametrize("num_cus", [8, 80, 256])
+def test_spmm_schedule_uniform(num_cus):
+    w = W.spmm_workload(2048, 2048, 512, 32, 32, 0.1, seed=1)
+    _check_spmm_schedule(w["a"], 512, num_cus)
+
+
+def test_spmm_schedule_skewed_splits_long_rows():
+    s = W.workload_spmm_skewed()["a"]
+    sch = _check_spmm_schedule(s, 1024, 256)
+    info = sch["info"]
+    counts = np.diff(s.indptr)
+    assert info["n_split_rows"] > 0
+    assert info["max_item_entries"] < counts.max()
+    # Per-XCD cost spread stays within one item's cost.
+    costs = {}
+    for g, u in enumerate(sch["wgmap"]):
+        if u >= 0:
+            it = sch["items"][u // info["n_tiles"]]
+            costs[g % 8] = costs.get(g % 8, 0) + (it[2] - it[1]) + (4 if it[3] >= 0 else 2)
+    assert max(costs.values()) - min(costs.values()) <= info["max_item_entries"] + 4
+
+
+@pytest.mark.parametrize("split", [1, 2, 5])
+def test_spmm_schedule_forced_splits(monkeypatch, split):
+    w = W.spmm_workload(1024, 1024, 256, 32, 32, 0.3, seed=2)
+    sch = _check_spmm_schedule(w["a"], 256, 256, split, monkeypatch)
+    assert sch["info"]["max_item_entries"] <= split
+
+
+@pytest.mark.parametrize("name,s", [
+    ("R64", W.random_positions(512, 512, 64, 64, 20, np.random.default_rng(3))),
+    ("R32C64", W.random_positions(512, 512, 32, 64, 30, np.random.default_rng(4))),
+    ("R256", W.fill_tril(1024, 1024, 256, 256)),
+    ("dups", W.fill_col_as_reference(128, 128, 32, 32, 10)),
+    ("empty", W.BsrArrays(256, 256, 32, 32, np.zeros(9, np.int32), np.zeros(0, np.int32))),
+])
+def test_spmm_schedule_structures(name, s):
+    _check_spmm_schedule(s, 128, 256)
+
+
+def test_sddmm_schedule_covers_every_output_sub_block_once():
+    rng = np.random.default_rng(8)
+    for R, C in [(32, 32), (64, 32), (32, 64), (128, 128)]:
+        m = W.random_positions(1024, 1024, R, C, 12, rng)
+        sch = capi.sddmm_schedule(capi.Bsr(1024, 1024, R, C, m.indptr, m.indices), 64)
+        offs = sorted(sch["ent_off"].tolist())
+        expect = sorted(blk * R * C + 32 * s * C + 32 * t for blk in range(m.nblocks)
+                        for s in range(R // 32) for t in range(C // 32))
+        assert offs == expect
+        covered = []
+        for x_row0, e0, e1, *_ in sch["items"]:
+            assert 0 < e1 - e0 <= sch["info"]["max_item_entries"]
+            covered += list(range(e0, e1))
+            for e in range(e0, e1):  # x rows of the item are the block row of its entries
+                blk = sch["ent_off"][e] // (R * C)
+                i = int(np.searchsorted(m.indptr, blk, side="right") - 1)
+                assert i * R <= x_row0 < (i + 1) * R
+        assert sorted(covered) == list(range(len(offs)))
+        wg = sch["wgmap"]
+        np.testing.assert_array_equal(np.sort(wg[wg >= 0]), np.arange(len(sch["items"])))

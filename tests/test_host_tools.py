@@ -1,0 +1,48 @@
+"""The C++ host mirror (bsr_matrix / dense_matrix / HostCodeFunctionPtr-shaped
+entry points) through the reference-shaped test drivers in tests/cpp."""
+import subprocess
+
+import pytest
+
+from helpers import REPO
+
+BUILD = REPO / "tests" / "cpp" / "_build"
+
+
+def _tool(name):
+    exe = BUILD / name
+    if not exe.exists():  # built by __graft_entry__.build(); build here only if missing
+        subprocess.run(["make", "-s", "-C", str(REPO / "tests" / "cpp")], check=True, capture_output=True)
+    return str(exe)
+
+
+def _run(args, timeout):
+    p = subprocess.run(args, capture_output=True, text=True, timeout=timeout)
+    print(p.stdout[-4000:])
+    return p
+
+
+def test_sddmm_cpu_only_structure_mode():
+    """test_sddmm <all> -1: the reference's device-free mode (structure only)."""
+    p = _run([_tool("test_sddmm"), "-1", "-1"], 120)
+    assert p.returncode == 0, p.stdout + p.stderr
+    assert "Passed: 17 / 17" in p.stdout
+
+
+def test_block_spmm_lists_registry():
+    p = _run([_tool("test_block_spmm"), "list"], 120)
+    assert p.returncode == 0 and "test_1_block_id" in p.stdout
+
+
+@pytest.mark.gpu
+def test_block_spmm_registry_on_gpu():
+    p = _run([_tool("test_block_spmm"), "all", "0"], 600)
+    assert p.returncode == 0, p.stdout[-3000:] + p.stderr[-2000:]
+    assert "FAIL" not in p.stdout
+
+
+@pytest.mark.gpu
+def test_sddmm_registry_on_gpu():
+    p = _run([_tool("test_sddmm"), "-1", "0"], 300)
+    assert p.returncode == 0, p.stdout[-3000:] + p.stderr[-2000:]
+    assert "Passed: 17 / 17" in p.stdout

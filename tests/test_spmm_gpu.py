@@ -148,11 +148,25 @@ def test_forced_splits(monkeypatch, split):
     _case(w["a"], w["b"], "bf16", f"split={split} bf16")
 
 
-@pytest.mark.parametrize("tile_n", [32, 64, 128, 256])
-def test_tile_widths(monkeypatch, tile_n):
+@pytest.mark.parametrize("tile_n,stages", [(256, 4), (256, 6), (128, 6), (128, 8), (64, 8), (64, 12)])
+def test_tile_widths_and_stages(monkeypatch, tile_n, stages):
     monkeypatch.setenv("BSP_SPMM_TILE_N", str(tile_n))
+    monkeypatch.setenv("BSP_SPMM_STAGES", str(stages))
     w = W.spmm_workload(2048, 2048, 512, 32, 32, 0.1, seed=12)
-    _case(w["a"], w["b"], "f32", f"tile_n={tile_n}")
+    plan = capi.SpmmPlan(capi.Bsr(2048, 2048, 32, 32, w["a"].indptr, w["a"].indices), 512, "f32")
+    info = plan.info()
+    assert (info["tile_n"], info["stages"]) == (tile_n, stages)
+    got = run_spmm(w["a"], w["b"], "f32", plan=plan)
+    plan.close()
+    assert_parity(got, golden_spmm(w["a"], w["b"]), spmm_k_eff(w["a"]), f"tile_n={tile_n} stages={stages}")
+
+
+@pytest.mark.parametrize("N", [32, 96, 160, 288, 384])
+def test_partial_last_tile(N):
+    """N not a multiple of the tile width: the last tile is partial."""
+    w = W.spmm_workload(1024, 1024, N, 32, 32, 0.15, seed=N)
+    _case(w["a"], w["b"], "f32", f"N={N}")
+    _case(w["a"], w["b"], "bf16", f"N={N} bf16")
 
 
 def test_linearity_full_size():
