@@ -76,20 +76,20 @@ __device__ __forceinline__ void pack_pairs(const u32x4& r0, const u32x4& r1, u32
 }
 
 // ---------------------------------------------------------------------------
-// SpMM.  Every wave works alone on one 32 x 64 output tile (two 32x32 MFMA
-// tiles) of one work item (a run of one 32-row stripe's sub-block products);
-// a workgroup packs NW waves that cover NW consecutive 64-column tiles of the
-// same item (so they read the same A blocks, through the same L1).  There is
-// no barrier: each wave streams its entries through its own S-stage ring in
-// LDS, filled by direct global->LDS loads (global_load_lds_dwordx4, no
-// register staging), S-1 entries ahead of the one it computes.
-// A stage holds
-//   - the entry's 32x32 A sub-block (2 KB) as 128 16-byte chunks, chunk
-//     64*s + 32*q + r = A[r][16*s + 8*q .. +7], so the A operand of k-step s
-//     is one conflict-free ds_read_b128 at chunk 64*s + lane;
-//   - the 32 x 64 slice of row-major B (4 KB), row k at 128*k bytes, its
-//     16-byte chunk c stored at slot c ^ 4*((k >> 1) & 1) so that the rows a
-//     transpose read touches fall on distinct LDS banks.
+// SpMM.  Workgroup = one work item (a run of one 32-row stripe's sub-block
+// products) x one tile of TN = 128*NTW output columns; 4 waves, each owning
+// NTW 32-column MFMA tiles.
+//
+// Data movement is an S-stage ring in LDS filled by direct global->LDS loads
+// (global_load_lds_dwordx4, no register staging), so S-1 entries are in flight
+// per workgroup while one computes; one barrier per entry.  A stage holds
+//   - the entry's 32x32 A sub-block (2 KB, shared by the four waves) as 128
+//     16-byte chunks, chunk 64*s + 32*q + r = A[r][16*s + 8*q .. +7], so the
+//     A operand of k-step s is one conflict-free ds_read_b128 at chunk
+//     64*s + lane;
+//   - the 32 x TN slice of row-major B (64*TN bytes), row k at k*2*TN bytes,
+//     its 16-byte chunk c stored at slot c ^ 4*(k % 4) (spreads the rows one
+//     transpose read touches over the LDS banks).
 // The B operand (8 consecutive k at one column) is read with two
 // ds_read_b64_tr_b16: in each 16-lane group, source lane 4*j + m addresses
 // row k0+j, columns n+4m..n+4m+3, and output lane i receives rows k0..k0+3 of
@@ -97,16 +97,13 @@ __device__ __forceinline__ void pack_pairs(const u32x4& r0, const u32x4& r1, u32
 namespace spmm_detail {
 
 constexpr int kA_BYTES = 2048;
-constexpr int kB_BYTES = 4096;  // 32 rows x 64 columns of bf16
-constexpr int kSTAGE = kA_BYTES + kB_BYTES;
-constexpr int kLOADS = 6;       // 16-byte DMA instructions per stage: 2 for A, 4 for B
 
 // Direct global->LDS load of 16 bytes per lane: lane L's bytes land at
 // lds_wave_base + 16*L (lds_wave_base is wave-uniform).  Issued as inline asm
 // so that the compiler does not track it: its own bookkeeping would otherwise
-// wait for every outstanding load before each LDS read, which serialises the
-// ring.  Completion is awaited explicitly with wait_vmcnt.  Nothing else in
-// these kernels uses M0.
+// wait for every outstanding load before each LDS read or barrier, which
+// serialises the ring.  Completion is awaited explicitly with wait_vmcnt.
+// Nothing else in these kernels uses M0.
 __device__ __forceinline__ void gl_lds16(const void* g, uint32_t lds_wave_base) {
     const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_wave_base);
     __asm__ volatile(
@@ -115,6 +112,15 @@ __device__ __forceinline__ void gl_lds16(const void* g, uint32_t lds_wave_base) 
         :
         : "v"(g), "s"(lds)
         : "memory");
+}
+
+// Workgroup barrier without a memory fence (a fence would wait for all
+// outstanding loads); the empty asm statements keep the compiler from moving
+// memory accesses across it.
+__device__ __forceinline__ void barrier_no_fence() {
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
 }
 
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
@@ -150,13 +156,13 @@ __device__ __forceinline__ u32x4 ld_tr_b16(const uint8_t* lds) {
 
 }  // namespace spmm_detail
 
-// Stores the accumulators of one wave's 32 x 64 tile (columns past N skipped).
-template <bool OUT_BF16>
-__device__ __forceinline__ void spmm_store_wave(const SpmmArgs& p, const f32x16 (&acc)[2], int64_t row0,
-                                                int col0, int l32, int q) {
+// Stores the accumulators of one 32 x TN tile (columns past N skipped).
+template <int NTW, bool OUT_BF16>
+__device__ __forceinline__ void spmm_store_tile(const SpmmArgs& p, const f32x16 (&acc)[NTW], int64_t row0,
+                                                int n0, int wave, int l32, int q) {
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-        const int64_t col = col0 + nt * 32 + l32;
+    for (int nt = 0; nt < NTW; ++nt) {
+        const int64_t col = n0 + wave * (NTW * 32) + nt * 32 + l32;
         if (col >= p.N) continue;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
@@ -169,75 +175,83 @@ __device__ __forceinline__ void spmm_store_wave(const SpmmArgs& p, const f32x16 
     }
 }
 
-template <int NW, int S, bool OUT_BF16>
-__global__ __launch_bounds__(NW * 64) void spmm_kernel(SpmmArgs p) {
+template <int NTW, int S, bool OUT_BF16>
+__global__ __launch_bounds__(256) void spmm_kernel(SpmmArgs p) {
     using namespace spmm_detail;
-    static_assert(kLOADS * (S - 2) < 64, "vmcnt budget");
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[NW * S * kSTAGE];
+    constexpr int TN = 128 * NTW;
+    constexpr int ROW_BYTES = 2 * TN;
+    constexpr int B_BYTES = 32 * ROW_BYTES;
+    constexpr int STAGE = kA_BYTES + B_BYTES;
+    constexpr int BI = B_BYTES / 1024 / 4;  // B wave-instructions per wave per stage (= 2*NTW)
+    constexpr int PER = BI + 1;              // loads per wave per stage (B + a half-wave of A)
+    static_assert(PER * (S - 2) < 64, "vmcnt budget");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[S * STAGE];
 
     const SpmmWg it = load_const(p.wgs + blockIdx.x);
     if (it.row < 0) return;
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave
     const int l32 = lane & 31, q = lane >> 5;
-    const int col0 = (it.tile * NW + wave) * 64;  // this wave's first output column
-    if (col0 >= p.N) return;                       // a partial last group
-    const uint32_t ring = lds_address(smem) + wave * S * kSTAGE;
-    const uint8_t* ring_ptr = smem + wave * S * kSTAGE;
+    const int n0 = it.tile * TN;
+    const uint32_t lds0 = lds_address(smem);
 
-    // Per-lane global offsets of this lane's chunks in an entry.
-    // A DMA d (d = 0, 1): chunk 64*d + lane = A[lane % 32][16*d + 8*(lane / 32)].
-    const int a_goff = (lane & 31) * p.lda + 8 * (lane >> 5);
-    // B DMA j (j = 0..3): rows 8*j + lane/8, stored slot lane%8 holds chunk slot ^ f(row).
-    int64_t b_goff[4];
+    // Loads of one entry, per wave: lanes 0-31 fetch A chunks 32*wave + lane,
+    // i.e. A[lane][8*wave .. +7] (chunk 64*s + 32*q + r holds A[r][16*s + 8*q ..]),
+    // and BI wave-wide 1 KB pieces of the swizzled B slice.
+    const int a_goff = (lane & 31) * p.lda + 8 * wave;
+    const uint32_t a_lds = lds0 + wave * 512;
+    const uint32_t b_lds = lds0 + kA_BYTES + wave * BI * 1024;
+    int64_t b_goff[BI];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int r = 8 * j + (lane >> 3);
-        const int c = (lane & 7) ^ (4 * ((r >> 1) & 1));
+    for (int j = 0; j < BI; ++j) {
+        const int byte = (wave * BI + j) * 1024 + lane * 16;
+        const int r = byte / ROW_BYTES;
+        const int slot = (byte % ROW_BYTES) / 16;
         // Columns past N (a partial last tile) read a valid chunk; they are not stored.
-        b_goff[j] = (int64_t)r * p.ldb + min(col0 + 8 * c, p.N - 8);
+        const int col = min(n0 + 8 * (slot ^ (4 * (r & 3))), p.N - 8);
+        b_goff[j] = (int64_t)r * p.ldb + col;
     }
 
     auto issue = [&](int64_t ent, int stage) {
         const int32_t brow = (int32_t)(ent & 0xffffffff);
         const uint16_t* ablk = p.a + (ent >> 32) * 32;
         const uint16_t* bpan = p.b + (int64_t)brow * p.ldb;
-        const uint32_t st = ring + (uint32_t)stage * kSTAGE;
-        gl_lds16(ablk + a_goff, st);
-        gl_lds16(ablk + a_goff + 16, st + 1024);
+        const uint32_t soff = (uint32_t)stage * STAGE;
+        if (lane < 32) gl_lds16(ablk + a_goff, a_lds + soff);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) gl_lds16(bpan + b_goff[j], st + kA_BYTES + j * 1024);
+        for (int j = 0; j < BI; ++j) gl_lds16(bpan + b_goff[j], b_lds + soff + j * 1024);
     };
 
     // Per-lane LDS offsets of the operand reads (stage-relative).
     const int a_rd = lane * 16;  // + s * 1024
-    int b_rd[2][2][2];           // [k-step][half][tile]
+    int b_rd[2][2][NTW];         // [k-step][half][tile]
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
+            for (int nt = 0; nt < NTW; ++nt) {
                 const int g = lane >> 4;
                 const int r = 16 * s2 + 8 * (g >> 1) + 4 * h + ((lane & 15) >> 2);
-                const int col = nt * 32 + 16 * (g & 1) + 4 * (lane & 3);
+                const int col = wave * (NTW * 32) + nt * 32 + 16 * (g & 1) + 4 * (lane & 3);
                 const int c = col >> 3;
-                b_rd[s2][h][nt] = kA_BYTES + r * 128 + 16 * (c ^ (4 * ((r >> 1) & 1))) + 2 * (col & 7);
+                b_rd[s2][h][nt] = kA_BYTES + r * ROW_BYTES + 16 * (c ^ (4 * (r & 3))) + 2 * (col & 7);
             }
 
-    f32x16 acc[2];
+    f32x16 acc[NTW];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < NTW; ++i)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
 
     auto compute = [&](int stage) {
-        const uint8_t* st = ring_ptr + stage * kSTAGE;
+        const uint8_t* st = smem + stage * STAGE;
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
             const u32x4 av = *(const u32x4*)(st + s2 * 1024 + a_rd);
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
+            for (int nt = 0; nt < NTW; ++nt) {
                 const u32x4 lo = ld_tr_b16(st + b_rd[s2][0][nt]);
                 const u32x4 hi = ld_tr_b16(st + b_rd[s2][1][nt]);
                 acc[nt] = mfma32(av, u32x4{lo.x, lo.y, hi.x, hi.y}, acc[nt]);
@@ -250,13 +264,15 @@ __global__ __launch_bounds__(NW * 64) void spmm_kernel(SpmmArgs p) {
 #pragma unroll
     for (int i = 0; i < S - 1; ++i)
         if (i < n) issue(load_const(ents + i), i);
-    // Main loop: stage k is complete once kLOADS*(S-2) loads (the stages
-    // issued after it) remain.  The slot refilled here was read by the
-    // previous iteration, whose operands the MFMAs have already consumed.
-    int k = 0, stage = 0;
+    // Main loop: stage k is complete once PER*(S-2) loads (the stages issued
+    // after it) remain; the entry word for the next issue is fetched one
+    // iteration ahead.
+    int k = 0;
+    int stage = 0;
     int64_t next_ent = (S - 1 < n) ? load_const(ents + S - 1) : 0;
     for (; k < n - (S - 1); ++k) {
-        wait_vmcnt<kLOADS * (S - 2)>();
+        wait_vmcnt<PER * (S - 2)>();
+        barrier_no_fence();  // stage k visible to all; every wave is done with stage k-1
         issue(next_ent, stage == 0 ? S - 1 : stage - 1);
         next_ent = (k + S < n) ? load_const(ents + k + S) : 0;
         compute(stage);
@@ -264,7 +280,8 @@ __global__ __launch_bounds__(NW * 64) void spmm_kernel(SpmmArgs p) {
     }
     // Tail: nothing left to issue; fewer stages are in flight.
     for (; k < n; ++k) {
-        wait_stages<kLOADS, S - 2>(n - 1 - k);
+        wait_stages<PER, S - 2>(n - 1 - k);
+        barrier_no_fence();
         compute(stage);
         stage = stage == S - 1 ? 0 : stage + 1;
     }
@@ -272,39 +289,39 @@ __global__ __launch_bounds__(NW * 64) void spmm_kernel(SpmmArgs p) {
     if (it.slot >= 0) {
         // Piece of a split row: the partial goes to scratch; spmm_reduce_kernel
         // adds the pieces in order after this launch.
-        float* mine = p.ws + ((int64_t)it.slot * p.n_tiles + it.tile) * (NW * 64 * 32) + wave * (64 * 32);
+        constexpr int PF = NTW * 16 * 256;
+        float* mine = p.ws + ((int64_t)it.slot * p.n_tiles + it.tile) * PF;
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < NTW; ++nt)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) mine[(nt * 16 + v) * 64 + lane] = acc[nt][v];
+            for (int v = 0; v < 16; ++v) mine[(nt * 16 + v) * 256 + tid] = acc[nt][v];
         return;
     }
-    spmm_store_wave<OUT_BF16>(p, acc, (int64_t)it.row * 32, col0, l32, q);
+    spmm_store_tile<NTW, OUT_BF16>(p, acc, (int64_t)it.row * 32, n0, wave, l32, q);
 }
 
 // Adds the partials of each split row in piece order (deterministic) and
-// stores the tile: one workgroup of NW waves per (split row, column group).
-template <int NW, bool OUT_BF16>
-__global__ __launch_bounds__(NW * 64) void spmm_reduce_kernel(SpmmArgs p) {
+// stores the 32 x TN tile: one workgroup per (split row, tile).
+template <int NTW, bool OUT_BF16>
+__global__ __launch_bounds__(256) void spmm_reduce_kernel(SpmmArgs p) {
+    constexpr int PF = NTW * 16 * 256;
     const int tile = blockIdx.x % p.n_tiles;
     const SpmmSplit sp = load_const(p.splits + blockIdx.x / p.n_tiles);
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int col0 = (tile * NW + wave) * 64;
-    if (col0 >= p.N) return;
-    f32x16 acc[2];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    f32x16 acc[NTW];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
+    for (int nt = 0; nt < NTW; ++nt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[nt][v] = 0.0f;
     for (int pc = 0; pc < sp.npieces; ++pc) {
-        const float* src = p.ws + ((int64_t)(sp.base + pc) * p.n_tiles + tile) * (NW * 64 * 32) + wave * (64 * 32);
+        const float* src = p.ws + ((int64_t)(sp.base + pc) * p.n_tiles + tile) * PF;
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < NTW; ++nt)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) acc[nt][v] += src[(nt * 16 + v) * 64 + lane];
+            for (int v = 0; v < 16; ++v) acc[nt][v] += src[(nt * 16 + v) * 256 + tid];
     }
-    spmm_store_wave<OUT_BF16>(p, acc, (int64_t)sp.row * 32, col0, lane & 31, lane >> 5);
+    spmm_store_tile<NTW, OUT_BF16>(p, acc, (int64_t)sp.row * 32, tile * 128 * NTW, wave, lane & 31, lane >> 5);
 }
 
 // ---------------------------------------------------------------------------
@@ -385,18 +402,18 @@ __global__ __launch_bounds__(256) void sddmm_kernel(SddmmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-template <int NW, int S>
+template <int NTW, int S>
 static void launch_spmm_t(const SpmmArgs& a, bool out_bf16, int grid, int n_split, hipStream_t stream) {
     if (out_bf16)
-        hipLaunchKernelGGL((spmm_kernel<NW, S, true>), dim3(grid), dim3(NW * 64), 0, stream, a);
+        hipLaunchKernelGGL((spmm_kernel<NTW, S, true>), dim3(grid), dim3(256), 0, stream, a);
     else
-        hipLaunchKernelGGL((spmm_kernel<NW, S, false>), dim3(grid), dim3(NW * 64), 0, stream, a);
+        hipLaunchKernelGGL((spmm_kernel<NTW, S, false>), dim3(grid), dim3(256), 0, stream, a);
     if (n_split > 0) {
         const int g = n_split * a.n_tiles;
         if (out_bf16)
-            hipLaunchKernelGGL((spmm_reduce_kernel<NW, true>), dim3(g), dim3(NW * 64), 0, stream, a);
+            hipLaunchKernelGGL((spmm_reduce_kernel<NTW, true>), dim3(g), dim3(256), 0, stream, a);
         else
-            hipLaunchKernelGGL((spmm_reduce_kernel<NW, false>), dim3(g), dim3(NW * 64), 0, stream, a);
+            hipLaunchKernelGGL((spmm_reduce_kernel<NTW, false>), dim3(g), dim3(256), 0, stream, a);
     }
 }
 
@@ -404,12 +421,11 @@ hipError_t launch_spmm(const SpmmArgs& a, int tile_n, int stages, bool out_bf16,
                        hipStream_t stream) {
     if (grid <= 0) return hipSuccess;
     switch (tile_n * 100 + stages) {
-        case 25604: launch_spmm_t<4, 4>(a, out_bf16, grid, n_split, stream); break;
-        case 25606: launch_spmm_t<4, 6>(a, out_bf16, grid, n_split, stream); break;
-        case 12806: launch_spmm_t<2, 6>(a, out_bf16, grid, n_split, stream); break;
-        case 12808: launch_spmm_t<2, 8>(a, out_bf16, grid, n_split, stream); break;
-        case 6408: launch_spmm_t<1, 8>(a, out_bf16, grid, n_split, stream); break;
-        case 6412: launch_spmm_t<1, 12>(a, out_bf16, grid, n_split, stream); break;
+        case 12804: launch_spmm_t<1, 4>(a, out_bf16, grid, n_split, stream); break;
+        case 12806: launch_spmm_t<1, 6>(a, out_bf16, grid, n_split, stream); break;
+        case 12808: launch_spmm_t<1, 8>(a, out_bf16, grid, n_split, stream); break;
+        case 25603: launch_spmm_t<2, 3>(a, out_bf16, grid, n_split, stream); break;
+        case 25604: launch_spmm_t<2, 4>(a, out_bf16, grid, n_split, stream); break;
         default:
             return hipErrorInvalidValue;
     }

@@ -42,14 +42,13 @@ struct SddmmArgs {
 // Floats of partial-result scratch per (slot, tile): a 32 x tile_n block.
 inline int64_t spmm_partial_floats(int tile_n) { return (int64_t)tile_n * 32; }
 
-// Workgroup tile widths (64 columns per wave) and the LDS ring stages each
-// supports: the default and the supported set.
-inline int spmm_default_stages(int tile_n) { return tile_n >= 256 ? 6 : 8; }
+// Workgroup tile widths (4 waves of 32 or 64 columns) and the LDS ring stages
+// each supports: the default and the supported set.
+inline int spmm_default_stages(int tile_n) { return tile_n >= 256 ? 4 : 6; }
 inline bool spmm_stages_supported(int tile_n, int stages) {
     switch (tile_n) {
-        case 256: return stages == 4 || stages == 6;
-        case 128: return stages == 6 || stages == 8;
-        case 64: return stages == 8 || stages == 12;
+        case 256: return stages == 3 || stages == 4;
+        case 128: return stages == 4 || stages == 6 || stages == 8;
         default: return false;
     }
 }

@@ -203,11 +203,12 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
         return BSP_ERR_UNSUPPORTED;
     }
 
-    // Workgroup width: 256 columns (four waves of 64), or 128 / 64 when N is
-    // narrow; the last group of a row may be partial.
+    // Workgroup width: 128 columns (four waves of 32); 256 (four waves of 64)
+    // only when N is a multiple of 256 and rows alone give two workgroups per
+    // compute unit.  The last tile of a row may be partial.
     int64_t tn = env_int("BSP_SPMM_TILE_N", 0);
-    if (tn != 0 && tn != 64 && tn != 128 && tn != 256) tn = 0;
-    if (tn == 0) tn = N >= 256 ? 256 : (N >= 128 ? 128 : 64);
+    if (tn != 0 && tn != 128 && tn != 256) tn = 0;
+    if (tn == 0) tn = (N % 256 == 0 && nsr * (N / 256) >= 2 * (int64_t)num_cus) ? 256 : 128;
     s.tile_n = (int32_t)tn;
     s.n_tiles = (int32_t)((N + tn - 1) / tn);
 
