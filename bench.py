@@ -51,9 +51,9 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--copy-calibration", action="store_true",
-                   help="first run one 256 MiB device-to-device copy (a kernel of known traffic, "
+                   help="first run a 256 MiB device copy and a 256 MiB elementwise multiply (kernels of known traffic, "
                         "for scaling FETCH_SIZE / WRITE_SIZE counters)")
-    p.add_argument("--only", default="", help="comma list of sections to run: head (25%% fp32 only), sweep, sddmm, skewed, attention")
+    p.add_argument("--only", default="", help="comma list of sections to run: head (25%% fp32 only), sweep, sddmm, skewed, attention, host")
     return p.parse_args()
 
 
@@ -187,6 +187,24 @@ def kernel_name(tile_n, stages):
     return f"bsp::spmm_kernel<{tile_n // 128}, {stages}, false>"
 
 
+TRAFFIC_FILE = REPO / "profiles" / "spmm_kernel_d25_4096x4096_N512_traffic.md"
+
+
+def measured_traffic(kernel):
+    """HBM-side bytes per launch of the headline kernel: FETCH_SIZE x 2.0 +
+    WRITE_SIZE x 1.0 (factors from kernels of known traffic), from the
+    committed counter summary, or None when that summary is for another
+    kernel."""
+    try:
+        text = TRAFFIC_FILE.read_text()
+    except OSError:
+        return None
+    kv = dict(line.split(": ", 1) for line in text.splitlines() if line.startswith("traffic_"))
+    if kv.get("traffic_kernel") != kernel:
+        return None
+    return int(kv["traffic_bytes_per_launch"])
+
+
 def roofline(flops, nbytes, k_s, row):
     """The bound is the lower roof for the kernel's algorithmic intensity:
     MFMA when FLOP/byte >= peak FLOP/s / peak bytes/s (312.5), else HBM."""
@@ -194,9 +212,11 @@ def roofline(flops, nbytes, k_s, row):
     ridge = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
     tflops = flops / k_s / 1e12
     gbs = nbytes / k_s / 1e9
-    r = {"kernel": kernel_name(row["tile_n"], row["stages"]), "us_per_launch": row["us_per_launch"],
+    kernel = kernel_name(row["tile_n"], row["stages"])
+    r = {"kernel": kernel, "us_per_launch": row["us_per_launch"],
          "algorithmic_flop_per_launch": flops, "algorithmic_bytes_per_launch": nbytes,
-         "intensity_flop_per_byte": round(ai, 1), "traffic": None,
+         "intensity_flop_per_byte": round(ai, 1), "traffic": measured_traffic(kernel),
+         "traffic_source": TRAFFIC_FILE.name,
          "mfma_tflops": round(tflops, 3), "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 4),
          "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)}
     if ai >= ridge:
@@ -263,9 +283,12 @@ def main():
     only = set(filter(None, args.only.split(",")))
     steps, warmup = args.steps, args.warmup
     if args.copy_calibration:
-        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")  # 256 MiB
+        # Two kernels that each read 256 MiB and write 256 MiB: the runtime's
+        # device-to-device copy and an elementwise multiply.
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
         dst.copy_(src)
+        torch.mul(src, 2.0, out=dst)
         torch.cuda.synchronize()
         del src, dst
 
@@ -318,6 +341,25 @@ def main():
                             "spmm": summarize(t2, f2, b2, steps),
                             "pair_tflops": round((f1 + f2) / ((t1["launch_ms"] + t2["launch_ms"]) * 1e-3)
                                                  / 1e12, 3)}
+
+    if not only or "host" in only:
+        # The blocking host-buffer entry point (the reference operator's shape):
+        # plan, device allocation, PCIe upload of A and B, launch, download of
+        # C, synchronise, free.  Reported beside `value`, never as it.
+        w = W.workload_spmm_sweep(0.25)
+        a = w["a"]
+        bsr = capi.Bsr(a.H, a.W, a.R, a.C, a.indptr, a.indices)
+        capi.host_spmm(bsr, a.data, w["b"], "f32")
+        ts = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            capi.host_spmm(bsr, a.data, w["b"], "f32")
+            ts.append(time.perf_counter() - t0)
+        t_host = float(np.median(ts))
+        fl = W.spmm_flops(a.nblocks, 32, 32, 512)
+        out["host_entry"] = {"workload": "25% SpMM through bsp_host_spmm (host buffers, blocking)",
+                             "ms_per_call": round(t_host * 1e3, 3),
+                             "tflops": round(fl / t_host / 1e12, 4)}
 
     cpu = None
     if not args.no_cpu:

@@ -98,7 +98,7 @@ typedef struct bsp_plan_info {
     int32_t n_slots;     /* SpMM: partial-result slots used by split rows */
     int32_t grid;        /* workgroups per launch */
     int32_t max_item_entries;
-    int32_t stages;      /* SpMM: entries staged per pipeline group */
+    int32_t stages;      /* SpMM: depth of the LDS ring (entries in flight + 1) */
     int64_t workspace_bytes; /* device scratch owned by the plan */
 } bsp_plan_info;
 

@@ -8,9 +8,10 @@
 //   result:    acc[4*i + j] is C[8*i + 4*q + j][lane % 32]
 // Both operands must therefore be contiguous along k in each lane.  A blocks
 // and X rows already are; a row-major dense operand (B of SpMM, Y of SDDMM) is
-// contiguous along n instead, so it is staged through LDS as k-pairs: dword
-// (p, n) holds (B[2p][n], B[2p+1][n]), and a lane gathers its 8 k-values with
-// four dword reads.
+// contiguous along n instead.  SpMM stages B in LDS as it lies in memory and
+// reads it with the LDS transpose read (ds_read_b64_tr_b16); SDDMM re-packs
+// row-major Y into k-pairs in LDS (dword (p, n) holds (Y[2p][n], Y[2p+1][n]))
+// and a lane gathers its 8 k-values with four dword reads.
 //
 // Reference semantics followed: block_spmm/inc/bsr_matrix.hpp:954-1000 (SpMM),
 // sparse_common/bsr_matrix.hpp:816-857 (SDDMM).
