@@ -16,6 +16,7 @@ import numpy as np
 PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = PKG_DIR / "libbsparse.so"
 
+ABI_VERSION = 1  # BSP_ABI_VERSION of include/bsparse.h
 BSP_OK = 0
 BSP_ERR_INVALID_ARGUMENT = 1
 BSP_ERR_BAD_STRUCTURE = 2
@@ -109,6 +110,9 @@ def load(path: Optional[Path] = None, force_reload: bool = False) -> ctypes.CDLL
         fn = getattr(lib, name)  # AttributeError if a declared symbol is missing
         fn.restype = res
         fn.argtypes = args
+    if lib.bsp_abi_version() != ABI_VERSION:
+        raise ImportError(f"{p}: ABI version {lib.bsp_abi_version()}, this binding expects {ABI_VERSION}; "
+                          "rebuild with __graft_entry__.build()")
     if path is None:
         _lib = lib
     return lib

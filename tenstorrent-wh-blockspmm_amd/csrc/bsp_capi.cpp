@@ -105,11 +105,14 @@ void fill_info_spmm(const bsp::SpmmSchedule& s, bsp_plan_info* info) {
     info->n_slots = s.n_slots;
     info->grid = (int32_t)s.wgmap.size();
     info->max_item_entries = s.max_item_entries;
-    info->stages = bsp::spmm_default_stages(s.tile_n);
-    if (const char* v = std::getenv("BSP_SPMM_STAGES")) {
-        const int st = std::atoi(v);
-        if (bsp::spmm_stages_supported(s.tile_n, st)) info->stages = st;
+    // Ring depth: the tile width's default, or a supported override
+    // (BSP_SPMM_STAGES) for experiments.
+    bsp::SpmmVariant v = bsp::spmm_default_variant(s.tile_n);
+    if (const char* e = std::getenv("BSP_SPMM_STAGES")) {
+        const bsp::SpmmVariant w{s.tile_n, std::atoi(e)};
+        if (bsp::spmm_variant_supported(w)) v = w;
     }
+    info->stages = v.stages;
     info->workspace_bytes =
         (int64_t)s.n_slots * s.n_tiles * bsp::spmm_partial_floats(s.tile_n) * (int64_t)sizeof(float);
 }
@@ -269,8 +272,9 @@ int bsp_spmm(const bsp_plan* p, const uint16_t* a_vals, const uint16_t* b, int64
     args.lda = (int32_t)p->C;
     args.n_tiles = p->info.n_tiles;
     args.N = (int32_t)p->N;
-    hipError_t e = bsp::launch_spmm(args, p->info.tile_n, p->info.stages, p->out_dtype == BSP_DTYPE_BF16,
-                                    p->info.grid, p->info.n_split_rows, (hipStream_t)stream);
+    const bsp::SpmmVariant v{p->info.tile_n, p->info.stages};
+    hipError_t e = bsp::launch_spmm(args, v, p->out_dtype == BSP_DTYPE_BF16, p->info.grid, p->info.n_split_rows,
+                                    (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "SpMM launch");
     return BSP_OK;
 }

@@ -83,11 +83,15 @@ __device__ __forceinline__ void pack_pairs(const u32x4& r0, const u32x4& r1, u32
 //
 // Data movement is an S-stage ring in LDS filled by direct global->LDS loads
 // (global_load_lds_dwordx4, no register staging), so S-1 entries are in flight
-// per workgroup while one computes; one barrier per entry.  A stage holds
-//   - the entry's 32x32 A sub-block (2 KB, shared by the four waves) as 128
-//     16-byte chunks, chunk 64*s + 32*q + r = A[r][16*s + 8*q .. +7], so the
-//     A operand of k-step s is one conflict-free ds_read_b128 at chunk
-//     64*s + lane;
+// per workgroup while one is multiplied; one barrier per entry.  The operands
+// of the next entry are read into registers while the current one is
+// multiplied.  Stage s holds (in an A array and a B array)
+//   - the entry's 32x32 A sub-block (2 KB, shared by the four waves) as four
+//     512-byte segments, segment w = rows 8w..8w+7, its 16-byte chunk
+//     8*j + r%8 = A[8w + r%8][8*j .. 8*j+7].  Wave w loads segment w from 512
+//     contiguous bytes (a 32x32 block), and the A operand of k-step s for lane
+//     (r, q) is the chunk 8*(2s+q) + r%8 of segment r/8: each 8-lane group of
+//     the ds_read_b128 reads 128 contiguous bytes;
 //   - the 32 x TN slice of row-major B (64*TN bytes), row k at k*2*TN bytes,
 //     its 16-byte chunk c stored at slot c ^ 4*(k % 4) (spreads the rows one
 //     transpose read touches over the LDS banks).
@@ -182,11 +186,11 @@ __global__ __launch_bounds__(256) void spmm_kernel(SpmmArgs p) {
     constexpr int TN = 128 * NTW;
     constexpr int ROW_BYTES = 2 * TN;
     constexpr int B_BYTES = 32 * ROW_BYTES;
-    constexpr int STAGE = kA_BYTES + B_BYTES;
-    constexpr int BI = B_BYTES / 1024 / 4;  // B wave-instructions per wave per stage (= 2*NTW)
-    constexpr int PER = BI + 1;              // loads per wave per stage (B + a half-wave of A)
+    constexpr int BI = B_BYTES / 1024 / 4;  // B wave-instructions per wave per step (= 2*NTW)
+    constexpr int PER = BI + 1;              // loads per wave per step (B + a half-wave of A)
+    constexpr int B_RING = S * kA_BYTES;     // A ring first, then the B ring
     static_assert(PER * (S - 2) < 64, "vmcnt budget");
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[S * STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[S * (kA_BYTES + B_BYTES)];
 
     const SpmmWg it = load_const(p.wgs + blockIdx.x);
     if (it.row < 0) return;
@@ -197,12 +201,12 @@ __global__ __launch_bounds__(256) void spmm_kernel(SpmmArgs p) {
     const int n0 = it.tile * TN;
     const uint32_t lds0 = lds_address(smem);
 
-    // Loads of one entry, per wave: lanes 0-31 fetch A chunks 32*wave + lane,
-    // i.e. A[lane][8*wave .. +7] (chunk 64*s + 32*q + r holds A[r][16*s + 8*q ..]),
-    // and BI wave-wide 1 KB pieces of the swizzled B slice.
-    const int a_goff = (lane & 31) * p.lda + 8 * wave;
+    // Loads of one entry, per wave: lanes 0-31 fetch A segment `wave` (lane
+    // 8*j + i loads A[8*wave + i][8*j .. +7]) and BI wave-wide 1 KB pieces of
+    // the swizzled B slice.
+    const int a_goff = (8 * wave + (lane & 7)) * p.lda + 8 * ((lane & 31) >> 3);
     const uint32_t a_lds = lds0 + wave * 512;
-    const uint32_t b_lds = lds0 + kA_BYTES + wave * BI * 1024;
+    const uint32_t b_lds = lds0 + B_RING + wave * BI * 1024;
     int64_t b_goff[BI];
 #pragma unroll
     for (int j = 0; j < BI; ++j) {
@@ -214,18 +218,21 @@ __global__ __launch_bounds__(256) void spmm_kernel(SpmmArgs p) {
         b_goff[j] = (int64_t)r * p.ldb + col;
     }
 
-    auto issue = [&](int64_t ent, int stage) {
-        const int32_t brow = (int32_t)(ent & 0xffffffff);
-        const uint16_t* ablk = p.a + (ent >> 32) * 32;
-        const uint16_t* bpan = p.b + (int64_t)brow * p.ldb;
-        const uint32_t soff = (uint32_t)stage * STAGE;
-        if (lane < 32) gl_lds16(ablk + a_goff, a_lds + soff);
+    // Entry words: low 32 bits = first row of B, high 32 bits = A offset / 32.
+    const int e0 = it.e_begin, n = it.e_end - it.e_begin;
+    const uint32_t* words = (const uint32_t*)(p.ents + e0);
+    // Issues the PER loads of one entry into ring stage `stage`.
+    auto issue = [&](int e, int stage) {
+        const uint32_t bw = load_const(words + 2 * e);
+        const uint32_t aw = load_const(words + 2 * e + 1);
+        if (lane < 32) gl_lds16(p.a + (int64_t)aw * 32 + a_goff, a_lds + stage * kA_BYTES);
+        const uint16_t* bpan = p.b + (int64_t)bw * p.ldb;
 #pragma unroll
-        for (int j = 0; j < BI; ++j) gl_lds16(bpan + b_goff[j], b_lds + soff + j * 1024);
+        for (int j = 0; j < BI; ++j) gl_lds16(bpan + b_goff[j], b_lds + stage * B_BYTES + j * 1024);
     };
 
-    // Per-lane LDS offsets of the operand reads (stage-relative).
-    const int a_rd = lane * 16;  // + s * 1024
+    // Per-lane LDS offsets of the operand reads (ring-stage relative).
+    const int a_rd = (l32 >> 3) * 512 + (8 * q + (l32 & 7)) * 16;  // + s * 256
     int b_rd[2][2][NTW];         // [k-step][half][tile]
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
@@ -237,7 +244,7 @@ __global__ __launch_bounds__(256) void spmm_kernel(SpmmArgs p) {
                 const int r = 16 * s2 + 8 * (g >> 1) + 4 * h + ((lane & 15) >> 2);
                 const int col = wave * (NTW * 32) + nt * 32 + 16 * (g & 1) + 4 * (lane & 3);
                 const int c = col >> 3;
-                b_rd[s2][h][nt] = kA_BYTES + r * ROW_BYTES + 16 * (c ^ (4 * (r & 3))) + 2 * (col & 7);
+                b_rd[s2][h][nt] = r * ROW_BYTES + 16 * (c ^ (4 * (r & 3))) + 2 * (col & 7);
             }
 
     f32x16 acc[NTW];
@@ -246,45 +253,75 @@ __global__ __launch_bounds__(256) void spmm_kernel(SpmmArgs p) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
 
-    auto compute = [&](int stage) {
-        const uint8_t* st = smem + stage * STAGE;
+    // Operands of one entry in registers: A of both k-steps and the B
+    // operands of every tile.  The LDS reads of entry k+1 are issued right
+    // after entry k's MFMAs, so their latency overlaps the MFMAs, the wait for
+    // the next stage and the barrier.
+    struct Operands {
+        u32x4 a[2];
+        u32x4 b[2][NTW];
+    };
+    auto read_operands = [&](int stage, Operands& o) {
+        const uint8_t* as = smem + stage * kA_BYTES;
+        const uint8_t* bs = smem + B_RING + stage * B_BYTES;
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
-            const u32x4 av = *(const u32x4*)(st + s2 * 1024 + a_rd);
+            o.a[s2] = *(const u32x4*)(as + s2 * 256 + a_rd);
 #pragma unroll
             for (int nt = 0; nt < NTW; ++nt) {
-                const u32x4 lo = ld_tr_b16(st + b_rd[s2][0][nt]);
-                const u32x4 hi = ld_tr_b16(st + b_rd[s2][1][nt]);
-                acc[nt] = mfma32(av, u32x4{lo.x, lo.y, hi.x, hi.y}, acc[nt]);
+                const u32x4 lo = ld_tr_b16(bs + b_rd[s2][0][nt]);
+                const u32x4 hi = ld_tr_b16(bs + b_rd[s2][1][nt]);
+                o.b[s2][nt] = u32x4{lo.x, lo.y, hi.x, hi.y};
             }
         }
     };
-
-    const int e0 = it.e_begin, n = it.e_end - it.e_begin;
-    const int64_t* ents = p.ents + e0;
+    auto multiply = [&](const Operands& o) {
 #pragma unroll
-    for (int i = 0; i < S - 1; ++i)
-        if (i < n) issue(load_const(ents + i), i);
-    // Main loop: stage k is complete once PER*(S-2) loads (the stages issued
-    // after it) remain; the entry word for the next issue is fetched one
-    // iteration ahead.
-    int k = 0;
-    int stage = 0;
-    int64_t next_ent = (S - 1 < n) ? load_const(ents + S - 1) : 0;
-    for (; k < n - (S - 1); ++k) {
-        wait_vmcnt<PER * (S - 2)>();
-        barrier_no_fence();  // stage k visible to all; every wave is done with stage k-1
-        issue(next_ent, stage == 0 ? S - 1 : stage - 1);
-        next_ent = (k + S < n) ? load_const(ents + k + S) : 0;
-        compute(stage);
-        stage = stage == S - 1 ? 0 : stage + 1;
-    }
-    // Tail: nothing left to issue; fewer stages are in flight.
-    for (; k < n; ++k) {
-        wait_stages<PER, S - 2>(n - 1 - k);
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int nt = 0; nt < NTW; ++nt) acc[nt] = mfma32(o.a[s2], o.b[s2][nt], acc[nt]);
+    };
+
+    // Entry e lives in ring stage e % S.  Entries 0..S-2 are issued first;
+    // entry S-1 goes into the still unused last stage once entry 0 has landed.
+    // Iteration k multiplies entry k from registers, waits for entry k+1 to
+    // land (the loads issued after it are those of entries k+2..k+S-1), and
+    // after the barrier (every wave holds entry k's operands in registers, so
+    // stage k % S is free) issues entry k+S into stage k % S and reads entry
+    // k+1's operands.
+#pragma unroll
+    for (int e = 0; e < S - 1; ++e)
+        if (e < n) issue(e, e);
+    Operands cur;
+    if (n > 0) {
+        wait_stages<PER, S - 2>(n - 1);  // entry 0 landed
         barrier_no_fence();
-        compute(stage);
+        if (S - 1 < n) issue(S - 1, S - 1);
+        read_operands(0, cur);
+    }
+    int k = 0;
+    int stage = 0;  // stage of entry k
+    for (; k < n - S + 1; ++k) {
+        multiply(cur);
+        // Entry k's operand reads must be complete before the barrier frees
+        // its stage (the compiler would otherwise wait only at their first
+        // use, which it may schedule after the barrier and the next issue).
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        wait_vmcnt<PER * (S - 2)>();  // entry k+1 landed
+        barrier_no_fence();
+        if (k + S < n) issue(k + S, stage);
         stage = stage == S - 1 ? 0 : stage + 1;
+        read_operands(stage, cur);
+    }
+    // Tail: every entry is issued; fewer are in flight.
+    for (; k < n; ++k) {
+        multiply(cur);
+        if (k + 1 < n) {
+            wait_stages<PER, S - 2>(n - 2 - k);  // entry k+1 landed
+            barrier_no_fence();
+            stage = stage == S - 1 ? 0 : stage + 1;
+            read_operands(stage, cur);
+        }
     }
 
     if (it.slot >= 0) {
@@ -418,19 +455,18 @@ static void launch_spmm_t(const SpmmArgs& a, bool out_bf16, int grid, int n_spli
     }
 }
 
-hipError_t launch_spmm(const SpmmArgs& a, int tile_n, int stages, bool out_bf16, int grid, int n_split,
+hipError_t launch_spmm(const SpmmArgs& a, const SpmmVariant& v, bool out_bf16, int grid, int n_split,
                        hipStream_t stream) {
     if (grid <= 0) return hipSuccess;
-    switch (tile_n * 100 + stages) {
-        case 12804: launch_spmm_t<1, 4>(a, out_bf16, grid, n_split, stream); break;
-        case 12806: launch_spmm_t<1, 6>(a, out_bf16, grid, n_split, stream); break;
-        case 12808: launch_spmm_t<1, 8>(a, out_bf16, grid, n_split, stream); break;
-        case 25603: launch_spmm_t<2, 3>(a, out_bf16, grid, n_split, stream); break;
-        case 25604: launch_spmm_t<2, 4>(a, out_bf16, grid, n_split, stream); break;
-        default:
-            return hipErrorInvalidValue;
+    if (!spmm_variant_supported(v)) return hipErrorInvalidValue;
+#define BSP_SPMM_CASE(TN, S)                                              \
+    if (v.tile_n == TN && v.stages == S) {                               \
+        launch_spmm_t<TN / 128, S>(a, out_bf16, grid, n_split, stream);  \
+        return hipGetLastError();                                        \
     }
-    return hipGetLastError();
+    BSP_SPMM_VARIANTS(BSP_SPMM_CASE)
+#undef BSP_SPMM_CASE
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_sddmm(const SddmmArgs& a, bool y_colmajor, bool out_bf16, int grid,

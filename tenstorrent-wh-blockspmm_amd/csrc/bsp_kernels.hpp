@@ -42,19 +42,37 @@ struct SddmmArgs {
 // Floats of partial-result scratch per (slot, tile): a 32 x tile_n block.
 inline int64_t spmm_partial_floats(int tile_n) { return (int64_t)tile_n * 32; }
 
-// Workgroup tile widths (4 waves of 32 or 64 columns) and the LDS ring stages
-// each supports: the default and the supported set.
-inline int spmm_default_stages(int tile_n) { return tile_n >= 256 ? 4 : 6; }
-inline bool spmm_stages_supported(int tile_n, int stages) {
-    switch (tile_n) {
-        case 256: return stages == 3 || stages == 4;
-        case 128: return stages == 4 || stages == 6 || stages == 8;
-        default: return false;
-    }
+// Compiled SpMM kernel variants: workgroup tile width (4 waves of 32 or 64
+// columns) and ring depth (entries in flight + 1).  LDS per workgroup =
+// (2 KB + 64 * tile_n bytes) * stages; two workgroups share a compute unit
+// while that is at most 80 KB.
+#define BSP_SPMM_VARIANTS(X) \
+    X(128, 4)                \
+    X(128, 6)                \
+    X(128, 8)                \
+    X(256, 3)                \
+    X(256, 4)
+
+struct SpmmVariant {
+    int tile_n;
+    int stages;
+};
+
+inline bool spmm_variant_supported(const SpmmVariant& v) {
+#define BSP_SPMM_MATCH(TN, S) \
+    if (v.tile_n == TN && v.stages == S) return true;
+    BSP_SPMM_VARIANTS(BSP_SPMM_MATCH)
+#undef BSP_SPMM_MATCH
+    return false;
+}
+
+// Default ring depth for a tile width.
+inline SpmmVariant spmm_default_variant(int tile_n) {
+    return tile_n >= 256 ? SpmmVariant{256, 4} : SpmmVariant{128, 6};
 }
 
 // Launches the SpMM kernel and, when the plan has split rows, the reduce kernel.
-hipError_t launch_spmm(const SpmmArgs& a, int tile_n, int stages, bool out_bf16, int grid, int n_split,
+hipError_t launch_spmm(const SpmmArgs& a, const SpmmVariant& v, bool out_bf16, int grid, int n_split,
                        hipStream_t stream);
 hipError_t launch_sddmm(const SddmmArgs& a, bool y_colmajor, bool out_bf16, int grid,
                         hipStream_t stream);

@@ -148,17 +148,24 @@ def test_forced_splits(monkeypatch, split):
     _case(w["a"], w["b"], "bf16", f"split={split} bf16")
 
 
-@pytest.mark.parametrize("tile_n,stages", [(128, 4), (128, 6), (128, 8), (256, 3), (256, 4)])
-def test_tile_widths_and_stages(monkeypatch, tile_n, stages):
+# Every compiled kernel variant (tile_n, ring depth), on items shorter and
+# longer than the ring.
+SPMM_VARIANTS = [(128, 4), (128, 6), (128, 8), (256, 3), (256, 4)]
+
+
+@pytest.mark.parametrize("density", [0.1, 0.5])
+@pytest.mark.parametrize("tile_n,stages", SPMM_VARIANTS)
+def test_kernel_variants(monkeypatch, tile_n, stages, density):
     monkeypatch.setenv("BSP_SPMM_TILE_N", str(tile_n))
     monkeypatch.setenv("BSP_SPMM_STAGES", str(stages))
-    w = W.spmm_workload(2048, 2048, 512, 32, 32, 0.1, seed=12)
+    w = W.spmm_workload(2048, 2048, 512, 32, 32, density, seed=12)
     plan = capi.SpmmPlan(capi.Bsr(2048, 2048, 32, 32, w["a"].indptr, w["a"].indices), 512, "f32")
     info = plan.info()
     assert (info["tile_n"], info["stages"]) == (tile_n, stages)
     got = run_spmm(w["a"], w["b"], "f32", plan=plan)
     plan.close()
-    assert_parity(got, golden_spmm(w["a"], w["b"]), spmm_k_eff(w["a"]), f"tile_n={tile_n} stages={stages}")
+    assert_parity(got, golden_spmm(w["a"], w["b"]), spmm_k_eff(w["a"]),
+                  f"variant=({tile_n},{stages}) d={density}")
 
 
 @pytest.mark.parametrize("N", [32, 96, 160, 288, 384])
