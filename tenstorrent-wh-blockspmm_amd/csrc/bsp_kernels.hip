@@ -8,10 +8,8 @@
 //   result:    acc[4*i + j] is C[8*i + 4*q + j][lane % 32]
 // Both operands must therefore be contiguous along k in each lane.  A blocks
 // and X rows already are; a row-major dense operand (B of SpMM, Y of SDDMM) is
-// contiguous along n instead.  SpMM stages B in LDS as it lies in memory and
-// reads it with the LDS transpose read (ds_read_b64_tr_b16); SDDMM re-packs
-// row-major Y into k-pairs in LDS (dword (p, n) holds (Y[2p][n], Y[2p+1][n]))
-// and a lane gathers its 8 k-values with four dword reads.
+// contiguous along n instead: both kernels stage it in LDS as it lies in
+// memory and read it with the LDS transpose read (ds_read_b64_tr_b16).
 //
 // Reference semantics followed: block_spmm/inc/bsr_matrix.hpp:954-1000 (SpMM),
 // sparse_common/bsr_matrix.hpp:816-857 (SDDMM).
@@ -60,20 +58,6 @@ __device__ __forceinline__ T load_const(const T* ptr) {
     T out;
     __builtin_memcpy(&out, w, sizeof(T));
     return out;
-}
-
-// Packs rows k (r0) and k+1 (r1), 8 columns each, into 8 k-pair dwords in
-// column order.
-__device__ __forceinline__ void pack_pairs(const u32x4& r0, const u32x4& r1, u32x4& lo,
-                                           u32x4& hi) {
-    lo.x = (r0.x & 0xffffu) | (r1.x << 16);
-    lo.y = (r0.x >> 16) | (r1.x & 0xffff0000u);
-    lo.z = (r0.y & 0xffffu) | (r1.y << 16);
-    lo.w = (r0.y >> 16) | (r1.y & 0xffff0000u);
-    hi.x = (r0.z & 0xffffu) | (r1.z << 16);
-    hi.y = (r0.z >> 16) | (r1.z & 0xffff0000u);
-    hi.z = (r0.w & 0xffffu) | (r1.w << 16);
-    hi.w = (r0.w >> 16) | (r1.w & 0xffff0000u);
 }
 
 // ---------------------------------------------------------------------------
@@ -363,78 +347,219 @@ __global__ __launch_bounds__(256) void spmm_reduce_kernel(SpmmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// SDDMM.  Workgroup = one work item (up to `chunk` output sub-blocks sharing
-// the same 32 rows of X); its four waves take the item's entries round-robin
-// and each computes one 32x32 output sub-block at a time over the full K,
-// then applies the mask values and stores.  X rows are read straight into
-// A-operand registers (contiguous along k).  Y in BSP_COL_MAJOR (Y^T row-major,
-// e.g. K of Q*K^T) is read the same way; row-major Y goes through a
-// wave-private LDS k-pair stage.
-template <bool Y_COLMAJOR, bool OUT_BF16>
+// SDDMM.  Workgroup = one work item: a run of output sub-blocks (entries) of
+// one 32-row stripe, taken one entry at a time by all four waves, each over a
+// quarter of K: wave w takes the k-steps (32 deep) w, w+4, w+8, ...  The
+// partial 32x32 sums meet in LDS; wave w then adds the four partials of rows
+// 8w..8w+7, applies the mask values there and stores them.
+//
+// Operands go straight from global memory into MFMA registers: X rows and the
+// rows of Y^T (Y in BSP_COL_MAJOR, e.g. the key matrix of Q*K^T) are
+// contiguous along k.  Row-major Y is loaded as it lies (16 rows x 64 bytes
+// per instruction) into a wave-private LDS tile and read back with the LDS
+// transpose read, as in the SpMM kernel.  Each wave issues the loads of its
+// next entry before it multiplies the current one; when a wave's k-steps fit
+// in one register chunk (K <= 256) its X operands are loaded once per item.
+namespace sddmm_detail {
+
+constexpr int kKW = 2;  // k-steps per register chunk and wave
+
+// One unit of a wave's stream: up to kKW k-steps of one entry.  With X_KEEP
+// (K <= 256: every wave's k-steps fit one chunk) the X operands are loaded
+// once per item and the chunk carries only Y.
+template <bool X_KEEP>
+struct Chunk {
+    u32x4 b[kKW][2];   // Y operands (k-step j, half s), or raw row-major Y rows (i = 0, 1)
+    u32x4 a[kKW][2];   // X operands
+    uint32_t m[4];     // mask values (bf16 bits) of this wave's 4 rows, first chunk only
+};
+template <>
+struct Chunk<true> {
+    u32x4 b[kKW][2];
+    uint32_t m[4];
+};
+
+}  // namespace sddmm_detail
+
+template <bool Y_COLMAJOR, bool OUT_BF16, bool X_KEEP>
 __global__ __launch_bounds__(256) void sddmm_kernel(SddmmArgs p) {
-    constexpr int Y_LD = 40;  // dwords per LDS k-pair row (32 + 8 pad)
-    __shared__ __attribute__((aligned(16))) uint32_t sY[4][16 * Y_LD];
+    using namespace sddmm_detail;
+    __shared__ __attribute__((aligned(16))) float red[4][16 * 64];  // partial sums of one entry
+    __shared__ __attribute__((aligned(16))) uint8_t ytile[Y_COLMAJOR ? 1 : 4][2048];
 
-    const SddmmItem it = p.wgs[blockIdx.x];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const SddmmItem it = load_const(p.wgs + blockIdx.x);
+    const int n_e = it.e_end - it.e_begin;
+    if (n_e <= 0) return;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, q = lane >> 5;
+    const int KT = p.K >> 5;
+    const int nks = KT > wave ? (KT - wave + 3) >> 2 : 0;  // k-steps of this wave
+    // Chunks per entry and the unit count are the same for every wave (wave 0
+    // has the most k-steps), so all waves meet at the same barriers.
+    const int nks0 = (KT + 3) >> 2;
+    const int nch = X_KEEP ? 1 : (nks0 + kKW - 1) / kKW;
+    const int UW = n_e * nch;  // units (entry, chunk)
+
+    // The item's entry words, one entry per lane (an item holds at most 64
+    // entries), fetched once; entry eu's words are read back with readlane.
+    int32_t lane_col = 0;
+    int64_t lane_off = 0;
+    if (lane < n_e) {
+        lane_col = p.ent_col[it.e_begin + lane];
+        lane_off = p.ent_off[it.e_begin + lane];
+    }
+    auto entry_col = [&](int eu) { return __builtin_amdgcn_readlane(lane_col, eu); };
+    auto entry_off = [&](int eu) {
+        const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)lane_off, eu);
+        const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)lane_off >> 32), eu);
+        return (int64_t)(((uint64_t)hi << 32) | lo);
+    };
+
     const uint16_t* xlane = p.x + (int64_t)(it.x_row0 + l32) * p.ldx + 8 * q;
-    uint32_t* sw = sY[wave];
-    const int pr = lane >> 2, c8 = (lane & 3) * 8;  // row-major Y staging role
-
-    for (int e = it.e_begin + wave; e < it.e_end; e += 4) {
-        const int32_t ycol = p.ent_col[e];
-        const int64_t off = p.ent_off[e];
-        f32x16 acc;
+    auto load_x = [&](int c, u32x4 (&a)[kKW][2]) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+        for (int j = 0; j < kKW; ++j) {
+            const int kj = c * kKW + j;
+            if (kj < nks) {
+                const int k0 = (wave + 4 * kj) * 32;
+                a[j][0] = *(const u32x4*)(xlane + k0);
+                a[j][1] = *(const u32x4*)(xlane + k0 + 16);
+            }
+        }
+    };
+    auto load = [&](int u, Chunk<X_KEEP>& ch) {
+        const int eu = X_KEEP ? u : u / nch, c = u - eu * nch;
+        const int32_t ycol = entry_col(eu);
+        if constexpr (!X_KEEP) load_x(c, ch.a);
+#pragma unroll
+        for (int j = 0; j < kKW; ++j) {
+            const int kj = c * kKW + j;
+            if (kj < nks) {
+                const int k0 = (wave + 4 * kj) * 32;
+                if (Y_COLMAJOR) {
+                    const uint16_t* yl = p.y + (int64_t)(ycol + l32) * p.ldy + k0 + 8 * q;
+                    ch.b[j][0] = *(const u32x4*)yl;
+                    ch.b[j][1] = *(const u32x4*)(yl + 16);
+                } else {
+                    const uint16_t* yl = p.y + (int64_t)(k0 + (lane >> 2)) * p.ldy + ycol + 8 * (lane & 3);
+                    ch.b[j][0] = *(const u32x4*)yl;
+                    ch.b[j][1] = *(const u32x4*)(yl + 16 * p.ldy);
+                }
+            }
+        }
+        if (c == 0) {
+            const uint16_t* ml = p.mask + entry_off(eu) + (int64_t)(8 * wave + 4 * q) * p.ldo + l32;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) ch.m[j] = ml[j * p.ldo];
+        }
+    };
 
-        if (Y_COLMAJOR) {
-            const uint16_t* ylane = p.y + (int64_t)(ycol + l32) * p.ldy + 8 * q;
-            for (int k0 = 0; k0 < p.K; k0 += 32) {
-                const u32x4 a0 = *(const u32x4*)(xlane + k0);
-                const u32x4 a1 = *(const u32x4*)(xlane + k0 + 16);
-                const u32x4 b0 = *(const u32x4*)(ylane + k0);
-                const u32x4 b1 = *(const u32x4*)(ylane + k0 + 16);
+    // Row-major Y: LDS offsets of the transpose reads for k-step half s and
+    // 4-row group h (16-lane group g reads rows 16s + 8(g/2) + 4h .. +3 of
+    // columns 16(g%2) + i).
+    int ytr[2][2];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int g = lane >> 4, ll = lane & 15;
+            const int row = 16 * s2 + 8 * (g >> 1) + 4 * h + (ll >> 2);
+            const int col = 16 * (g & 1) + 4 * (ll & 3);
+            ytr[s2][h] = row * 64 + col * 2;
+        }
+
+    f32x16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+    u32x4 xa[kKW][2];
+    if constexpr (X_KEEP) load_x(0, xa);
+    uint32_t mcur[4] = {0u, 0u, 0u, 0u};
+
+    auto compute = [&](int u, Chunk<X_KEEP>& ch) {
+        const int eu = X_KEEP ? u : u / nch, c = u - eu * nch;
+        if (c == 0) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) mcur[j] = ch.m[j];
+        }
+#pragma unroll
+        for (int j = 0; j < kKW; ++j) {
+            const int kj = c * kKW + j;
+            if (kj < nks) {
+                u32x4 a0, a1;
+                if constexpr (X_KEEP) {
+                    a0 = xa[j][0];
+                    a1 = xa[j][1];
+                } else {
+                    a0 = ch.a[j][0];
+                    a1 = ch.a[j][1];
+                }
+                u32x4 b0, b1;
+                if (Y_COLMAJOR) {
+                    b0 = ch.b[j][0];
+                    b1 = ch.b[j][1];
+                } else {
+                    // Rows 16i + lane/4, 16-byte chunk lane%4: 64-byte rows.
+                    // One tile per wave: the LDS serves a wave's accesses in
+                    // order, so the next k-step's writes follow these reads.
+                    uint8_t* yt = ytile[wave];
+                    *(u32x4*)(yt + lane * 16) = ch.b[j][0];
+                    *(u32x4*)(yt + 1024 + lane * 16) = ch.b[j][1];
+                    const u32x4 l0 = spmm_detail::ld_tr_b16(yt + ytr[0][0]);
+                    const u32x4 h0 = spmm_detail::ld_tr_b16(yt + ytr[0][1]);
+                    const u32x4 l1 = spmm_detail::ld_tr_b16(yt + ytr[1][0]);
+                    const u32x4 h1 = spmm_detail::ld_tr_b16(yt + ytr[1][1]);
+                    b0 = u32x4{l0.x, l0.y, h0.x, h0.y};
+                    b1 = u32x4{l1.x, l1.y, h1.x, h1.y};
+                }
                 acc = mfma32(a0, b0, acc);
                 acc = mfma32(a1, b1, acc);
             }
-        } else {
-            const uint16_t* ysrc = p.y + (int64_t)(2 * pr) * p.ldy + ycol + c8;
-            for (int k0 = 0; k0 < p.K; k0 += 32) {
-                const u32x4 a0 = *(const u32x4*)(xlane + k0);
-                const u32x4 a1 = *(const u32x4*)(xlane + k0 + 16);
-                const u32x4 y0 = *(const u32x4*)(ysrc + (int64_t)k0 * p.ldy);
-                const u32x4 y1 = *(const u32x4*)(ysrc + (int64_t)(k0 + 1) * p.ldy);
-                u32x4 lo, hi;
-                pack_pairs(y0, y1, lo, hi);
-                // The previous k-step's reads of this wave-private stage were
-                // issued before these writes; LDS serves one wave in order.
-                *(u32x4*)&sw[pr * Y_LD + c8] = lo;
-                *(u32x4*)&sw[pr * Y_LD + c8 + 4] = hi;
-                __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-                for (int s = 0; s < 2; ++s) {
-                    const uint32_t* bp = &sw[(8 * s + 4 * q) * Y_LD + l32];
-                    u32x4 bv;
-                    bv.x = bp[0];
-                    bv.y = bp[Y_LD];
-                    bv.z = bp[2 * Y_LD];
-                    bv.w = bp[3 * Y_LD];
-                    acc = mfma32(s == 0 ? a0 : a1, bv, acc);
-                }
-                __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            }
         }
-
+        if (c == nch - 1) {
+            // Entry done: meet the other waves' partials, finish rows 8w..8w+7.
+            // The first barrier keeps this entry's writes behind every wave's
+            // reads of the previous entry; the waits before each barrier make
+            // the LDS accesses complete without a fence (a fence would also
+            // wait for the next unit's loads, which stay in flight).
+            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            spmm_detail::barrier_no_fence();
+            float* mine = red[wave];
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int64_t idx = off + (int64_t)(8 * (v >> 2) + 4 * q + (v & 3)) * p.ldo + l32;
-            const float val = acc[v] * bf16_to_f32(p.mask[idx]);
-            if (OUT_BF16)
-                ((uint16_t*)p.out)[idx] = f32_to_bf16_rne(val);
-            else
-                ((float*)p.out)[idx] = val;
+            for (int v = 0; v < 16; ++v) mine[v * 64 + lane] = acc[v];
+            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            spmm_detail::barrier_no_fence();
+            const int64_t off = entry_off(eu);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int v = 4 * wave + j;
+                float sum = 0.0f;
+#pragma unroll
+                for (int w2 = 0; w2 < 4; ++w2) sum += red[w2][v * 64 + lane];
+                const float val = sum * bf16_to_f32((uint16_t)mcur[j]);
+                const int64_t idx = off + (int64_t)(8 * wave + 4 * q + j) * p.ldo + l32;
+                if (OUT_BF16)
+                    ((uint16_t*)p.out)[idx] = f32_to_bf16_rne(val);
+                else
+                    ((float*)p.out)[idx] = val;
+            }
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+        }
+    };
+
+    // Unit u+1's loads are issued before unit u is multiplied; unrolled by
+    // two so that the two chunks keep their registers (a copy would wait for
+    // the loads).
+    Chunk<X_KEEP> c0, c1;
+    load(0, c0);
+    for (int u = 0; u < UW; u += 2) {
+        if (u + 1 < UW) load(u + 1, c1);
+        compute(u, c0);
+        if (u + 1 < UW) {
+            if (u + 2 < UW) load(u + 2, c0);
+            compute(u + 1, c1);
         }
     }
 }
@@ -469,19 +594,28 @@ hipError_t launch_spmm(const SpmmArgs& a, const SpmmVariant& v, bool out_bf16, i
     return hipErrorInvalidValue;
 }
 
+template <bool Y_COLMAJOR, bool OUT_BF16>
+static void launch_sddmm_t(const SddmmArgs& a, int grid, hipStream_t stream) {
+    // X operands stay in registers when every wave has at most two k-steps.
+    if (a.K <= 4 * 32 * sddmm_detail::kKW)
+        hipLaunchKernelGGL((sddmm_kernel<Y_COLMAJOR, OUT_BF16, true>), dim3(grid), dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL((sddmm_kernel<Y_COLMAJOR, OUT_BF16, false>), dim3(grid), dim3(256), 0, stream, a);
+}
+
 hipError_t launch_sddmm(const SddmmArgs& a, bool y_colmajor, bool out_bf16, int grid,
                         hipStream_t stream) {
     if (grid <= 0) return hipSuccess;
     if (y_colmajor) {
         if (out_bf16)
-            hipLaunchKernelGGL((sddmm_kernel<true, true>), dim3(grid), dim3(256), 0, stream, a);
+            launch_sddmm_t<true, true>(a, grid, stream);
         else
-            hipLaunchKernelGGL((sddmm_kernel<true, false>), dim3(grid), dim3(256), 0, stream, a);
+            launch_sddmm_t<true, false>(a, grid, stream);
     } else {
         if (out_bf16)
-            hipLaunchKernelGGL((sddmm_kernel<false, true>), dim3(grid), dim3(256), 0, stream, a);
+            launch_sddmm_t<false, true>(a, grid, stream);
         else
-            hipLaunchKernelGGL((sddmm_kernel<false, false>), dim3(grid), dim3(256), 0, stream, a);
+            launch_sddmm_t<false, false>(a, grid, stream);
     }
     return hipGetLastError();
 }

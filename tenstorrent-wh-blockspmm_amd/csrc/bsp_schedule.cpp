@@ -301,12 +301,13 @@ int build_sddmm_schedule(const bsp_bsr_desc* m, int64_t K, int num_cus, SddmmSch
         msg = "problem too large for int32 schedule fields";
         return BSP_ERR_UNSUPPORTED;
     }
-    // Entries per item: a multiple of 4 (one per wave), sized for about two
-    // workgroups per compute unit, between 4 and 32.
+    // Entries per item (all four waves work on each entry in turn): about two
+    // workgroups per compute unit, at most 4 (measured best for 1600-2700
+    // entries on 256 compute units).
     int64_t q = (total + 2 * num_cus - 1) / (2 * (int64_t)num_cus);
-    q = std::min<int64_t>(32, std::max<int64_t>(4, (q + 3) / 4 * 4));
+    q = std::min<int64_t>(4, std::max<int64_t>(1, q));
     q = env_int("BSP_SDDMM_CHUNK", q);
-    if (q < 1) q = 1;
+    q = std::min<int64_t>(64, std::max<int64_t>(1, q));  // the kernel holds an item's entries in one wave
     s.chunk = (int32_t)q;
 
     s.items.clear();
@@ -329,8 +330,7 @@ int build_sddmm_schedule(const bsp_bsr_desc* m, int64_t K, int num_cus, SddmmSch
         for (int32_t b = e0; b < e1; b += (int32_t)q) {
             const int32_t b1 = std::min<int32_t>(e1, b + (int32_t)q);
             s.items.push_back({(int32_t)(sr * kSub), b, b1, 0});
-            // Four waves share an item: its time is the longest wave's share.
-            cost.push_back((b1 - b + 3) / 4 + 1);
+            cost.push_back((b1 - b) + 1);
             s.max_item_entries = std::max<int32_t>(s.max_item_entries, b1 - b);
         }
     }
