@@ -167,6 +167,34 @@ def bench_sddmm(torch, capi, W, mask, x, y, y_layout, out_dtype, steps, warmup):
     return t, flops, nbytes
 
 
+def bench_attention(torch, capi, W, w, out_dtype, steps, warmup):
+    """Times the fused pair (bsp_attention) on the attention workload; bytes
+    are Q, K, V, the mask values, the index arrays and O (S never leaves the
+    chip)."""
+    m, q, k, v, d = w["mask"], w["q"], w["k"], w["v"], w["d"]
+    plan = capi.AttentionPlan(capi.Bsr(m.H, m.W, m.R, m.C, m.indptr, m.indices), d, out_dtype)
+    out_bytes = 4 if out_dtype == "f32" else 2
+    per_copy = m.data.nbytes + q.nbytes + k.nbytes + v.nbytes + m.H * d * out_bytes
+    ncopy = max(1, -(-ROTATE_BYTES // per_copy))
+    base = [dev_u16(torch, x) for x in (m.data, q, k, v)]
+    copies = []
+    for _ in range(ncopy):
+        do = torch.empty((m.H, d), dtype=torch.float32 if out_dtype == "f32" else torch.int16, device="cuda")
+        copies.append([x.clone() for x in base] + [do])
+
+    def launch(i, stream):
+        dm, dq, dk, dv, do = copies[i % ncopy]
+        plan.run(dm, dq, dk, dv, do, stream=stream)
+
+    t = Timer(torch, steps).run(launch, steps, warmup)
+    plan.close()
+    del copies
+    flops = W.sddmm_flops(m.nblocks, m.R, m.C, d) + W.spmm_flops(m.nblocks, m.R, m.C, d)
+    nbytes = (float(m.data.nbytes + q.nbytes + k.nbytes + v.nbytes) + 4.0 * (m.nblocks + m.nbrows + 1)
+              + float(m.H) * d * out_bytes)
+    return t, flops, nbytes
+
+
 def summarize(t, flops, nbytes, steps):
     """Per-launch figures from the graph replay (us, TFLOP/s, GB/s and the
     fractions of peak) plus the eager per-launch event figure."""
@@ -335,12 +363,14 @@ def main():
         t1, f1, b1 = bench_sddmm(torch, capi, W, m, w["q"], w["k"], capi.COL_MAJOR, "bf16", steps, warmup)
         a = W.BsrArrays(m.H, m.W, 32, 32, m.indptr, m.indices, m.data)
         t2, f2, b2, _, _ = bench_spmm(torch, capi, W, a, w["v"], "f32", steps, warmup)
+        t3, f3, b3 = bench_attention(torch, capi, W, w, "f32", steps, warmup)
         out["attention"] = {"workload": "seq 8192, d 128, 8 causal block bands + 1% global; S=mask(.)QK^T "
                                         "(bf16) then O=S*V (fp32)",
                             "nnzb": m.nblocks, "sddmm": summarize(t1, f1, b1, steps),
                             "spmm": summarize(t2, f2, b2, steps),
                             "pair_tflops": round((f1 + f2) / ((t1["launch_ms"] + t2["launch_ms"]) * 1e-3)
-                                                 / 1e12, 3)}
+                                                 / 1e12, 3),
+                            "fused": summarize(t3, f3, b3, steps)}
 
     if not only or "host" in only:
         # The blocking host-buffer entry point (the reference operator's shape):

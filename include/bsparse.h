@@ -89,7 +89,7 @@ typedef struct bsp_plan bsp_plan;
 
 /* Schedule summary of a plan (for tests and the bench report). */
 typedef struct bsp_plan_info {
-    int32_t kind;        /* 1 = SpMM, 2 = SDDMM */
+    int32_t kind;        /* 1 = SpMM, 2 = SDDMM, 3 = fused attention pair */
     int32_t tile_n;      /* SpMM: output columns per workgroup */
     int32_t n_tiles;     /* SpMM: N / tile_n */
     int32_t n_items;     /* work items (row pieces / mask-row chunks) */
@@ -148,6 +148,28 @@ int bsp_sddmm_plan_create(bsp_plan** plan, const bsp_bsr_desc* mask, int64_t K,
  * mask_vals: device, nblocks*R*C bf16.  out_vals: device, nblocks*R*C. */
 int bsp_sddmm(const bsp_plan* plan, const uint16_t* mask_vals, const uint16_t* x, int64_t ldx,
               const uint16_t* y, int64_t ldy, void* out_vals, void* stream);
+
+/* ---- fused block-sparse attention pair: O = S * V,
+ *      S = bf16(mask (.) (Q * K^T)) at the mask's blocks -------------------
+ * The reference has no fused operator; this is the pair of its two operators
+ * on one structure: SDDMMHostCodeFunctionPtr (block_sddmm/inc/host_code.hpp
+ * :104-115) with c = Q and d = K^T, its output cast to bf16 (the reference's
+ * output type), then HostCodeFunctionPtr (block_spmm/inc/host_code.hpp
+ * :165-177) with a = S and b = V.  S stays on the compute unit.  The result
+ * equals bsp_sddmm (y_layout BSP_COL_MAJOR with y = K, bf16 output) followed
+ * by bsp_spmm (a_vals = S, b = V) up to the fp32 summation order of O.
+ * mask: queries x keys (H x W), R and C multiples of 32; head_dim 32, 64 or
+ * 128. */
+int bsp_attention_plan_create(bsp_plan** plan, const bsp_bsr_desc* mask, int64_t head_dim,
+                              int out_dtype, int device);
+
+/* mask_vals: device, nblocks*R*C bf16.  q: queries x head_dim, k and v:
+ * keys x head_dim, all bf16 row-major (16-byte aligned, leading dimensions
+ * multiples of 8).  out: queries x head_dim row-major, fp32 or bf16 as
+ * planned; every element is written. */
+int bsp_attention(const bsp_plan* plan, const uint16_t* mask_vals, const uint16_t* q, int64_t ldq,
+                  const uint16_t* k, int64_t ldk, const uint16_t* v, int64_t ldv, void* out,
+                  int64_t ldo, void* stream);
 
 int bsp_plan_info_get(const bsp_plan* plan, bsp_plan_info* info);
 int bsp_plan_destroy(bsp_plan* plan);

@@ -77,6 +77,9 @@ SIGNATURES = {
     "bsp_spmm": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p]),
     "bsp_sddmm_plan_create": (c_int, [POINTER(c_void_p), _DESC_P, c_int64, c_int, c_int, c_int]),
     "bsp_sddmm": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p]),
+    "bsp_attention_plan_create": (c_int, [POINTER(c_void_p), _DESC_P, c_int64, c_int, c_int]),
+    "bsp_attention": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+                              c_void_p, c_int64, c_void_p]),
     "bsp_plan_info_get": (c_int, [c_void_p, _INFO_P]),
     "bsp_plan_destroy": (c_int, [c_void_p]),
     "bsp_spmm_schedule": (c_int, [_DESC_P, c_int64, c_int, _INFO_P, _I32P, _I32P, _I64P, _I32P]),
@@ -241,6 +244,24 @@ class SddmmPlan(_Plan):
             ldy = self.mask.W if self.y_layout == ROW_MAJOR else self.K
         check(load().bsp_sddmm(self.handle, _ptr(mask_vals), _ptr(x), ldx or self.K, _ptr(y), ldy,
                                _ptr(out_vals), stream))
+
+
+class AttentionPlan(_Plan):
+    """Plan for the fused pair O = bf16(mask (.) (Q * K^T)) * V on the mask's
+    structure (queries x keys), head dimension 32, 64 or 128."""
+
+    def __init__(self, mask: Bsr, head_dim: int, out_dtype="f32", device: int = 0):
+        super().__init__()
+        self.mask, self.d, self.out_dtype = mask, int(head_dim), _dtype_code(out_dtype)
+        dsc = mask.desc()
+        check(load().bsp_attention_plan_create(ctypes.byref(self._h), ctypes.byref(dsc), self.d,
+                                               self.out_dtype, device))
+
+    def run(self, mask_vals, q, k, v, out, ldq: Optional[int] = None, ldk: Optional[int] = None,
+            ldv: Optional[int] = None, ldo: Optional[int] = None, stream: Optional[int] = None) -> None:
+        d = self.d
+        check(load().bsp_attention(self.handle, _ptr(mask_vals), _ptr(q), ldq or d, _ptr(k), ldk or d,
+                                   _ptr(v), ldv or d, _ptr(out), ldo or d, stream))
 
 
 def _schedule(fn_name: str, bsr: Bsr, n: int, num_cus: int) -> dict:

@@ -13,7 +13,7 @@
 #include "bsparse.h"
 
 struct bsp_plan {
-    int kind = 0;  // 1 SpMM, 2 SDDMM
+    int kind = 0;  // 1 SpMM, 2 SDDMM, 3 fused attention pair
     int device = 0;
     int out_dtype = BSP_DTYPE_F32;
     int layout = BSP_ROW_MAJOR;
@@ -193,16 +193,14 @@ int bsp_sddmm_schedule(const bsp_bsr_desc* m, int64_t K, int num_cus, bsp_plan_i
     return BSP_OK;
 }
 
-int bsp_spmm_plan_create(bsp_plan** out, const bsp_bsr_desc* a, int64_t N, int b_layout,
-                         int out_dtype, int device) {
-    if (!out) return fail(BSP_ERR_INVALID_ARGUMENT, "plan output pointer is null");
-    *out = nullptr;
-    if (out_dtype != BSP_DTYPE_F32 && out_dtype != BSP_DTYPE_BF16)
-        return fail(BSP_ERR_INVALID_ARGUMENT, "out_dtype must be BSP_DTYPE_F32 or BSP_DTYPE_BF16");
-    if (b_layout != BSP_ROW_MAJOR && b_layout != BSP_COL_MAJOR)
-        return fail(BSP_ERR_INVALID_ARGUMENT, "b_layout must be BSP_ROW_MAJOR or BSP_COL_MAJOR");
-    if (b_layout != BSP_ROW_MAJOR)
-        return fail(BSP_ERR_UNSUPPORTED, "SpMM takes B row-major (the reference's layout)");
+}  // extern "C"
+
+namespace {
+
+// Plan of an SpMM-shaped launch (SpMM, or the fused attention pair with the
+// mask as A and N = head dimension): schedule, upload, split-row scratch.
+int make_spmm_plan(bsp_plan** out, int kind, const bsp_bsr_desc* a, int64_t N, int out_dtype, int device,
+                   int force_tile_n) {
     std::string msg;
     int st = bsp::validate_bsr(a, msg);
     if (st != BSP_OK) return fail(st, msg);
@@ -212,16 +210,16 @@ int bsp_spmm_plan_create(bsp_plan** out, const bsp_bsr_desc* a, int64_t N, int b
     st = device_cus(device, &cus);
     if (st != BSP_OK) return st;
     bsp::SpmmSchedule s;
-    st = bsp::build_spmm_schedule(a, N, cus, s, msg);
+    st = bsp::build_spmm_schedule(a, N, cus, s, msg, force_tile_n);
     if (st != BSP_OK) return fail(st, msg);
 
     DeviceGuard g(device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     bsp_plan* p = new bsp_plan();
-    p->kind = 1;
+    p->kind = kind;
     p->device = device;
     p->out_dtype = out_dtype;
-    p->layout = b_layout;
+    p->layout = BSP_ROW_MAJOR;
     p->M = a->H;
     p->K = a->W;
     p->N = N;
@@ -229,6 +227,10 @@ int bsp_spmm_plan_create(bsp_plan** out, const bsp_bsr_desc* a, int64_t N, int b
     p->C = a->C;
     p->nblocks = a->nblocks;
     fill_info_spmm(s, &p->info);
+    if (kind == 3) {
+        p->info.kind = 3;
+        p->info.stages = bsp::kAttentionStages;
+    }
     hipError_t e = upload((bsp::SpmmWg**)&p->d_wgs, bsp::spmm_wg_records(s));
     if (e == hipSuccess) e = upload(&p->d_ent_off, bsp::spmm_packed_entries(s));
     if (e == hipSuccess) e = upload(&p->d_splits, bsp::spmm_splits(s));
@@ -240,10 +242,46 @@ int bsp_spmm_plan_create(bsp_plan** out, const bsp_bsr_desc* a, int64_t N, int b
     if (e != hipSuccess) {
         free_plan_buffers(p);
         delete p;
-        return hip_fail(e, "SpMM plan upload");
+        return hip_fail(e, kind == 3 ? "attention plan upload" : "SpMM plan upload");
     }
     *out = p;
     return BSP_OK;
+}
+
+// Kernel arguments of an SpMM-shaped plan.
+bsp::SpmmArgs spmm_args(const bsp_plan* p, const uint16_t* a_vals, const uint16_t* b, int64_t ldb, void* c,
+                        int64_t ldc) {
+    bsp::SpmmArgs args{};
+    args.a = a_vals;
+    args.b = b;
+    args.c = c;
+    args.wgs = (const bsp::SpmmWg*)p->d_wgs;
+    args.ents = p->d_ent_off;
+    args.splits = p->d_splits;
+    args.ws = p->d_ws;
+    args.ldb = ldb;
+    args.ldc = ldc;
+    args.lda = (int32_t)p->C;
+    args.n_tiles = p->info.n_tiles;
+    args.N = (int32_t)p->N;
+    return args;
+}
+
+}  // namespace
+
+extern "C" {
+
+int bsp_spmm_plan_create(bsp_plan** out, const bsp_bsr_desc* a, int64_t N, int b_layout,
+                         int out_dtype, int device) {
+    if (!out) return fail(BSP_ERR_INVALID_ARGUMENT, "plan output pointer is null");
+    *out = nullptr;
+    if (out_dtype != BSP_DTYPE_F32 && out_dtype != BSP_DTYPE_BF16)
+        return fail(BSP_ERR_INVALID_ARGUMENT, "out_dtype must be BSP_DTYPE_F32 or BSP_DTYPE_BF16");
+    if (b_layout != BSP_ROW_MAJOR && b_layout != BSP_COL_MAJOR)
+        return fail(BSP_ERR_INVALID_ARGUMENT, "b_layout must be BSP_ROW_MAJOR or BSP_COL_MAJOR");
+    if (b_layout != BSP_ROW_MAJOR)
+        return fail(BSP_ERR_UNSUPPORTED, "SpMM takes B row-major (the reference's layout)");
+    return make_spmm_plan(out, 1, a, N, out_dtype, device, 0);
 }
 
 int bsp_spmm(const bsp_plan* p, const uint16_t* a_vals, const uint16_t* b, int64_t ldb, void* c,
@@ -259,23 +297,51 @@ int bsp_spmm(const bsp_plan* p, const uint16_t* a_vals, const uint16_t* b, int64
     if (((uintptr_t)c % esz) != 0) return fail(BSP_ERR_INVALID_ARGUMENT, "C is misaligned");
     DeviceGuard g(p->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
-    bsp::SpmmArgs args{};
-    args.a = a_vals;
-    args.b = b;
-    args.c = c;
-    args.wgs = (const bsp::SpmmWg*)p->d_wgs;
-    args.ents = p->d_ent_off;
-    args.splits = p->d_splits;
-    args.ws = p->d_ws;
-    args.ldb = ldb;
-    args.ldc = ldc;
-    args.lda = (int32_t)p->C;
-    args.n_tiles = p->info.n_tiles;
-    args.N = (int32_t)p->N;
+    const bsp::SpmmArgs args = spmm_args(p, a_vals, b, ldb, c, ldc);
     const bsp::SpmmVariant v{p->info.tile_n, p->info.stages};
     hipError_t e = bsp::launch_spmm(args, v, p->out_dtype == BSP_DTYPE_BF16, p->info.grid, p->info.n_split_rows,
                                     (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "SpMM launch");
+    return BSP_OK;
+}
+
+int bsp_attention_plan_create(bsp_plan** out, const bsp_bsr_desc* mask, int64_t head_dim, int out_dtype,
+                              int device) {
+    if (!out) return fail(BSP_ERR_INVALID_ARGUMENT, "plan output pointer is null");
+    *out = nullptr;
+    if (out_dtype != BSP_DTYPE_F32 && out_dtype != BSP_DTYPE_BF16)
+        return fail(BSP_ERR_INVALID_ARGUMENT, "out_dtype must be BSP_DTYPE_F32 or BSP_DTYPE_BF16");
+    if (!bsp::attention_head_dim_supported(head_dim))
+        return fail(BSP_ERR_UNSUPPORTED, "head_dim must be 32, 64 or 128");
+    return make_spmm_plan(out, 3, mask, head_dim, out_dtype, device, bsp::kAttentionTileN);
+}
+
+int bsp_attention(const bsp_plan* p, const uint16_t* mask_vals, const uint16_t* q, int64_t ldq,
+                  const uint16_t* k, int64_t ldk, const uint16_t* v, int64_t ldv, void* out, int64_t ldo,
+                  void* stream) {
+    if (!p || p->kind != 3) return fail(BSP_ERR_INVALID_ARGUMENT, "not an attention plan");
+    if (!q || !k || !v || !out || (p->nblocks > 0 && !mask_vals))
+        return fail(BSP_ERR_INVALID_ARGUMENT, "null device pointer");
+    const int64_t d = p->N;
+    if (ldq < d || ldk < d || ldv < d || ldo < d)
+        return fail(BSP_ERR_INVALID_ARGUMENT, "leading dimensions must be >= head_dim");
+    if (ldq % 8 || ldk % 8 || ldv % 8)
+        return fail(BSP_ERR_INVALID_ARGUMENT, "ldq, ldk and ldv must be multiples of 8");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || (mask_vals && !aligned16(mask_vals)))
+        return fail(BSP_ERR_INVALID_ARGUMENT, "mask values, Q, K and V must be 16-byte aligned");
+    const size_t esz = p->out_dtype == BSP_DTYPE_BF16 ? 2 : 4;
+    if (((uintptr_t)out % esz) != 0) return fail(BSP_ERR_INVALID_ARGUMENT, "output is misaligned");
+    DeviceGuard g(p->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    bsp::AttentionArgs args{};
+    args.s = spmm_args(p, mask_vals, v, ldv, out, ldo);
+    args.q = q;
+    args.k = k;
+    args.ldq = ldq;
+    args.ldk = ldk;
+    hipError_t e = bsp::launch_attention(args, (int)d, p->out_dtype == BSP_DTYPE_BF16, p->info.grid,
+                                         p->info.n_split_rows, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "attention launch");
     return BSP_OK;
 }
 

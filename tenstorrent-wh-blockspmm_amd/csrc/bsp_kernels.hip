@@ -25,11 +25,18 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// fp32 -> bf16 with round-to-nearest-even: gfx950's v_cvt_pk_bf16_f32, which
+// converts two values per instruction.
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
+// Two values to packed bf16 (lo in bits 0-15).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
@@ -145,6 +152,14 @@ __device__ __forceinline__ u32x4 ld_tr_b16(const uint8_t* lds) {
 
 }  // namespace spmm_detail
 
+// Output stores are non-temporal: the output is written once and not read by
+// the kernel, so it should not displace the operands from the caches
+// (measured on the 1% SpMM sweep case: 5.5 -> 4.3 us per launch).
+template <typename T>
+__device__ __forceinline__ void store_out(T* p, T v) {
+    __builtin_nontemporal_store(v, p);
+}
+
 // Stores the accumulators of one 32 x TN tile (columns past N skipped).
 template <int NTW, bool OUT_BF16>
 __device__ __forceinline__ void spmm_store_tile(const SpmmArgs& p, const f32x16 (&acc)[NTW], int64_t row0,
@@ -157,131 +172,40 @@ __device__ __forceinline__ void spmm_store_tile(const SpmmArgs& p, const f32x16 
         for (int v = 0; v < 16; ++v) {
             const int64_t row = row0 + 8 * (v >> 2) + 4 * q + (v & 3);
             if (OUT_BF16)
-                ((uint16_t*)p.c)[row * p.ldc + col] = f32_to_bf16_rne(acc[nt][v]);
+                store_out(&((uint16_t*)p.c)[row * p.ldc + col], f32_to_bf16_rne(acc[nt][v]));
             else
-                ((float*)p.c)[row * p.ldc + col] = acc[nt][v];
+                store_out(&((float*)p.c)[row * p.ldc + col], acc[nt][v]);
         }
     }
 }
 
-template <int NTW, int S, bool OUT_BF16>
-__global__ __launch_bounds__(256) void spmm_kernel(SpmmArgs p) {
-    using namespace spmm_detail;
-    constexpr int TN = 128 * NTW;
-    constexpr int ROW_BYTES = 2 * TN;
-    constexpr int B_BYTES = 32 * ROW_BYTES;
-    constexpr int BI = B_BYTES / 1024 / 4;  // B wave-instructions per wave per step (= 2*NTW)
-    constexpr int PER = BI + 1;              // loads per wave per step (B + a half-wave of A)
-    constexpr int B_RING = S * kA_BYTES;     // A ring first, then the B ring
+namespace spmm_detail {
+
+// Runs the LDS ring of an SpMM-shaped kernel over n entries.  Entry e lives
+// in ring stage e % S; issue(e, stage) issues its PER loads per wave,
+// read(stage, ops) reads its operands into registers, multiply(ops)
+// accumulates.  Entries 0..S-2 are issued first; entry S-1 goes into the
+// still unused last stage once entry 0 has landed.  Iteration k multiplies
+// entry k from registers, waits for entry k+1 to land (the loads issued after
+// it are those of entries k+2..k+S-1), and after the barrier (every wave holds
+// entry k's operands in registers, so stage k % S is free) issues entry k+S
+// into stage k % S and reads entry k+1's operands, whose LDS latency then
+// overlaps the next multiply.  landed() runs once entry 0 (and every load
+// issued before it) has landed and is visible to all waves.
+template <int S, int PER, class Ops, class Issue, class Read, class Multiply, class Landed>
+__device__ __forceinline__ void run_ring(int n, Issue&& issue, Read&& read, Multiply&& multiply,
+                                         Landed&& landed) {
     static_assert(PER * (S - 2) < 64, "vmcnt budget");
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[S * (kA_BYTES + B_BYTES)];
-
-    const SpmmWg it = load_const(p.wgs + blockIdx.x);
-    if (it.row < 0) return;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave
-    const int l32 = lane & 31, q = lane >> 5;
-    const int n0 = it.tile * TN;
-    const uint32_t lds0 = lds_address(smem);
-
-    // Loads of one entry, per wave: lanes 0-31 fetch A segment `wave` (lane
-    // 8*j + i loads A[8*wave + i][8*j .. +7]) and BI wave-wide 1 KB pieces of
-    // the swizzled B slice.
-    const int a_goff = (8 * wave + (lane & 7)) * p.lda + 8 * ((lane & 31) >> 3);
-    const uint32_t a_lds = lds0 + wave * 512;
-    const uint32_t b_lds = lds0 + B_RING + wave * BI * 1024;
-    int64_t b_goff[BI];
-#pragma unroll
-    for (int j = 0; j < BI; ++j) {
-        const int byte = (wave * BI + j) * 1024 + lane * 16;
-        const int r = byte / ROW_BYTES;
-        const int slot = (byte % ROW_BYTES) / 16;
-        // Columns past N (a partial last tile) read a valid chunk; they are not stored.
-        const int col = min(n0 + 8 * (slot ^ (4 * (r & 3))), p.N - 8);
-        b_goff[j] = (int64_t)r * p.ldb + col;
-    }
-
-    // Entry words: low 32 bits = first row of B, high 32 bits = A offset / 32.
-    const int e0 = it.e_begin, n = it.e_end - it.e_begin;
-    const uint32_t* words = (const uint32_t*)(p.ents + e0);
-    // Issues the PER loads of one entry into ring stage `stage`.
-    auto issue = [&](int e, int stage) {
-        const uint32_t bw = load_const(words + 2 * e);
-        const uint32_t aw = load_const(words + 2 * e + 1);
-        if (lane < 32) gl_lds16(p.a + (int64_t)aw * 32 + a_goff, a_lds + stage * kA_BYTES);
-        const uint16_t* bpan = p.b + (int64_t)bw * p.ldb;
-#pragma unroll
-        for (int j = 0; j < BI; ++j) gl_lds16(bpan + b_goff[j], b_lds + stage * B_BYTES + j * 1024);
-    };
-
-    // Per-lane LDS offsets of the operand reads (ring-stage relative).
-    const int a_rd = (l32 >> 3) * 512 + (8 * q + (l32 & 7)) * 16;  // + s * 256
-    int b_rd[2][2][NTW];         // [k-step][half][tile]
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int nt = 0; nt < NTW; ++nt) {
-                const int g = lane >> 4;
-                const int r = 16 * s2 + 8 * (g >> 1) + 4 * h + ((lane & 15) >> 2);
-                const int col = wave * (NTW * 32) + nt * 32 + 16 * (g & 1) + 4 * (lane & 3);
-                const int c = col >> 3;
-                b_rd[s2][h][nt] = r * ROW_BYTES + 16 * (c ^ (4 * (r & 3))) + 2 * (col & 7);
-            }
-
-    f32x16 acc[NTW];
-#pragma unroll
-    for (int i = 0; i < NTW; ++i)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
-
-    // Operands of one entry in registers: A of both k-steps and the B
-    // operands of every tile.  The LDS reads of entry k+1 are issued right
-    // after entry k's MFMAs, so their latency overlaps the MFMAs, the wait for
-    // the next stage and the barrier.
-    struct Operands {
-        u32x4 a[2];
-        u32x4 b[2][NTW];
-    };
-    auto read_operands = [&](int stage, Operands& o) {
-        const uint8_t* as = smem + stage * kA_BYTES;
-        const uint8_t* bs = smem + B_RING + stage * B_BYTES;
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-            o.a[s2] = *(const u32x4*)(as + s2 * 256 + a_rd);
-#pragma unroll
-            for (int nt = 0; nt < NTW; ++nt) {
-                const u32x4 lo = ld_tr_b16(bs + b_rd[s2][0][nt]);
-                const u32x4 hi = ld_tr_b16(bs + b_rd[s2][1][nt]);
-                o.b[s2][nt] = u32x4{lo.x, lo.y, hi.x, hi.y};
-            }
-        }
-    };
-    auto multiply = [&](const Operands& o) {
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-            for (int nt = 0; nt < NTW; ++nt) acc[nt] = mfma32(o.a[s2], o.b[s2][nt], acc[nt]);
-    };
-
-    // Entry e lives in ring stage e % S.  Entries 0..S-2 are issued first;
-    // entry S-1 goes into the still unused last stage once entry 0 has landed.
-    // Iteration k multiplies entry k from registers, waits for entry k+1 to
-    // land (the loads issued after it are those of entries k+2..k+S-1), and
-    // after the barrier (every wave holds entry k's operands in registers, so
-    // stage k % S is free) issues entry k+S into stage k % S and reads entry
-    // k+1's operands.
 #pragma unroll
     for (int e = 0; e < S - 1; ++e)
         if (e < n) issue(e, e);
-    Operands cur;
+    Ops cur;
     if (n > 0) {
         wait_stages<PER, S - 2>(n - 1);  // entry 0 landed
         barrier_no_fence();
+        landed();
         if (S - 1 < n) issue(S - 1, S - 1);
-        read_operands(0, cur);
+        read(0, cur);
     }
     int k = 0;
     int stage = 0;  // stage of entry k
@@ -295,7 +219,7 @@ __global__ __launch_bounds__(256) void spmm_kernel(SpmmArgs p) {
         barrier_no_fence();
         if (k + S < n) issue(k + S, stage);
         stage = stage == S - 1 ? 0 : stage + 1;
-        read_operands(stage, cur);
+        read(stage, cur);
     }
     // Tail: every entry is issued; fewer are in flight.
     for (; k < n; ++k) {
@@ -304,13 +228,77 @@ __global__ __launch_bounds__(256) void spmm_kernel(SpmmArgs p) {
             wait_stages<PER, S - 2>(n - 2 - k);  // entry k+1 landed
             barrier_no_fence();
             stage = stage == S - 1 ? 0 : stage + 1;
-            read_operands(stage, cur);
+            read(stage, cur);
         }
     }
+}
 
+// The 32 x TN slice of row-major B (rows brow..brow+31, columns n0..) in LDS:
+// row k at k*2*TN bytes, its 16-byte chunk c at slot c ^ 4*(k % 4).  Each of
+// the four waves loads BI = TN/64 pieces of 1 KB.
+template <int NTW>
+struct BSlice {
+    static constexpr int TN = 128 * NTW;
+    static constexpr int ROW_BYTES = 2 * TN;
+    static constexpr int BYTES = 32 * ROW_BYTES;
+    static constexpr int BI = BYTES / 1024 / 4;
+    int64_t goff[BI];     // element offsets of this lane's chunks from the slice's first row
+    int rd[2][2][NTW];    // LDS offsets of the transpose reads [k-step][4-row group][tile]
+
+    // key_major: the rows read by the B operand of k-step s2, lane half q,
+    // 4-row group h are 16*s2 + 8*q + 4*h (the MFMA's own order) or, with
+    // permuted = true, 16*s2 + 8*h + 4*q (the order in which a 32x32 MFMA
+    // result holds its rows, for an A operand built from a result).
+    __device__ __forceinline__ BSlice(int wave, int lane, int n0, int N, int64_t ldb, bool permuted) {
+#pragma unroll
+        for (int j = 0; j < BI; ++j) {
+            const int byte = (wave * BI + j) * 1024 + lane * 16;
+            const int r = byte / ROW_BYTES;
+            const int slot = (byte % ROW_BYTES) / 16;
+            // Columns past N (a partial last tile) read a valid chunk; they are not stored.
+            const int col = min(n0 + 8 * (slot ^ (4 * (r & 3))), N - 8);
+            goff[j] = (int64_t)r * ldb + col;
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int nt = 0; nt < NTW; ++nt) {
+                    const int g = lane >> 4;
+                    const int r = 16 * s2 + (permuted ? 8 * h + 4 * (g >> 1) : 8 * (g >> 1) + 4 * h) +
+                                  ((lane & 15) >> 2);
+                    const int col = wave * (NTW * 32) + nt * 32 + 16 * (g & 1) + 4 * (lane & 3);
+                    const int c = col >> 3;
+                    rd[s2][h][nt] = r * ROW_BYTES + 16 * (c ^ (4 * (r & 3))) + 2 * (col & 7);
+                }
+    }
+    __device__ __forceinline__ void issue(const uint16_t* b, int64_t ldb, uint32_t brow, uint32_t lds_wave) const {
+        const uint16_t* bpan = b + (int64_t)brow * ldb;
+#pragma unroll
+        for (int j = 0; j < BI; ++j) gl_lds16(bpan + goff[j], lds_wave + j * 1024);
+    }
+    __device__ __forceinline__ void read(const uint8_t* bs, u32x4 (&o)[2][NTW]) const {
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int nt = 0; nt < NTW; ++nt) {
+                const u32x4 lo = ld_tr_b16(bs + rd[s2][0][nt]);
+                const u32x4 hi = ld_tr_b16(bs + rd[s2][1][nt]);
+                o[s2][nt] = u32x4{lo.x, lo.y, hi.x, hi.y};
+            }
+    }
+};
+
+}  // namespace spmm_detail
+
+// Ends a work item: a piece of a split row leaves its partial in scratch
+// (spmm_reduce_kernel adds the pieces in order after this launch); a whole
+// row stores its tile.
+template <int NTW, bool OUT_BF16>
+__device__ __forceinline__ void spmm_finish(const SpmmArgs& p, const SpmmWg& it, const f32x16 (&acc)[NTW], int tid) {
+    const int lane = tid & 63, wave = tid >> 6;
     if (it.slot >= 0) {
-        // Piece of a split row: the partial goes to scratch; spmm_reduce_kernel
-        // adds the pieces in order after this launch.
         constexpr int PF = NTW * 16 * 256;
         float* mine = p.ws + ((int64_t)it.slot * p.n_tiles + it.tile) * PF;
 #pragma unroll
@@ -319,7 +307,193 @@ __global__ __launch_bounds__(256) void spmm_kernel(SpmmArgs p) {
             for (int v = 0; v < 16; ++v) mine[(nt * 16 + v) * 256 + tid] = acc[nt][v];
         return;
     }
-    spmm_store_tile<NTW, OUT_BF16>(p, acc, (int64_t)it.row * 32, n0, wave, l32, q);
+    spmm_store_tile<NTW, OUT_BF16>(p, acc, (int64_t)it.row * 32, it.tile * 128 * NTW, wave, lane & 31, lane >> 5);
+}
+
+template <int NTW, int S, bool OUT_BF16>
+__global__ __launch_bounds__(256) void spmm_kernel(SpmmArgs p) {
+    using namespace spmm_detail;
+    using Slice = BSlice<NTW>;
+    constexpr int PER = Slice::BI + 1;          // loads per wave per entry (B + a half-wave of A)
+    constexpr int B_RING = S * kA_BYTES;         // A ring first, then the B ring
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[S * (kA_BYTES + Slice::BYTES)];
+
+    const SpmmWg it = load_const(p.wgs + blockIdx.x);
+    if (it.row < 0) return;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave
+    const int l32 = lane & 31, q = lane >> 5;
+    const uint32_t lds0 = lds_address(smem);
+    const Slice bsl(wave, lane, it.tile * Slice::TN, p.N, p.ldb, false);
+
+    // Loads of one entry, per wave: lanes 0-31 fetch A segment `wave` (lane
+    // 8*j + i loads A[8*wave + i][8*j .. +7]) and the wave's pieces of the B slice.
+    const int a_goff = (8 * wave + (lane & 7)) * p.lda + 8 * ((lane & 31) >> 3);
+    const uint32_t a_lds = lds0 + wave * 512;
+    const uint32_t b_lds = lds0 + B_RING + wave * Slice::BI * 1024;
+    // Entry words: low 32 bits = first row of B, high 32 bits = A offset / 32.
+    const uint32_t* words = (const uint32_t*)(p.ents + it.e_begin);
+    auto issue = [&](int e, int stage) {
+        const uint32_t bw = load_const(words + 2 * e);
+        const uint32_t aw = load_const(words + 2 * e + 1);
+        if (lane < 32) gl_lds16(p.a + (int64_t)aw * 32 + a_goff, a_lds + stage * kA_BYTES);
+        bsl.issue(p.b, p.ldb, bw, b_lds + stage * Slice::BYTES);
+    };
+
+    const int a_rd = (l32 >> 3) * 512 + (8 * q + (l32 & 7)) * 16;  // + s * 256
+    f32x16 acc[NTW];
+#pragma unroll
+    for (int i = 0; i < NTW; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
+
+    struct Operands {
+        u32x4 a[2];
+        u32x4 b[2][NTW];
+    };
+    run_ring<S, PER, Operands>(
+        it.e_end - it.e_begin, issue,
+        [&](int stage, Operands& o) {
+            const uint8_t* as = smem + stage * kA_BYTES;
+            o.a[0] = *(const u32x4*)(as + a_rd);
+            o.a[1] = *(const u32x4*)(as + 256 + a_rd);
+            bsl.read(smem + B_RING + stage * Slice::BYTES, o.b);
+        },
+        [&](const Operands& o) {
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+                for (int nt = 0; nt < NTW; ++nt) acc[nt] = mfma32(o.a[s2], o.b[s2][nt], acc[nt]);
+        },
+        [] {});
+    spmm_finish<NTW, OUT_BF16>(p, it, acc, tid);
+}
+
+// ---------------------------------------------------------------------------
+// Block-sparse attention pair, fused: O = S * V with S = bf16(mask (.) (Q*K^T))
+// at the mask's blocks, S never leaving the compute unit.  Same schedule and
+// ring as the SpMM (the mask plays A, V plays B, one 128-column tile); each
+// ring stage also carries the entry's 32 x DK block of K.  Every wave
+// computes the whole 32x32 S^T = K_blk * Q^T of its entry from LDS (Q^T of the
+// stripe stays in registers), applies the mask and rounds to bf16, and uses
+// the result directly as the A operand of O += S * V: the result holds, per
+// lane, keys 8i + 4q + j of one query row, so the B operand reads V's rows in
+// that order.  Numerically the same as bsp_sddmm (column-major Y = K, bf16
+// output) followed by bsp_spmm with the same structure.
+template <int DK, int S, bool OUT_BF16>
+__global__ __launch_bounds__(256) void attention_kernel(AttentionArgs pa) {
+    using namespace spmm_detail;
+    using Slice = BSlice<1>;
+    const SpmmArgs& p = pa.s;
+    constexpr int K_BYTES = 64 * DK;              // 32 keys x DK bf16
+    constexpr int K_LANES = DK >= 64 ? 64 : 32;    // lanes per K load instruction
+    constexpr int KI = K_BYTES / 4 / (16 * K_LANES);  // K load instructions per wave
+    constexpr int PER = 1 + KI + Slice::BI;
+    constexpr int K_RING = S * kA_BYTES;
+    constexpr int B_RING = K_RING + S * K_BYTES;
+    constexpr int Q_AREA = B_RING + S * Slice::BYTES;
+    static_assert(KI >= 1 && DK % 32 == 0 && DK <= 128, "head dimension");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[Q_AREA + K_BYTES];
+
+    const SpmmWg it = load_const(p.wgs + blockIdx.x);
+    if (it.row < 0) return;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31, q = lane >> 5;
+    const uint32_t lds0 = lds_address(smem);
+    const Slice bsl(wave, lane, 0, p.N, p.ldb, true);
+
+    // K blocks and the stripe's Q rows in LDS as 16-byte chunks (c, row r) at
+    // (32c + r) * 16, so that the operand of step s of row l32 (chunk 2s + q)
+    // is one conflict-free ds_read_b128.  Wave w loads chunks [w*DK, (w+1)*DK).
+    int64_t k_goff[KI];
+    int64_t q_goff[KI];
+#pragma unroll
+    for (int j = 0; j < KI; ++j) {
+        const int ci = wave * DK + j * K_LANES + (lane & (K_LANES - 1));
+        k_goff[j] = (int64_t)(ci & 31) * pa.ldk + 8 * (ci >> 5);
+        q_goff[j] = (int64_t)(ci & 31) * pa.ldq + 8 * (ci >> 5);
+    }
+    const int n = it.e_end - it.e_begin;
+    // Q of the stripe goes through the same DMA path ahead of the ring, so it
+    // has landed once entry 0 has; its operands are then read from LDS (plain
+    // global loads here would be waited for inside the loop by the compiler,
+    // which cannot see that they completed, draining the ring every entry).
+    if (n > 0) {
+        const uint16_t* qrow = pa.q + (int64_t)it.row * 32 * pa.ldq;
+#pragma unroll
+        for (int j = 0; j < KI; ++j)
+            if (lane < K_LANES) gl_lds16(qrow + q_goff[j], lds0 + Q_AREA + wave * DK * 16 + j * K_LANES * 16);
+    }
+    // Q^T operands of the stripe: lane (query l32, half q) holds
+    // Q[row][16s + 8q .. +7] for every 16-deep step s of the head dimension.
+    u32x4 qv[DK / 16];
+    const int a_goff = (8 * wave + (lane & 7)) * p.lda + 8 * ((lane & 31) >> 3);
+    const uint32_t a_lds = lds0 + wave * 512;
+    const uint32_t k_lds = lds0 + K_RING + wave * DK * 16;
+    const uint32_t b_lds = lds0 + B_RING + wave * Slice::BI * 1024;
+    const uint32_t* words = (const uint32_t*)(p.ents + it.e_begin);
+    auto issue = [&](int e, int stage) {
+        const uint32_t bw = load_const(words + 2 * e);  // first key of the block
+        const uint32_t aw = load_const(words + 2 * e + 1);
+        if (lane < 32) gl_lds16(p.a + (int64_t)aw * 32 + a_goff, a_lds + stage * kA_BYTES);
+        const uint16_t* kblk = pa.k + (int64_t)bw * pa.ldk;
+#pragma unroll
+        for (int j = 0; j < KI; ++j)
+            if (lane < K_LANES) gl_lds16(kblk + k_goff[j], k_lds + stage * K_BYTES + j * K_LANES * 16);
+        bsl.issue(p.b, p.ldb, bw, b_lds + stage * Slice::BYTES);
+    };
+
+    // Mask values of lane (query l32, half q): keys 8i + 4q .. +3 are 8 bytes
+    // of chunk i of the query's row in the A layout.
+    const int m_rd = (l32 >> 3) * 512 + (l32 & 7) * 16 + 8 * q;  // + i * 128
+    f32x16 acc[1];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[0][v] = 0.0f;
+
+    struct Operands {
+        u32x4 a[2];
+        u32x4 b[2][1];
+    };
+    run_ring<S, PER, Operands>(
+        n, issue,
+        [&](int stage, Operands& o) {
+            const uint8_t* ks = smem + K_RING + stage * K_BYTES;
+            f32x16 st;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) st[v] = 0.0f;
+#pragma unroll
+            for (int s2 = 0; s2 < DK / 16; ++s2)
+                st = mfma32(*(const u32x4*)(ks + (32 * (2 * s2 + q) + l32) * 16), qv[s2], st);
+            const uint8_t* ms = smem + stage * kA_BYTES;
+            uint32_t mk[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint64_t w = *(const uint64_t*)(ms + m_rd + i * 128);
+                mk[2 * i] = (uint32_t)w;
+                mk[2 * i + 1] = (uint32_t)(w >> 32);
+            }
+            uint32_t sb[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+                sb[t] = pack_bf16x2(st[2 * t] * __uint_as_float(mk[t] << 16),
+                                    st[2 * t + 1] * __uint_as_float(mk[t] & 0xffff0000u));
+            o.a[0] = u32x4{sb[0], sb[1], sb[2], sb[3]};
+            o.a[1] = u32x4{sb[4], sb[5], sb[6], sb[7]};
+            bsl.read(smem + B_RING + stage * Slice::BYTES, o.b);
+        },
+        [&](const Operands& o) {
+            acc[0] = mfma32(o.a[0], o.b[0][0], acc[0]);
+            acc[0] = mfma32(o.a[1], o.b[1][0], acc[0]);
+        },
+        [&] {
+#pragma unroll
+            for (int s2 = 0; s2 < DK / 16; ++s2)
+                qv[s2] = *(const u32x4*)(smem + Q_AREA + (32 * (2 * s2 + q) + l32) * 16);
+        });
+    spmm_finish<1, OUT_BF16>(p, it, acc, tid);
 }
 
 // Adds the partials of each split row in piece order (deterministic) and
@@ -540,9 +714,9 @@ __global__ __launch_bounds__(256) void sddmm_kernel(SddmmArgs p) {
                 const float val = sum * bf16_to_f32((uint16_t)mcur[j]);
                 const int64_t idx = off + (int64_t)(8 * wave + 4 * q + j) * p.ldo + l32;
                 if (OUT_BF16)
-                    ((uint16_t*)p.out)[idx] = f32_to_bf16_rne(val);
+                    store_out(&((uint16_t*)p.out)[idx], f32_to_bf16_rne(val));
                 else
-                    ((float*)p.out)[idx] = val;
+                    store_out(&((float*)p.out)[idx], val);
             }
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
@@ -592,6 +766,33 @@ hipError_t launch_spmm(const SpmmArgs& a, const SpmmVariant& v, bool out_bf16, i
     BSP_SPMM_VARIANTS(BSP_SPMM_CASE)
 #undef BSP_SPMM_CASE
     return hipErrorInvalidValue;
+}
+
+template <int DK>
+static void launch_attention_t(const AttentionArgs& a, bool out_bf16, int grid, int n_split, hipStream_t stream) {
+    if (out_bf16)
+        hipLaunchKernelGGL((attention_kernel<DK, kAttentionStages, true>), dim3(grid), dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL((attention_kernel<DK, kAttentionStages, false>), dim3(grid), dim3(256), 0, stream, a);
+    if (n_split > 0) {
+        const int g = n_split * a.s.n_tiles;
+        if (out_bf16)
+            hipLaunchKernelGGL((spmm_reduce_kernel<1, true>), dim3(g), dim3(256), 0, stream, a.s);
+        else
+            hipLaunchKernelGGL((spmm_reduce_kernel<1, false>), dim3(g), dim3(256), 0, stream, a.s);
+    }
+}
+
+hipError_t launch_attention(const AttentionArgs& a, int head_dim, bool out_bf16, int grid, int n_split,
+                            hipStream_t stream) {
+    if (grid <= 0) return hipSuccess;
+    switch (head_dim) {
+        case 32: launch_attention_t<32>(a, out_bf16, grid, n_split, stream); break;
+        case 64: launch_attention_t<64>(a, out_bf16, grid, n_split, stream); break;
+        case 128: launch_attention_t<128>(a, out_bf16, grid, n_split, stream); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 template <bool Y_COLMAJOR, bool OUT_BF16>

@@ -25,6 +25,16 @@ struct SpmmArgs {
     int32_t pad;
 };
 
+// Fused attention pair: the SpMM arguments with the mask as A (a = mask
+// values), V as B (b, ldb) and O as C (c, ldc), N = head dimension; plus Q and K.
+struct AttentionArgs {
+    SpmmArgs s;
+    const uint16_t* q;        // Q (bf16), row-major queries x d, leading dim ldq
+    const uint16_t* k;        // K (bf16), row-major keys x d, leading dim ldk
+    int64_t ldq;
+    int64_t ldk;
+};
+
 struct SddmmArgs {
     const uint16_t* mask;     // mask block values (bf16), nblocks*R*C
     const uint16_t* x;        // X (bf16), row-major M x K, leading dim ldx
@@ -74,6 +84,15 @@ inline SpmmVariant spmm_default_variant(int tile_n) {
 // Launches the SpMM kernel and, when the plan has split rows, the reduce kernel.
 hipError_t launch_spmm(const SpmmArgs& a, const SpmmVariant& v, bool out_bf16, int grid, int n_split,
                        hipStream_t stream);
+// Head dimensions of the fused attention kernel (one 128-column tile).
+inline bool attention_head_dim_supported(int64_t d) { return d == 32 || d == 64 || d == 128; }
+constexpr int kAttentionTileN = 128;
+constexpr int kAttentionStages = 4;
+
+// Launches the fused attention kernel and, for split rows, the reduce kernel.
+hipError_t launch_attention(const AttentionArgs& a, int head_dim, bool out_bf16, int grid, int n_split,
+                            hipStream_t stream);
+
 hipError_t launch_sddmm(const SddmmArgs& a, bool y_colmajor, bool out_bf16, int grid,
                         hipStream_t stream);
 

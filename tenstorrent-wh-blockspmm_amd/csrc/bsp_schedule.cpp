@@ -182,7 +182,7 @@ std::vector<SddmmItem> sddmm_wg_records(const SddmmSchedule& s) {
 }
 
 int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSchedule& s,
-                        std::string& msg) {
+                        std::string& msg, int force_tile_n) {
     int st = validate_bsr(a, msg);
     if (st != BSP_OK) return st;
     if (N <= 0) {
@@ -206,7 +206,7 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
     // Workgroup width: 128 columns (four waves of 32); 256 (four waves of 64)
     // only when N is a multiple of 256 and rows alone give two workgroups per
     // compute unit.  The last tile of a row may be partial.
-    int64_t tn = env_int("BSP_SPMM_TILE_N", 0);
+    int64_t tn = force_tile_n ? force_tile_n : env_int("BSP_SPMM_TILE_N", 0);
     if (tn != 0 && tn != 128 && tn != 256) tn = 0;
     if (tn == 0) tn = (N % 256 == 0 && nsr * (N / 256) >= 2 * (int64_t)num_cus) ? 256 : 128;
     s.tile_n = (int32_t)tn;

@@ -98,8 +98,10 @@ std::vector<SddmmItem> sddmm_wg_records(const SddmmSchedule& s);
 // bsp_status and fills `msg`.
 int validate_bsr(const bsp_bsr_desc* d, std::string& msg);
 
+// force_tile_n: a fixed workgroup width (the fused attention kernel's one
+// 128-column tile) instead of the automatic choice.
 int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSchedule& out,
-                        std::string& msg);
+                        std::string& msg, int force_tile_n = 0);
 int build_sddmm_schedule(const bsp_bsr_desc* mask, int64_t K, int num_cus, SddmmSchedule& out,
                          std::string& msg);
 

@@ -143,3 +143,36 @@ def with_values(s, content="RAND", seed=0):
     rng = np.random.default_rng(seed)
     s.data = W.block_content(s.nblocks, s.R, s.C, content, rng)
     return s
+
+
+def run_attention(mask, q: np.ndarray, k: np.ndarray, v: np.ndarray, out_dtype="f32", plan=None,
+                  poison=True) -> np.ndarray:
+    """Fused O = bf16(mask (.) Q K^T) V on the GPU; returns fp32."""
+    import torch
+    d = q.shape[1]
+    own = plan is None
+    if own:
+        plan = capi.AttentionPlan(bsr_of(mask), d, out_dtype)
+    dm, dq, dk, dv = _dev_u16(mask.data), _dev_u16(q), _dev_u16(k), _dev_u16(v)
+    M = mask.H
+    if out_dtype == "f32":
+        do = torch.full((M, d), float("nan") if poison else 0.0, dtype=torch.float32, device="cuda")
+    else:
+        do = torch.full((M, d), 0x7FC0 if poison else 0, dtype=torch.int16, device="cuda")
+    plan.run(dm, dq, dk, dv, do, stream=torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    out = do.cpu().numpy()
+    if own:
+        plan.close()
+    if out_dtype == "f32":
+        return out
+    return W.bf16_to_f32(out.view(np.uint16))
+
+
+def golden_attention(mask, q, k, v):
+    """The oracle chain: S = mask (.) Q K^T (SDDMM with K as column-major Y),
+    rounded to bf16, then O = S V (SpMM on the mask's structure).  Returns
+    (O, S as BSR arrays)."""
+    s = golden_sddmm(mask, q, k, y_colmajor=True)
+    a = W.BsrArrays(mask.H, mask.W, mask.R, mask.C, mask.indptr, mask.indices, W.bf16_from_f32(s))
+    return golden_spmm(a, v), a

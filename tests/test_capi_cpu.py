@@ -93,6 +93,10 @@ def test_null_arguments():
         capi.BSP_ERR_INVALID_ARGUMENT
     assert lib.bsp_spmm(None, None, None, 0, None, 0, None) == capi.BSP_ERR_INVALID_ARGUMENT
     assert lib.bsp_sddmm(None, None, None, 0, None, 0, None, None) == capi.BSP_ERR_INVALID_ARGUMENT
+    assert lib.bsp_attention_plan_create(None, ctypes.byref(_bsr(**GOOD).desc()), 64, 0, 0) == \
+        capi.BSP_ERR_INVALID_ARGUMENT
+    assert lib.bsp_attention(None, None, None, 64, None, 64, None, 64, None, 64, None) == \
+        capi.BSP_ERR_INVALID_ARGUMENT
     assert lib.bsp_plan_destroy(None) == capi.BSP_OK
     g = _bsr(**GOOD)
     assert lib.bsp_host_spmm(ctypes.byref(g.desc()), None, None, 64, None, 0, 0) == \
@@ -114,6 +118,13 @@ def test_plan_create_rejects_before_touching_a_device():
     assert lib.bsp_spmm_plan_create(ctypes.byref(h), ctypes.byref(bad.desc()), 64, 0, 0, 0) == \
         capi.BSP_ERR_BAD_STRUCTURE
     assert lib.bsp_sddmm_plan_create(ctypes.byref(h), ctypes.byref(bad.desc()), 64, 0, 0, 0) == \
+        capi.BSP_ERR_BAD_STRUCTURE
+    for d in (0, 48, 96, 256):  # the fused attention kernel takes head dimensions 32, 64, 128
+        assert lib.bsp_attention_plan_create(ctypes.byref(h), ctypes.byref(good.desc()), d, 0, 0) == \
+            capi.BSP_ERR_UNSUPPORTED
+    assert lib.bsp_attention_plan_create(ctypes.byref(h), ctypes.byref(good.desc()), 64, 9, 0) == \
+        capi.BSP_ERR_INVALID_ARGUMENT  # bad dtype
+    assert lib.bsp_attention_plan_create(ctypes.byref(h), ctypes.byref(bad.desc()), 64, 0, 0) == \
         capi.BSP_ERR_BAD_STRUCTURE
     assert not h
 

@@ -216,3 +216,29 @@ def test_small_vectors_fixture():
     M, K, R, C = (int(t) for t in v["spmm_shape"])
     s = W.BsrArrays(M, K, R, C, v["spmm_indptr"], v["spmm_indices"], v["spmm_a"])
     assert_parity(run_spmm(s, v["spmm_b"]), v["spmm_golden"], spmm_k_eff(s), "fixture")
+
+
+def test_bf16_output_rounds_to_nearest_even():
+    """bf16 outputs are the fp32 result rounded to nearest, ties to even,
+    bit for bit.  C = b1 + b2 + b3 with A = three all-ones blocks in one row
+    and bf16 B rows chosen so that the (exact) fp32 sums are ties at bf16
+    precision (1 + 2^-8 -> 1, 1 + 3*2^-8 -> 1 + 2^-6, 65280 + 128 -> 65536,
+    ...) or just above / below a tie (+-2^-16)."""
+    R = C = 32
+    N = 32
+    a_vals = W.bf16_from_f32(np.ones(3 * R * C, np.float32))
+    a = W.BsrArrays(32, 96, R, C, np.array([0, 3], np.int32), np.array([0, 1, 2], np.int32), a_vals)
+    cases = [(1.0, 2 ** -8, 0.0), (1.0, 3 * 2 ** -8, 0.0), (1.0, 2 ** -8, 2 ** -16), (-1.0, -2 ** -8, 0.0),
+             (256.0, 1.0, 0.0), (2.0 ** -20, 2.0 ** -28, 0.0), (1.0, 2 ** -8, -2 ** -16), (3.0, 2 ** -7, 0.0),
+             (0.5, 2 ** -10, 0.0), (1.0, 5 * 2 ** -8, 0.0), (65280.0, 128.0, 0.0), (1.0, -2 ** -9, 0.0)]
+    b = np.zeros((96, N), np.float32)
+    for j, (x, y, z) in enumerate(cases):
+        b[0, j], b[32, j], b[64, j] = x, y, z
+    b16 = W.bf16_from_f32(b)
+    assert np.array_equal(W.bf16_to_f32(b16), b)  # inputs exactly representable
+    gold = golden_spmm(a, b16)  # fp32 sums, exact here
+    assert np.array_equal(gold[0, :len(cases)], np.array([x + y + z for x, y, z in cases], np.float32))
+    expect = W.bf16_to_f32(W.bf16_from_f32(gold))
+    assert list(expect[0, :len(cases)]) == [1.0, 1.015625, 1.0078125, -1.0, 256.0, 2.0 ** -20, 1.0, 3.0,
+                                            0.5, 1.015625, 65536.0, 1.0]
+    np.testing.assert_array_equal(run_spmm(a, b16, "bf16"), expect)
