@@ -53,7 +53,7 @@ def parse_args():
     p.add_argument("--copy-calibration", action="store_true",
                    help="first run a 256 MiB device copy and a 256 MiB elementwise multiply (kernels of known traffic, "
                         "for scaling FETCH_SIZE / WRITE_SIZE counters)")
-    p.add_argument("--only", default="", help="comma list of sections to run: head (25%% fp32 only), sweep, sddmm, skewed, attention, host")
+    p.add_argument("--only", default="", help="comma list of sections to run: head (25%% fp32 only), sweep, sddmm, skewed, attention, large, host")
     return p.parse_args()
 
 
@@ -371,6 +371,20 @@ def main():
                             "pair_tflops": round((f1 + f2) / ((t1["launch_ms"] + t2["launch_ms"]) * 1e-3)
                                                  / 1e12, 3),
                             "fused": summarize(t3, f3, b3, steps)}
+
+    if not only or "large" in only:
+        # The reference's own published configuration: M = N = K = 8192 with
+        # 256 x 256 blocks at 25% (its best: 50.6 TFLOP/s on a Wormhole N150).
+        w = W.workload_spmm_large_blocks(0.25)
+        rows = []
+        for od in ("bf16", "f32"):
+            t, fl, nb, info, _ = bench_spmm(torch, capi, W, w["a"], w["b"], od, max(10, steps // 10),
+                                            max(2, warmup // 10))
+            rows.append({"out": od, **summarize(t, fl, nb, steps), "tile_n": info["tile_n"],
+                         "grid": info["grid"]})
+        out["large_blocks"] = {"workload": "SpMM 8192^3, 256x256 blocks, 25% (256 blocks)",
+                               "nnzb": w["a"].nblocks, "runs": rows}
+        del w
 
     if not only or "host" in only:
         # The blocking host-buffer entry point (the reference operator's shape):

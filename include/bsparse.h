@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define BSP_ABI_VERSION 1
+#define BSP_ABI_VERSION 2
 
 typedef enum bsp_status {
     BSP_OK = 0,
@@ -99,6 +99,9 @@ typedef struct bsp_plan_info {
     int32_t grid;        /* workgroups per launch */
     int32_t max_item_entries;
     int32_t stages;      /* SpMM: depth of the LDS ring (entries in flight + 1) */
+    int32_t group;       /* SpMM: 32-row stripes of one block row per workgroup
+                            (1; or 2, 4, 8 for blocks of R >= 64) */
+    int32_t reserved;
     int64_t workspace_bytes; /* device scratch owned by the plan */
 } bsp_plan_info;
 

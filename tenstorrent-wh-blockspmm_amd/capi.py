@@ -16,7 +16,7 @@ import numpy as np
 PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = PKG_DIR / "libbsparse.so"
 
-ABI_VERSION = 1  # BSP_ABI_VERSION of include/bsparse.h
+ABI_VERSION = 2  # BSP_ABI_VERSION of include/bsparse.h
 BSP_OK = 0
 BSP_ERR_INVALID_ARGUMENT = 1
 BSP_ERR_BAD_STRUCTURE = 2
@@ -58,6 +58,8 @@ class PlanInfo(ctypes.Structure):
         ("grid", c_int32),
         ("max_item_entries", c_int32),
         ("stages", c_int32),
+        ("group", c_int32),
+        ("reserved", c_int32),
         ("workspace_bytes", c_int64),
     ]
 

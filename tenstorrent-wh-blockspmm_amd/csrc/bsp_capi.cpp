@@ -105,14 +105,15 @@ void fill_info_spmm(const bsp::SpmmSchedule& s, bsp_plan_info* info) {
     info->n_slots = s.n_slots;
     info->grid = (int32_t)s.wgmap.size();
     info->max_item_entries = s.max_item_entries;
-    // Ring depth: the tile width's default, or a supported override
-    // (BSP_SPMM_STAGES) for experiments.
-    bsp::SpmmVariant v = bsp::spmm_default_variant(s.tile_n);
+    // Ring depth: the default for the tile width and row group, or a
+    // supported override (BSP_SPMM_STAGES) for experiments.
+    bsp::SpmmVariant v = bsp::spmm_default_variant(s.tile_n, s.group);
     if (const char* e = std::getenv("BSP_SPMM_STAGES")) {
-        const bsp::SpmmVariant w{s.tile_n, std::atoi(e)};
+        const bsp::SpmmVariant w{s.tile_n, std::atoi(e), s.group};
         if (bsp::spmm_variant_supported(w)) v = w;
     }
     info->stages = v.stages;
+    info->group = s.group;
     info->workspace_bytes =
         (int64_t)s.n_slots * s.n_tiles * bsp::spmm_partial_floats(s.tile_n) * (int64_t)sizeof(float);
 }
@@ -210,7 +211,7 @@ int make_spmm_plan(bsp_plan** out, int kind, const bsp_bsr_desc* a, int64_t N, i
     st = device_cus(device, &cus);
     if (st != BSP_OK) return st;
     bsp::SpmmSchedule s;
-    st = bsp::build_spmm_schedule(a, N, cus, s, msg, force_tile_n);
+    st = bsp::build_spmm_schedule(a, N, cus, s, msg, force_tile_n, kind == 3 ? 1 : 0);
     if (st != BSP_OK) return fail(st, msg);
 
     DeviceGuard g(device);
@@ -298,7 +299,7 @@ int bsp_spmm(const bsp_plan* p, const uint16_t* a_vals, const uint16_t* b, int64
     DeviceGuard g(p->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     const bsp::SpmmArgs args = spmm_args(p, a_vals, b, ldb, c, ldc);
-    const bsp::SpmmVariant v{p->info.tile_n, p->info.stages};
+    const bsp::SpmmVariant v{p->info.tile_n, p->info.stages, p->info.group};
     hipError_t e = bsp::launch_spmm(args, v, p->out_dtype == BSP_DTYPE_BF16, p->info.grid, p->info.n_split_rows,
                                     (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "SpMM launch");

@@ -160,76 +160,103 @@ __device__ __forceinline__ void store_out(T* p, T v) {
     __builtin_nontemporal_store(v, p);
 }
 
-// Stores the accumulators of one 32 x TN tile (columns past N skipped).
+// Stores one 32x32 MFMA result at rows row0.., column col (this lane's
+// column; skipped past N).
+template <bool OUT_BF16>
+__device__ __forceinline__ void store_tile32(const SpmmArgs& p, const f32x16& acc, int64_t row0, int64_t col,
+                                             int q) {
+    if (col >= p.N) return;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int64_t row = row0 + 8 * (v >> 2) + 4 * q + (v & 3);
+        if (OUT_BF16)
+            store_out(&((uint16_t*)p.c)[row * p.ldc + col], f32_to_bf16_rne(acc[v]));
+        else
+            store_out(&((float*)p.c)[row * p.ldc + col], acc[v]);
+    }
+}
+
+// Stores the accumulators of one 32 x TN tile (wave w holds columns
+// w*NTW*32 ..).
 template <int NTW, bool OUT_BF16>
 __device__ __forceinline__ void spmm_store_tile(const SpmmArgs& p, const f32x16 (&acc)[NTW], int64_t row0,
                                                 int n0, int wave, int l32, int q) {
 #pragma unroll
-    for (int nt = 0; nt < NTW; ++nt) {
-        const int64_t col = n0 + wave * (NTW * 32) + nt * 32 + l32;
-        if (col >= p.N) continue;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int64_t row = row0 + 8 * (v >> 2) + 4 * q + (v & 3);
-            if (OUT_BF16)
-                store_out(&((uint16_t*)p.c)[row * p.ldc + col], f32_to_bf16_rne(acc[nt][v]));
-            else
-                store_out(&((float*)p.c)[row * p.ldc + col], acc[nt][v]);
-        }
-    }
+    for (int nt = 0; nt < NTW; ++nt)
+        store_tile32<OUT_BF16>(p, acc[nt], row0, n0 + wave * (NTW * 32) + nt * 32 + l32, q);
 }
 
 namespace spmm_detail {
 
 // Runs the LDS ring of an SpMM-shaped kernel over n entries.  Entry e lives
 // in ring stage e % S; issue(e, stage) issues its PER loads per wave,
-// read(stage, ops) reads its operands into registers, multiply(ops)
-// accumulates.  Entries 0..S-2 are issued first; entry S-1 goes into the
-// still unused last stage once entry 0 has landed.  Iteration k multiplies
-// entry k from registers, waits for entry k+1 to land (the loads issued after
-// it are those of entries k+2..k+S-1), and after the barrier (every wave holds
-// entry k's operands in registers, so stage k % S is free) issues entry k+S
-// into stage k % S and reads entry k+1's operands, whose LDS latency then
-// overlaps the next multiply.  landed() runs once entry 0 (and every load
+// read(stage, ops) issues the LDS reads of its operands into registers,
+// multiply(ops) accumulates.  Entries 0..S-2 are issued first; entry S-1
+// goes into the still unused last stage once entry 0 has landed.  Step k
+// (entry k+1 exists): wait for this wave's reads of entry k, wait for entry
+// k+1 to land (the loads issued after it are those of entries k+2..k+S-1),
+// barrier (every wave has entry k's operands, so stage k % S is free, and
+// entry k+1 is visible), issue entry k+S into stage k % S, issue the reads of
+// entry k+1, then multiply entry k: the MFMAs cover the reads' latency.  The
+// loop is unrolled by two so the two operand sets keep their registers.
+// With OVERLAP = false (one operand set, for kernels whose accumulators leave
+// no registers for a second) entry k is multiplied before the barrier and
+// entry k+1's reads follow it.  landed() runs once entry 0 (and every load
 // issued before it) has landed and is visible to all waves.
-template <int S, int PER, class Ops, class Issue, class Read, class Multiply, class Landed>
+template <int S, int PER, bool OVERLAP, class Ops, class Issue, class Read, class Multiply, class Landed>
 __device__ __forceinline__ void run_ring(int n, Issue&& issue, Read&& read, Multiply&& multiply,
                                          Landed&& landed) {
     static_assert(PER * (S - 2) < 64, "vmcnt budget");
+    if (n <= 0) return;
 #pragma unroll
     for (int e = 0; e < S - 1; ++e)
         if (e < n) issue(e, e);
-    Ops cur;
-    if (n > 0) {
-        wait_stages<PER, S - 2>(n - 1);  // entry 0 landed
-        barrier_no_fence();
-        landed();
-        if (S - 1 < n) issue(S - 1, S - 1);
-        read(0, cur);
-    }
-    int k = 0;
+    Ops o0;
+    wait_stages<PER, S - 2>(n - 1);  // entry 0 landed
+    barrier_no_fence();
+    landed();
+    if (S - 1 < n) issue(S - 1, S - 1);
+    read(0, o0);
     int stage = 0;  // stage of entry k
-    for (; k < n - S + 1; ++k) {
-        multiply(cur);
-        // Entry k's operand reads must be complete before the barrier frees
-        // its stage (the compiler would otherwise wait only at their first
-        // use, which it may schedule after the barrier and the next issue).
+    // Waits for entry k+1 and frees stage k % S (entry k's reads are this
+    // wave's; the compiler would otherwise wait for them only at their first
+    // use, after the barrier and the next issue).
+    auto sync = [&](int k) {
         __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        wait_vmcnt<PER * (S - 2)>();  // entry k+1 landed
+        if (k <= n - S)
+            wait_vmcnt<PER * (S - 2)>();         // entry k+1 landed
+        else
+            wait_stages<PER, S - 2>(n - 2 - k);  // the same, fewer in flight
         barrier_no_fence();
         if (k + S < n) issue(k + S, stage);
         stage = stage == S - 1 ? 0 : stage + 1;
-        read(stage, cur);
-    }
-    // Tail: every entry is issued; fewer are in flight.
-    for (; k < n; ++k) {
-        multiply(cur);
-        if (k + 1 < n) {
-            wait_stages<PER, S - 2>(n - 2 - k);  // entry k+1 landed
-            barrier_no_fence();
-            stage = stage == S - 1 ? 0 : stage + 1;
-            read(stage, cur);
+    };
+    int k = 0;
+    if constexpr (OVERLAP) {
+        Ops o1;
+        for (; k + 2 < n; k += 2) {
+            sync(k);
+            read(stage, o1);
+            multiply(o0);
+            sync(k + 1);
+            read(stage, o0);
+            multiply(o1);
         }
+        if (k + 1 < n) {
+            sync(k);
+            read(stage, o1);
+            multiply(o0);
+            multiply(o1);
+        } else {
+            multiply(o0);
+        }
+    } else {
+        for (; k + 1 < n; ++k) {
+            multiply(o0);
+            sync(k);
+            read(stage, o0);
+        }
+        multiply(o0);
     }
 }
 
@@ -242,14 +269,9 @@ struct BSlice {
     static constexpr int ROW_BYTES = 2 * TN;
     static constexpr int BYTES = 32 * ROW_BYTES;
     static constexpr int BI = BYTES / 1024 / 4;
-    int64_t goff[BI];     // element offsets of this lane's chunks from the slice's first row
-    int rd[2][2][NTW];    // LDS offsets of the transpose reads [k-step][4-row group][tile]
+    int64_t goff[BI];  // element offsets of this lane's chunks from the slice's first row
 
-    // key_major: the rows read by the B operand of k-step s2, lane half q,
-    // 4-row group h are 16*s2 + 8*q + 4*h (the MFMA's own order) or, with
-    // permuted = true, 16*s2 + 8*h + 4*q (the order in which a 32x32 MFMA
-    // result holds its rows, for an A operand built from a result).
-    __device__ __forceinline__ BSlice(int wave, int lane, int n0, int N, int64_t ldb, bool permuted) {
+    __device__ __forceinline__ BSlice(int wave, int lane, int n0, int N, int64_t ldb) {
 #pragma unroll
         for (int j = 0; j < BI; ++j) {
             const int byte = (wave * BI + j) * 1024 + lane * 16;
@@ -259,30 +281,43 @@ struct BSlice {
             const int col = min(n0 + 8 * (slot ^ (4 * (r & 3))), N - 8);
             goff[j] = (int64_t)r * ldb + col;
         }
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int nt = 0; nt < NTW; ++nt) {
-                    const int g = lane >> 4;
-                    const int r = 16 * s2 + (permuted ? 8 * h + 4 * (g >> 1) : 8 * (g >> 1) + 4 * h) +
-                                  ((lane & 15) >> 2);
-                    const int col = wave * (NTW * 32) + nt * 32 + 16 * (g & 1) + 4 * (lane & 3);
-                    const int c = col >> 3;
-                    rd[s2][h][nt] = r * ROW_BYTES + 16 * (c ^ (4 * (r & 3))) + 2 * (col & 7);
-                }
     }
     __device__ __forceinline__ void issue(const uint16_t* b, int64_t ldb, uint32_t brow, uint32_t lds_wave) const {
         const uint16_t* bpan = b + (int64_t)brow * ldb;
 #pragma unroll
         for (int j = 0; j < BI; ++j) gl_lds16(bpan + goff[j], lds_wave + j * 1024);
     }
-    __device__ __forceinline__ void read(const uint8_t* bs, u32x4 (&o)[2][NTW]) const {
+};
+
+// B operands of NT 32-column tiles (from column col0 of a TN-wide slice) by
+// transpose reads.  The rows read for k-step s2, lane half q, 4-row group h
+// are 16*s2 + 8*q + 4*h (the MFMA's own order) or, with permuted, 16*s2 +
+// 8*h + 4*q (the order in which a 32x32 MFMA result holds its rows, for an A
+// operand built from a result).
+template <int TN, int NT>
+struct BReads {
+    int rd[2][2][NT];  // LDS offsets [k-step][4-row group][tile]
+
+    __device__ __forceinline__ BReads(int lane, int col0, bool permuted) {
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-            for (int nt = 0; nt < NTW; ++nt) {
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const int g = lane >> 4;
+                    const int r = 16 * s2 + (permuted ? 8 * h + 4 * (g >> 1) : 8 * (g >> 1) + 4 * h) +
+                                  ((lane & 15) >> 2);
+                    const int col = col0 + nt * 32 + 16 * (g & 1) + 4 * (lane & 3);
+                    const int c = col >> 3;
+                    rd[s2][h][nt] = r * (2 * TN) + 16 * (c ^ (4 * (r & 3))) + 2 * (col & 7);
+                }
+    }
+    __device__ __forceinline__ void read(const uint8_t* bs, u32x4 (&o)[2][NT]) const {
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
                 const u32x4 lo = ld_tr_b16(bs + rd[s2][0][nt]);
                 const u32x4 hi = ld_tr_b16(bs + rd[s2][1][nt]);
                 o[s2][nt] = u32x4{lo.x, lo.y, hi.x, hi.y};
@@ -325,7 +360,8 @@ __global__ __launch_bounds__(256) void spmm_kernel(SpmmArgs p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave
     const int l32 = lane & 31, q = lane >> 5;
     const uint32_t lds0 = lds_address(smem);
-    const Slice bsl(wave, lane, it.tile * Slice::TN, p.N, p.ldb, false);
+    const Slice bsl(wave, lane, it.tile * Slice::TN, p.N, p.ldb);
+    const BReads<Slice::TN, NTW> brd(lane, wave * NTW * 32, false);
 
     // Loads of one entry, per wave: lanes 0-31 fetch A segment `wave` (lane
     // 8*j + i loads A[8*wave + i][8*j .. +7]) and the wave's pieces of the B slice.
@@ -352,13 +388,13 @@ __global__ __launch_bounds__(256) void spmm_kernel(SpmmArgs p) {
         u32x4 a[2];
         u32x4 b[2][NTW];
     };
-    run_ring<S, PER, Operands>(
+    run_ring<S, PER, true, Operands>(
         it.e_end - it.e_begin, issue,
         [&](int stage, Operands& o) {
             const uint8_t* as = smem + stage * kA_BYTES;
             o.a[0] = *(const u32x4*)(as + a_rd);
             o.a[1] = *(const u32x4*)(as + 256 + a_rd);
-            bsl.read(smem + B_RING + stage * Slice::BYTES, o.b);
+            brd.read(smem + B_RING + stage * Slice::BYTES, o.b);
         },
         [&](const Operands& o) {
 #pragma unroll
@@ -368,6 +404,120 @@ __global__ __launch_bounds__(256) void spmm_kernel(SpmmArgs p) {
         },
         [] {});
     spmm_finish<NTW, OUT_BF16>(p, it, acc, tid);
+}
+
+// ---------------------------------------------------------------------------
+// SpMM over row groups: a workgroup takes RW (2, 4 or 8) consecutive 32-row
+// stripes of one block row (R >= 64) and one 128-column tile, so each entry's
+// B panel is loaded once and multiplied by the RW stripes' A sub-blocks
+// (which share the block row's column pattern).  The four waves form a WR x
+// WC grid: wave (wr, wc) holds SR = RW/WR stripes x NT = 4/WC 32-column
+// tiles.  A ring stage holds the entry's RW A sub-blocks (each in the layout
+// of the single-stripe kernel, sub-block s at s*2 KB) and the B slice; the
+// ring, B slice and epilogue are the single-stripe kernel's.
+// Two waves per SIMD (two workgroups per compute unit): the register budget
+// that keeps the 8-stripe accumulators of a wave (128 values) without spills.
+template <int RW, int S, bool OUT_BF16>
+__global__ __launch_bounds__(256, 2) void spmm_group_kernel(SpmmArgs p) {
+    using namespace spmm_detail;
+    using Slice = BSlice<1>;
+    constexpr int WR = RW < 4 ? RW : 4;
+    constexpr int WC = 4 / WR;
+    constexpr int SR = RW / WR;
+    constexpr int NT = 4 / WC;
+    constexpr int A_BYTES = RW * kA_BYTES;
+    constexpr int AI = RW / 2;  // A load instructions per wave (two 512-byte segments each)
+    constexpr int PER = AI + Slice::BI;
+    constexpr int B_RING = S * A_BYTES;
+    static_assert(RW == 2 || RW == 4 || RW == 8, "row group");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[S * (A_BYTES + Slice::BYTES)];
+
+    const SpmmWg it = load_const(p.wgs + blockIdx.x);
+    if (it.row < 0) return;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31, q = lane >> 5;
+    const int wr = wave / WC, wc = wave % WC;
+    const uint32_t lds0 = lds_address(smem);
+    const Slice bsl(wave, lane, it.tile * Slice::TN, p.N, p.ldb);
+    const BReads<Slice::TN, NT> brd(lane, wc * NT * 32, false);
+
+    // A of one entry: 4*RW segments of 512 bytes (sub-block L/4, rows
+    // 8*(L%4) .. +7); segment L lands at L*512, and wave w's load j covers
+    // segments 2*(w*AI + j) and 2*(w*AI + j) + 1.
+    int64_t a_goff[AI];
+#pragma unroll
+    for (int j = 0; j < AI; ++j) {
+        const int L = 2 * (wave * AI + j) + (lane >> 5);
+        a_goff[j] = (int64_t)(L >> 2) * 32 * p.lda + (8 * (L & 3) + (lane & 7)) * p.lda + 8 * ((lane & 31) >> 3);
+    }
+    const uint32_t a_lds = lds0 + wave * AI * 1024;
+    const uint32_t b_lds = lds0 + B_RING + wave * Slice::BI * 1024;
+    // Entry words: first row of B | A offset of the group's first stripe / 32.
+    const uint32_t* words = (const uint32_t*)(p.ents + it.e_begin);
+    auto issue = [&](int e, int stage) {
+        const uint32_t bw = load_const(words + 2 * e);
+        const uint32_t aw = load_const(words + 2 * e + 1);
+        const uint16_t* ablk = p.a + (int64_t)aw * 32;
+#pragma unroll
+        for (int j = 0; j < AI; ++j) gl_lds16(ablk + a_goff[j], a_lds + stage * A_BYTES + j * 1024);
+        bsl.issue(p.b, p.ldb, bw, b_lds + stage * Slice::BYTES);
+    };
+
+    const int a_rd = (l32 >> 3) * 512 + (8 * q + (l32 & 7)) * 16;  // + s * 256 + sub-block * 2 KB
+    f32x16 acc[SR][NT];
+#pragma unroll
+    for (int i = 0; i < SR; ++i)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][nt][v] = 0.0f;
+
+    struct Operands {
+        u32x4 a[SR][2];
+        u32x4 b[2][NT];
+    };
+    run_ring<S, PER, (RW < 8), Operands>(
+        it.e_end - it.e_begin, issue,
+        [&](int stage, Operands& o) {
+            const uint8_t* as = smem + stage * A_BYTES;
+#pragma unroll
+            for (int i = 0; i < SR; ++i) {
+                o.a[i][0] = *(const u32x4*)(as + (wr * SR + i) * kA_BYTES + a_rd);
+                o.a[i][1] = *(const u32x4*)(as + (wr * SR + i) * kA_BYTES + 256 + a_rd);
+            }
+            brd.read(smem + B_RING + stage * Slice::BYTES, o.b);
+        },
+        [&](const Operands& o) {
+#pragma unroll
+            for (int i = 0; i < SR; ++i)
+#pragma unroll
+                for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) acc[i][nt] = mfma32(o.a[i][s2], o.b[s2][nt], acc[i][nt]);
+        },
+        [] {});
+
+#pragma unroll
+    for (int i = 0; i < SR; ++i) {
+        const int st = wr * SR + i;  // stripe within the group
+        if (it.slot >= 0) {
+            // Piece of a split group: stripe st's partial goes to its own slot
+            // in the single-stripe layout (tile c's column l at c*64 + l).
+            const int slot = it.base + st * it.npieces + (it.slot - it.base);
+            float* mine = p.ws + ((int64_t)slot * p.n_tiles + it.tile) * (16 * 256);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) mine[v * 256 + (wc * NT + nt) * 64 + lane] = acc[i][nt][v];
+        } else {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+                store_tile32<OUT_BF16>(p, acc[i][nt], (int64_t)(it.row + st) * 32,
+                                       (int64_t)it.tile * Slice::TN + (wc * NT + nt) * 32 + l32, q);
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -403,7 +553,8 @@ __global__ __launch_bounds__(256) void attention_kernel(AttentionArgs pa) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, q = lane >> 5;
     const uint32_t lds0 = lds_address(smem);
-    const Slice bsl(wave, lane, 0, p.N, p.ldb, true);
+    const Slice bsl(wave, lane, 0, p.N, p.ldb);
+    const BReads<Slice::TN, 1> brd(lane, wave * 32, true);
 
     // K blocks and the stripe's Q rows in LDS as 16-byte chunks (c, row r) at
     // (32c + r) * 16, so that the operand of step s of row l32 (chunk 2s + q)
@@ -457,7 +608,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttentionArgs pa) {
         u32x4 a[2];
         u32x4 b[2][1];
     };
-    run_ring<S, PER, Operands>(
+    run_ring<S, PER, true, Operands>(
         n, issue,
         [&](int stage, Operands& o) {
             const uint8_t* ks = smem + K_RING + stage * K_BYTES;
@@ -482,7 +633,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttentionArgs pa) {
                                     st[2 * t + 1] * __uint_as_float(mk[t] & 0xffff0000u));
             o.a[0] = u32x4{sb[0], sb[1], sb[2], sb[3]};
             o.a[1] = u32x4{sb[4], sb[5], sb[6], sb[7]};
-            bsl.read(smem + B_RING + stage * Slice::BYTES, o.b);
+            brd.read(smem + B_RING + stage * Slice::BYTES, o.b);
         },
         [&](const Operands& o) {
             acc[0] = mfma32(o.a[0], o.b[0][0], acc[0]);
@@ -739,12 +890,19 @@ __global__ __launch_bounds__(256) void sddmm_kernel(SddmmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-template <int NTW, int S>
+template <int NTW, int S, int G>
 static void launch_spmm_t(const SpmmArgs& a, bool out_bf16, int grid, int n_split, hipStream_t stream) {
-    if (out_bf16)
-        hipLaunchKernelGGL((spmm_kernel<NTW, S, true>), dim3(grid), dim3(256), 0, stream, a);
-    else
-        hipLaunchKernelGGL((spmm_kernel<NTW, S, false>), dim3(grid), dim3(256), 0, stream, a);
+    if constexpr (G == 1) {
+        if (out_bf16)
+            hipLaunchKernelGGL((spmm_kernel<NTW, S, true>), dim3(grid), dim3(256), 0, stream, a);
+        else
+            hipLaunchKernelGGL((spmm_kernel<NTW, S, false>), dim3(grid), dim3(256), 0, stream, a);
+    } else {
+        if (out_bf16)
+            hipLaunchKernelGGL((spmm_group_kernel<G, S, true>), dim3(grid), dim3(256), 0, stream, a);
+        else
+            hipLaunchKernelGGL((spmm_group_kernel<G, S, false>), dim3(grid), dim3(256), 0, stream, a);
+    }
     if (n_split > 0) {
         const int g = n_split * a.n_tiles;
         if (out_bf16)
@@ -758,10 +916,10 @@ hipError_t launch_spmm(const SpmmArgs& a, const SpmmVariant& v, bool out_bf16, i
                        hipStream_t stream) {
     if (grid <= 0) return hipSuccess;
     if (!spmm_variant_supported(v)) return hipErrorInvalidValue;
-#define BSP_SPMM_CASE(TN, S)                                              \
-    if (v.tile_n == TN && v.stages == S) {                               \
-        launch_spmm_t<TN / 128, S>(a, out_bf16, grid, n_split, stream);  \
-        return hipGetLastError();                                        \
+#define BSP_SPMM_CASE(TN, S, G)                                                   \
+    if (v.tile_n == TN && v.stages == S && v.group == G) {                       \
+        launch_spmm_t<TN / 128, S, G>(a, out_bf16, grid, n_split, stream);      \
+        return hipGetLastError();                                                \
     }
     BSP_SPMM_VARIANTS(BSP_SPMM_CASE)
 #undef BSP_SPMM_CASE

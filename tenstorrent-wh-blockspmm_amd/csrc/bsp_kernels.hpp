@@ -53,32 +53,44 @@ struct SddmmArgs {
 inline int64_t spmm_partial_floats(int tile_n) { return (int64_t)tile_n * 32; }
 
 // Compiled SpMM kernel variants: workgroup tile width (4 waves of 32 or 64
-// columns) and ring depth (entries in flight + 1).  LDS per workgroup =
-// (2 KB + 64 * tile_n bytes) * stages; two workgroups share a compute unit
-// while that is at most 80 KB.
+// columns), ring depth (entries in flight + 1) and row group (32-row stripes
+// of one block row per workgroup; groups use 128-column tiles).  LDS per
+// workgroup = (2 KB * group + 64 * tile_n bytes) * stages; two workgroups
+// share a compute unit while that is at most 80 KB.
 #define BSP_SPMM_VARIANTS(X) \
-    X(128, 4)                \
-    X(128, 6)                \
-    X(128, 8)                \
-    X(256, 3)                \
-    X(256, 4)
+    X(128, 4, 1)             \
+    X(128, 6, 1)             \
+    X(128, 8, 1)             \
+    X(256, 3, 1)             \
+    X(256, 4, 1)             \
+    X(128, 6, 2)             \
+    X(128, 4, 4)             \
+    X(128, 5, 4)             \
+    X(128, 3, 8)             \
+    X(128, 4, 8)
 
 struct SpmmVariant {
     int tile_n;
     int stages;
+    int group;
 };
 
 inline bool spmm_variant_supported(const SpmmVariant& v) {
-#define BSP_SPMM_MATCH(TN, S) \
-    if (v.tile_n == TN && v.stages == S) return true;
+#define BSP_SPMM_MATCH(TN, S, G) \
+    if (v.tile_n == TN && v.stages == S && v.group == G) return true;
     BSP_SPMM_VARIANTS(BSP_SPMM_MATCH)
 #undef BSP_SPMM_MATCH
     return false;
 }
 
-// Default ring depth for a tile width.
-inline SpmmVariant spmm_default_variant(int tile_n) {
-    return tile_n >= 256 ? SpmmVariant{256, 4} : SpmmVariant{128, 6};
+// Default ring depth for a tile width and row group.
+inline SpmmVariant spmm_default_variant(int tile_n, int group) {
+    switch (group) {
+        case 2: return {128, 6, 2};
+        case 4: return {128, 4, 4};
+        case 8: return {128, 3, 8};
+        default: return tile_n >= 256 ? SpmmVariant{256, 4, 1} : SpmmVariant{128, 6, 1};
+    }
 }
 
 // Launches the SpMM kernel and, when the plan has split rows, the reduce kernel.

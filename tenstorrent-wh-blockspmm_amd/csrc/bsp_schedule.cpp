@@ -168,8 +168,17 @@ std::vector<int64_t> spmm_packed_entries(const SpmmSchedule& s) {
 std::vector<SpmmSplit> spmm_splits(const SpmmSchedule& s) {
     std::vector<SpmmSplit> out;
     for (const SpmmItem& it : s.items)
-        if (it.slot >= 0 && it.slot == it.base) out.push_back({it.row, it.base, it.npieces, 0});
+        if (it.slot >= 0 && it.slot == it.base)
+            for (int32_t st = 0; st < s.group; ++st)
+                out.push_back({it.row + st, it.base + st * it.npieces, it.npieces, 0});
     return out;
+}
+
+int spmm_choose_group(int64_t R, int64_t H, int64_t N, int num_cus) {
+    const int64_t rs = R / kSub, nsr = H / kSub, tiles = (N + 127) / 128;
+    for (int g : {8, 4, 2})
+        if (rs % g == 0 && (nsr / g) * tiles >= 2 * (int64_t)num_cus) return g;
+    return 1;
 }
 
 std::vector<SddmmItem> sddmm_wg_records(const SddmmSchedule& s) {
@@ -182,7 +191,7 @@ std::vector<SddmmItem> sddmm_wg_records(const SddmmSchedule& s) {
 }
 
 int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSchedule& s,
-                        std::string& msg, int force_tile_n) {
+                        std::string& msg, int force_tile_n, int group) {
     int st = validate_bsr(a, msg);
     if (st != BSP_OK) return st;
     if (N <= 0) {
@@ -203,6 +212,13 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
         return BSP_ERR_UNSUPPORTED;
     }
 
+    // Row groups: stripes of one block row that share every B panel.
+    if (group <= 0) group = (int)env_int("BSP_SPMM_GROUP", spmm_choose_group(a->R, a->H, N, num_cus));
+    if (group != 1 && group != 2 && group != 4 && group != 8) group = 1;
+    if (RS % group != 0) group = 1;
+    s.group = group;
+    if (group > 1) force_tile_n = 128;
+
     // Workgroup width: 128 columns (four waves of 32); 256 (four waves of 64)
     // only when N is a multiple of 256 and rows alone give two workgroups per
     // compute unit.  The last tile of a row may be partial.
@@ -216,10 +232,12 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
     // the mean length of non-empty rows (uniform rows stay whole) and half of
     // one compute unit's fair share of the total (skewed rows are cut so no
     // workgroup dwarfs the rest), and at least 32.
+    // (In units of group entries: one entry of a group serves `group` stripes.)
+    const int64_t gtotal = total / group;
     int64_t nonempty = 0;
-    for (int64_t i = 0; i < nbr; ++i) nonempty += (a->indptr[i + 1] > a->indptr[i]) ? RS : 0;
-    const int64_t mean = nonempty ? (total + nonempty - 1) / nonempty : 0;
-    const int64_t fair = (total * s.n_tiles + num_cus - 1) / num_cus;
+    for (int64_t i = 0; i < nbr; ++i) nonempty += (a->indptr[i + 1] > a->indptr[i]) ? RS / group : 0;
+    const int64_t mean = nonempty ? (gtotal + nonempty - 1) / nonempty : 0;
+    const int64_t fair = (gtotal * s.n_tiles + num_cus - 1) / num_cus;
     int64_t L = std::max<int64_t>({32, 2 * mean, (fair + 1) / 2});
     L = env_int("BSP_SPMM_SPLIT", L);
     if (L < 1) L = 1;
@@ -234,7 +252,7 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
     s.n_split_rows = 0;
     s.max_item_entries = 0;
     std::vector<int64_t> cost;
-    for (int64_t sr = 0; sr < nsr; ++sr) {
+    for (int64_t sr = 0; sr < nsr; sr += group) {
         const int64_t i = sr / RS, sub = sr % RS;
         const int32_t e0 = (int32_t)s.ent_row.size();
         for (int64_t blk = a->indptr[i]; blk < a->indptr[i + 1]; ++blk) {
@@ -245,22 +263,23 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
         }
         const int32_t e1 = (int32_t)s.ent_row.size();
         const int64_t cnt = e1 - e0;
-        // Cost model: one unit per 32x32 product plus a fixed share for the
-        // stripe's output store (split pieces add a partial round trip).
+        // Cost model: one unit per 32x32 product (per stripe of the group)
+        // plus a fixed share for the output store (split pieces add a
+        // partial round trip).
         if (cnt <= L) {
             s.items.push_back({(int32_t)sr, e0, e1, -1, -1, 0});
-            cost.push_back(cnt + 2);
+            cost.push_back((cnt + 2) * group);
             s.max_item_entries = std::max<int32_t>(s.max_item_entries, (int32_t)cnt);
         } else {
             const int64_t np = (cnt + L - 1) / L;
             const int32_t base = s.n_slots;
-            s.n_slots += (int32_t)np;
-            s.n_split_rows += 1;
+            s.n_slots += (int32_t)(np * group);
+            s.n_split_rows += group;
             for (int64_t p = 0; p < np; ++p) {
                 const int32_t b0 = e0 + (int32_t)(cnt * p / np);
                 const int32_t b1 = e0 + (int32_t)(cnt * (p + 1) / np);
                 s.items.push_back({(int32_t)sr, b0, b1, base + (int32_t)p, base, (int32_t)np});
-                cost.push_back((b1 - b0) + 4);
+                cost.push_back(((b1 - b0) + 4) * group);
                 s.max_item_entries = std::max<int32_t>(s.max_item_entries, b1 - b0);
             }
         }

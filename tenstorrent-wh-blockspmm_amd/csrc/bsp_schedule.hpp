@@ -54,6 +54,7 @@ static_assert(sizeof(SpmmSplit) == 16, "SpmmSplit layout is shared with the kern
 struct SpmmSchedule {
     int32_t tile_n = 0;
     int32_t n_tiles = 0;
+    int32_t group = 1;        // 32-row stripes per item (rows of one block row sharing B)
     int32_t split_limit = 0;  // max entries per piece
     int32_t n_slots = 0;
     int32_t n_split_rows = 0;
@@ -61,7 +62,8 @@ struct SpmmSchedule {
     int32_t xcd_col_groups = 1;  // column groups of the XCD map
     std::vector<SpmmItem> items;
     std::vector<int32_t> ent_row;  // first row of B for the entry
-    std::vector<int64_t> ent_off;  // element offset of the 32x32 A sub-block
+    std::vector<int64_t> ent_off;  // element offset of the 32x32 A sub-block (of the item's
+                                   // first stripe; stripe s of a group adds 32*s*C)
     std::vector<int32_t> wgmap;    // workgroup id -> item * n_tiles + tile, or -1
 };
 
@@ -69,7 +71,8 @@ struct SpmmSchedule {
 std::vector<SpmmWg> spmm_wg_records(const SpmmSchedule& s);
 // Entries packed for the kernel: first row of B | (A offset / 32) << 32.
 std::vector<int64_t> spmm_packed_entries(const SpmmSchedule& s);
-// The split rows in slot order.
+// The split stripes in slot order (a split group contributes each of its
+// stripes: stripe s of a group piece p uses slot base + s * npieces + p).
 std::vector<SpmmSplit> spmm_splits(const SpmmSchedule& s);
 
 // One unit of SDDMM work: a run of output sub-blocks that share 32 rows of X.
@@ -99,9 +102,14 @@ std::vector<SddmmItem> sddmm_wg_records(const SddmmSchedule& s);
 int validate_bsr(const bsp_bsr_desc* d, std::string& msg);
 
 // force_tile_n: a fixed workgroup width (the fused attention kernel's one
-// 128-column tile) instead of the automatic choice.
+// 128-column tile) instead of the automatic choice.  group: stripes per item
+// (1, or 2, 4, 8 dividing R/32, with a 128-column tile); 0 chooses.
 int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSchedule& out,
-                        std::string& msg, int force_tile_n = 0);
+                        std::string& msg, int force_tile_n = 0, int group = 0);
+
+// Row-group size for R x C blocks: the largest of 8, 4, 2 that divides R/32
+// and still gives two workgroups per compute unit, else 1.
+int spmm_choose_group(int64_t R, int64_t H, int64_t N, int num_cus);
 int build_sddmm_schedule(const bsp_bsr_desc* mask, int64_t K, int num_cus, SddmmSchedule& out,
                          std::string& msg);
 

@@ -281,6 +281,14 @@ def spmm_workload(M, K, N, R, C, density: float, seed: int, value_range=1.0, zip
 SPMM_SWEEP_DENSITIES = (0.01, 0.05, 0.25, 0.50)
 
 
+def workload_spmm_large_blocks(density=0.25, R=256, seed=SEED_BASE + 5) -> dict:
+    """The reference's published SpMM configuration (M = N = K = 8192,
+    256 x 256 blocks, uniform-random positions;
+    block_spmm/scripts/experiments_dram_reads_table.tex:27-35): A and B bf16
+    U[-1, 1]."""
+    return spmm_workload(8192, 8192, 8192, R, R, density, seed)
+
+
 def workload_spmm_small() -> dict:
     """A 1024x1024, 32x32 blocks, 10% uniform positions, B 1024x256, U[-1,1]."""
     return spmm_workload(1024, 1024, 256, 32, 32, 0.10, SEED_BASE + 0)

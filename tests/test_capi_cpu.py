@@ -42,7 +42,7 @@ def test_library_links_hip_and_has_gfx950_code():
 
 def test_abi_version_and_status_strings():
     lib = capi.load()
-    assert lib.bsp_abi_version() == capi.ABI_VERSION == 1
+    assert lib.bsp_abi_version() == capi.ABI_VERSION == 2
     for code, text in [(0, b"ok"), (2, b"malformed BSR structure"), (3, b"unsupported")]:
         assert lib.bsp_status_string(code) == text
 
@@ -261,3 +261,44 @@ def test_sddmm_schedule_covers_every_output_sub_block_once():
         assert sorted(covered) == list(range(len(offs)))
         wg = sch["wgmap"]
         np.testing.assert_array_equal(np.sort(wg[wg >= 0]), np.arange(len(sch["items"])))
+
+
+@pytest.mark.parametrize("group,R,C", [(2, 64, 64), (4, 128, 32), (8, 256, 256), (2, 128, 64)])
+@pytest.mark.parametrize("split", [None, 2])
+def test_spmm_schedule_row_groups(monkeypatch, group, R, C, split):
+    """Group items cover every (stripe, sub-block product) exactly once: an
+    item's entries serve stripes row..row+group-1 of one block row, and split
+    groups give each stripe its own slots."""
+    monkeypatch.setenv("BSP_SPMM_GROUP", str(group))
+    if split:
+        monkeypatch.setenv("BSP_SPMM_SPLIT", str(split))
+    rng = np.random.default_rng(group * 7 + R)
+    H = Wd = 2048
+    m = W.random_positions(H, Wd, R, C, (H // R) * (Wd // C) // 3, rng)
+    sch = capi.spmm_schedule(capi.Bsr(H, Wd, R, C, m.indptr, m.indices), 256)
+    info = sch["info"]
+    assert info["group"] == group and info["tile_n"] == 128
+    RS, CS = R // 32, C // 32
+    seen = []
+    slots = set()
+    for row, e0, e1, slot, base, npieces in sch["items"][:info["n_items"]]:
+        assert row % group == 0
+        i = (row * 32) // R
+        for e in range(e0, e1):
+            off = int(sch["ent_off"][e])
+            blk, rem = divmod(off, R * C)
+            assert m.indptr[i] <= blk < m.indptr[i + 1]
+            t = (rem % C) // 32
+            assert rem == (row % RS) * 32 * C + 32 * t
+            assert sch["ent_row"][e] == m.indices[blk] * C + 32 * t
+            for st in range(group):
+                seen.append((row + st, blk, t))
+        if slot >= 0:
+            for st in range(group):
+                s_ = base + st * npieces + (slot - base)
+                assert s_ not in slots
+                slots.add(s_)
+    expect = [(i * RS + s, blk, t) for i in range(H // R) for blk in range(m.indptr[i], m.indptr[i + 1])
+              for s in range(RS) for t in range(CS)]
+    assert sorted(seen) == sorted(expect)
+    assert len(slots) == info["n_slots"]

@@ -11,7 +11,7 @@ import zlib
 import numpy as np
 import pytest
 
-from helpers import (W, assert_parity, capi, golden_spmm, run_spmm, spmm_k_eff, with_values)
+from helpers import (W, assert_parity, bsr_of, capi, golden_spmm, run_spmm, spmm_k_eff, with_values)
 
 pytestmark = pytest.mark.gpu
 
@@ -242,3 +242,69 @@ def test_bf16_output_rounds_to_nearest_even():
     assert list(expect[0, :len(cases)]) == [1.0, 1.015625, 1.0078125, -1.0, 256.0, 2.0 ** -20, 1.0, 3.0,
                                             0.5, 1.015625, 65536.0, 1.0]
     np.testing.assert_array_equal(run_spmm(a, b16, "bf16"), expect)
+
+
+# ---- row groups: RW stripes of one block row share each B panel -------------
+
+GROUP_VARIANTS = [(2, 6, 64), (4, 4, 128), (4, 5, 128), (8, 3, 256), (8, 4, 256)]
+
+
+@pytest.mark.parametrize("density", [0.1, 0.5])
+@pytest.mark.parametrize("group,stages,R", GROUP_VARIANTS)
+def test_row_group_variants(monkeypatch, group, stages, R, density):
+    monkeypatch.setenv("BSP_SPMM_GROUP", str(group))
+    monkeypatch.setenv("BSP_SPMM_STAGES", str(stages))
+    w = W.spmm_workload(2048, 2048, 384, R, R, density, seed=50 + group)
+    plan = capi.SpmmPlan(bsr_of(w["a"]), 384, "f32")
+    info = plan.info()
+    assert (info["group"], info["stages"], info["tile_n"]) == (group, stages, 128)
+    got = run_spmm(w["a"], w["b"], "f32", plan=plan)
+    plan.close()
+    assert_parity(got, golden_spmm(w["a"], w["b"]), spmm_k_eff(w["a"]),
+                  f"group={group} stages={stages} R={R} d={density}")
+
+
+@pytest.mark.parametrize("N", [32, 96, 160])
+@pytest.mark.parametrize("group", [2, 4, 8])
+def test_row_group_partial_tiles_and_bf16(monkeypatch, group, N):
+    monkeypatch.setenv("BSP_SPMM_GROUP", str(group))
+    R = 32 * group
+    w = W.spmm_workload(1024, 1024, N, R, 64, 0.3, seed=60 + N)
+    for od in ("f32", "bf16"):
+        assert_parity(run_spmm(w["a"], w["b"], od), golden_spmm(w["a"], w["b"]), spmm_k_eff(w["a"]),
+                      f"group={group} N={N} {od}")
+
+
+@pytest.mark.parametrize("split", [1, 3])
+@pytest.mark.parametrize("group", [2, 8])
+def test_row_group_split_rows(monkeypatch, group, split):
+    monkeypatch.setenv("BSP_SPMM_GROUP", str(group))
+    monkeypatch.setenv("BSP_SPMM_SPLIT", str(split))
+    R = 32 * group
+    w = W.spmm_workload(2048, 2048, 256, R, 32, 0.2, seed=70 + group)
+    plan = capi.SpmmPlan(bsr_of(w["a"]), 256, "f32")
+    assert plan.info()["group"] == group and plan.info()["n_split_rows"] > 0
+    for run in range(2):
+        got = run_spmm(w["a"], w["b"], "f32", plan=plan)
+        assert_parity(got, golden_spmm(w["a"], w["b"]), spmm_k_eff(w["a"]), f"group={group} split={split}")
+        if run == 0:
+            first = got
+    np.testing.assert_array_equal(first, got)  # the split reduction is deterministic
+    plan.close()
+
+
+def test_row_group_chosen_for_large_blocks():
+    """The reference's published shape (8192^3, 256 x 256 blocks, 25%) runs
+    in groups of 8 stripes without any override; checked on its first 1024
+    rows (a block-row prefix) against the oracle."""
+    w = W.workload_spmm_large_blocks(0.25)
+    a = w["a"]
+    plan = capi.SpmmPlan(bsr_of(a), 8192, "bf16")
+    assert plan.info()["group"] == 8
+    got = run_spmm(a, w["b"], "bf16", plan=plan)
+    plan.close()
+    rows = 1024
+    nb = int(a.indptr[rows // 256])
+    sub = W.BsrArrays(rows, a.W, 256, 256, np.ascontiguousarray(a.indptr[:rows // 256 + 1]),
+                      a.indices[:nb], a.data[:nb * 65536])
+    assert_parity(got[:rows], golden_spmm(sub, w["b"]), spmm_k_eff(sub), "8192^3 R=256 prefix")
