@@ -2,7 +2,8 @@
  * ORACLE — test infrastructure, not product code.
  *
  * A plain-C restatement of the CPU golden that salmanra/Tenstorrent-WH-BlockSpMM
- * checks its block-sparse SpMM / SDDMM device paths against.  Only tests/,
+ * checks its block-sparse SpMM / SDDMM device paths against, and its BSR x BSR
+ * SpGEMM golden (a CPU routine with no device path in the reference).  Only tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this file's
  * library, and only as the checker (or, in bench.py, as the timed CPU baseline).
  * The product path (libbsparse.so) never links, loads or calls it.
@@ -220,6 +221,87 @@ int orc_sddmm(const int32_t* indptr, const int32_t* indices, const uint16_t* mas
             }
         }
     }
+    return 0;
+}
+
+/* ---- SpGEMM: BSR x BSR -> BSR ------------------------------------------------
+ * Follows bsr_matrix<T>::spgemm, sparse_common/bsr_matrix.hpp:741-810.  A is
+ * nbrows x (W/C) blocks of R x C, B has blocks of C x BC (A's C is B's R) in
+ * b_nbc block columns.  Output block (i, j) is present iff some A(i, k) and
+ * B(k, j) are stored blocks (decided by the structure, not the values); the
+ * output lists each block row's columns in ascending order (the reference
+ * builds it by scanning j).  For every pair, in A's CSR order then B's CSR
+ * order, each element gets the C-term fp32 dot product (c ascending) added to
+ * its fp32 accumulator; the accumulator is returned (the reference stores
+ * T(acc)).  Duplicate columns in A or B contribute once per stored block.
+ * Two calls: with out_indices == NULL it fills out_indptr and *nblocks_out;
+ * then with arrays of that size it fills indices and values (nblocks*R*BC).
+ * Pinned by: the block-pattern boolean product, the dense float64 product of
+ * to_dense(A) and to_dense(B), identity B, brute force on tiny inputs.
+ * Mutations: 1 transposed B block access, 2 skip the last A block of each row,
+ *            3 output column + 1, 4 skip the c = 0 term. */
+int orc_spgemm(const int32_t* a_indptr, const int32_t* a_indices, const uint16_t* a_vals,
+               int64_t nbrows, int64_t R, int64_t C, const int32_t* b_indptr,
+               const int32_t* b_indices, const uint16_t* b_vals, int64_t BC, int64_t b_nbc,
+               int32_t* out_indptr, int32_t* out_indices, float* out_vals, int64_t* nblocks_out,
+               int mutation) {
+    if (!a_indptr || !b_indptr || !out_indptr || !nblocks_out || R <= 0 || C <= 0 || BC <= 0 ||
+        b_nbc < 0 || nbrows < 0)
+        return 1;
+    const int64_t blk = R * BC;
+    unsigned char* present = (unsigned char*)calloc((size_t)(b_nbc > 0 ? b_nbc : 1), 1);
+    float* acc = NULL;
+    if (out_indices) {
+        acc = (float*)calloc((size_t)(b_nbc > 0 ? b_nbc : 1) * (size_t)blk, sizeof(float));
+        if (!acc) {
+            free(present);
+            return 2;
+        }
+    }
+    if (!present) {
+        free(acc);
+        return 2;
+    }
+    int64_t nout = 0;
+    out_indptr[0] = 0;
+    for (int64_t i = 0; i < nbrows; ++i) {
+        int64_t a_end = a_indptr[i + 1];
+        if (mutation == 2 && a_end > a_indptr[i]) a_end -= 1;
+        for (int64_t ai = a_indptr[i]; ai < a_end; ++ai) {
+            const int64_t k = a_indices[ai];
+            const uint16_t* ab = a_vals ? a_vals + ai * R * C : NULL;
+            for (int64_t bi = b_indptr[k]; bi < b_indptr[k + 1]; ++bi) {
+                const int64_t j = b_indices[bi];
+                present[j] = 1;
+                if (!acc) continue;
+                const uint16_t* bb = b_vals + bi * C * BC;
+                float* o = acc + j * blk;
+                for (int64_t r = 0; r < R; ++r)
+                    for (int64_t p = 0; p < BC; ++p) {
+                        float sum = 0.0f;
+                        for (int64_t c = (mutation == 4 ? 1 : 0); c < C; ++c) {
+                            const int64_t bidx = mutation == 1 ? (p * C + c) % (C * BC) : c * BC + p;
+                            sum += orc_bf16_to_f32(ab[r * C + c]) * orc_bf16_to_f32(bb[bidx]);
+                        }
+                        o[r * BC + p] += sum;
+                    }
+            }
+        }
+        for (int64_t j = 0; j < b_nbc; ++j) {
+            if (!present[j]) continue;
+            if (out_indices) {
+                out_indices[nout] = (int32_t)(mutation == 3 ? (j + 1) % b_nbc : j);
+                memcpy(out_vals + nout * blk, acc + j * blk, (size_t)blk * sizeof(float));
+                memset(acc + j * blk, 0, (size_t)blk * sizeof(float));
+            }
+            present[j] = 0;
+            ++nout;
+        }
+        out_indptr[i + 1] = (int32_t)nout;
+    }
+    *nblocks_out = nout;
+    free(present);
+    free(acc);
     return 0;
 }
 

@@ -41,6 +41,9 @@ def load() -> ctypes.CDLL:
     lib.orc_sddmm.argtypes = [p32, p32, pu16, c_int64, c_int64, c_int64, pu16, c_int64, pu16, c_int64,
                               c_int, pf, c_int, c_int]
     lib.orc_sddmm.restype = c_int
+    lib.orc_spgemm.argtypes = [p32, p32, pu16, c_int64, c_int64, c_int64, p32, p32, pu16, c_int64,
+                               c_int64, p32, p32, pf, POINTER(c_int64), c_int]
+    lib.orc_spgemm.restype = c_int
     lib.orc_bsr_to_dense.argtypes = [p32, p32, pu16, c_int64, c_int64, c_int64, c_int64, pu16]
     lib.orc_bsr_to_dense.restype = c_int
     lib.orc_gemm_bf16.argtypes = [pu16, pu16, c_int64, c_int64, c_int64, pf]
@@ -94,6 +97,29 @@ def sddmm(indptr, indices, mask_vals, H, W, R, C, x, y, y_colmajor: bool = False
                           threads, mutation)
     assert rc == 0
     return out[: nblocks * R * C]
+
+
+def spgemm(a_indptr, a_indices, a_vals, H, R, C, b_indptr, b_indices, b_vals, BW, BC,
+           mutation: int = 0):
+    """fp32 golden of BSR x BSR -> BSR (sparse_common/bsr_matrix.hpp:741-810):
+    returns (indptr, indices, values[nblocks*R*BC])."""
+    a_indptr, a_indices, a_vals = _i32(a_indptr), _i32(a_indices), _u16(a_vals)
+    b_indptr, b_indices, b_vals = _i32(b_indptr), _i32(b_indices), _u16(b_vals)
+    nbr, nbc = H // R, BW // BC
+    lib = load()
+    ai = a_indices if a_indices.size else np.zeros(1, np.int32)
+    av = a_vals if a_vals.size else np.zeros(1, np.uint16)
+    bi = b_indices if b_indices.size else np.zeros(1, np.int32)
+    bv = b_vals if b_vals.size else np.zeros(1, np.uint16)
+    indptr = np.zeros(nbr + 1, np.int32)
+    n = c_int64(0)
+    args = [_p(a_indptr, c_int32), _p(ai, c_int32), _p(av, c_uint16), nbr, R, C, _p(b_indptr, c_int32),
+            _p(bi, c_int32), _p(bv, c_uint16), BC, nbc, _p(indptr, c_int32)]
+    assert lib.orc_spgemm(*args, None, None, ctypes.byref(n), mutation) == 0
+    indices = np.zeros(max(n.value, 1), np.int32)
+    vals = np.zeros(max(n.value * R * BC, 1), np.float32)
+    assert lib.orc_spgemm(*args, _p(indices, c_int32), _p(vals, c_float), ctypes.byref(n), mutation) == 0
+    return indptr, indices[: n.value], vals[: n.value * R * BC]
 
 
 def to_dense(indptr, indices, vals, H, W, R, C) -> np.ndarray:

@@ -280,3 +280,125 @@ def test_small_vectors_fixture_reproduced():
     np.testing.assert_array_equal(
         orc.sddmm(v["sddmm_indptr"], v["sddmm_indices"], v["sddmm_mask"], M, N, R, C, v["sddmm_x"],
                   v["sddmm_y"]), v["sddmm_golden"])
+
+
+# ---------------------------------------------------------------------------
+# SpGEMM golden (sparse_common/bsr_matrix.hpp:741-810): BSR x BSR -> BSR
+def _spgemm(a, b, mutation=0):
+    return orc.spgemm(a.indptr, a.indices, a.data, a.H, a.R, a.C, b.indptr, b.indices, b.data, b.W, b.C,
+                      mutation=mutation)
+
+
+def _pattern(s):
+    p = np.zeros((s.H // s.R, s.W // s.C), np.int64)
+    for i in range(s.nbrows):
+        for blk in range(s.indptr[i], s.indptr[i + 1]):
+            p[i, s.indices[blk]] += 1
+    return p
+
+
+def _brute_spgemm(a, b):
+    """float64 dense product of every stored block (duplicates summed) and the
+    fp32 accumulation bound of the golden: (pairs * C) * 2^-23 * |A||B|."""
+    def dense(s):
+        d = np.zeros((s.H, s.W))
+        v = W.bf16_to_f32(s.data).astype(np.float64).reshape(-1, s.R, s.C)
+        for i in range(s.nbrows):
+            for blk in range(s.indptr[i], s.indptr[i + 1]):
+                j = s.indices[blk]
+                d[i * s.R:(i + 1) * s.R, j * s.C:(j + 1) * s.C] += v[blk]
+        return d
+    ad, bd = dense(a), dense(b)
+    pairs = max(1, int((_pattern(a) @ _pattern(b)).max(initial=0)))
+    return ad @ bd, pairs * a.C * 2.0 ** -23 * (np.abs(ad) @ np.abs(bd)) + 1e-30
+
+
+def _spgemm_checks_pass(a, b, got) -> bool:
+    """Structure equals the boolean product of the block patterns, columns
+    ascending per row; every stored value within the bound of the float64
+    product; every product entry outside the structure is zero."""
+    indptr, indices, vals = got
+    want = (_pattern(a) @ _pattern(b)) > 0
+    nbr, nbc = want.shape
+    R, BC = a.R, b.C
+    if indptr.size != nbr + 1 or indptr[-1] != indices.size or vals.size != indices.size * R * BC:
+        return False
+    ref, bound = _brute_spgemm(a, b)
+    covered = np.zeros((a.H, b.W), bool)
+    for i in range(nbr):
+        cols = indices[indptr[i]:indptr[i + 1]]
+        if not np.array_equal(cols, np.flatnonzero(want[i])):
+            return False
+        for n, j in enumerate(cols):
+            blk = vals[(indptr[i] + n) * R * BC:(indptr[i] + n + 1) * R * BC].reshape(R, BC).astype(np.float64)
+            sl = (slice(i * R, (i + 1) * R), slice(j * BC, (j + 1) * BC))
+            covered[sl] = True
+            if not np.all(np.abs(blk - ref[sl]) <= bound[sl]):
+                return False
+    return bool(np.all(ref[~covered] == 0))
+
+
+def test_spgemm_block_identity_returns_a():
+    """B = block-diagonal identity: every output block is one A block times I,
+    an exact product (one nonzero term per element)."""
+    a = _rand_bsr(128, 192, 32, 32, 9, 41)
+    b = W.fill_diag(192, 192, 32, 32, 6)
+    b.data = W.block_content(6, 32, 32, "ID")
+    indptr, indices, vals = _spgemm(a, b)
+    np.testing.assert_array_equal(indptr, a.indptr)
+    np.testing.assert_array_equal(indices, a.indices)
+    np.testing.assert_array_equal(vals, W.bf16_to_f32(a.data))
+
+
+def test_spgemm_uniform_closed_form():
+    """All-ones blocks: output element = (pairs contributing) * C exactly."""
+    a = W.fill_row(64, 128, 32, 32, 6)     # rows 0: cols 0..3, row 1: cols 0,1
+    a.data = W.block_content(6, 32, 32, "UNIFORM")
+    b = W.fill_diag(128, 128, 32, 32, 4)
+    b.data = W.block_content(4, 32, 32, "UNIFORM")
+    indptr, indices, vals = _spgemm(a, b)
+    np.testing.assert_array_equal(indptr, [0, 4, 6])
+    np.testing.assert_array_equal(indices, [0, 1, 2, 3, 0, 1])
+    np.testing.assert_array_equal(vals, np.full(6 * 1024, 32.0, np.float32))
+
+
+@pytest.mark.parametrize("R,C,BC", [(32, 32, 32), (64, 32, 32), (32, 64, 32), (32, 32, 64), (64, 64, 32)])
+def test_spgemm_brute_force(R, C, BC):
+    a = _rand_bsr(4 * R, 6 * C, R, C, 9, R + 7 * C)
+    b = _rand_bsr(6 * C, 5 * BC, C, BC, 12, 3 * R + BC)
+    assert _spgemm_checks_pass(a, b, _spgemm(a, b))
+
+
+def test_spgemm_duplicates_and_empty_rows():
+    """A duplicate (row, column) block contributes once per stored copy, as in
+    the golden's loop; an empty block row of A gives an empty output row."""
+    rng = np.random.default_rng(5)
+    a = W.BsrArrays(128, 96, 32, 32, np.array([0, 3, 3, 4, 5], np.int32), np.array([2, 0, 2, 1, 1], np.int32))
+    a.data = W.bf16_from_f32(W.uniform_f32(rng, 5 * 1024))
+    b = _rand_bsr(96, 128, 32, 32, 5, 6)
+    got = _spgemm(a, b)
+    assert got[0][2] == got[0][1]
+    assert _spgemm_checks_pass(a, b, got)
+
+
+def test_spgemm_structure_from_pattern_not_values():
+    """Zero-valued blocks still make output blocks (the golden marks presence
+    from the structure alone, :763-766)."""
+    a = W.fill_diag(64, 64, 32, 32, 2)
+    a.data = np.zeros(2 * 1024, np.uint16)
+    b = W.fill_row(64, 64, 32, 32, 4)
+    b.data = W.block_content(4, 32, 32, "UNIFORM")
+    indptr, indices, vals = _spgemm(a, b)
+    np.testing.assert_array_equal(indptr, [0, 2, 4])
+    np.testing.assert_array_equal(indices, [0, 1, 0, 1])
+    assert np.all(vals == 0)
+
+
+@pytest.mark.parametrize("mutation", [1, 2, 3, 4])
+def test_spgemm_checks_catch_planted_mistakes(mutation):
+    """1 B block transposed, 2 last A block of each row skipped, 3 output
+    column shifted, 4 first c term dropped."""
+    a = _rand_bsr(128, 128, 32, 32, 8, 21)
+    b = _rand_bsr(128, 128, 32, 32, 8, 22)
+    assert _spgemm_checks_pass(a, b, _spgemm(a, b))
+    assert not _spgemm_checks_pass(a, b, _spgemm(a, b, mutation=mutation))
