@@ -12,6 +12,8 @@
  *          replaces SDDMMHostCodeFunctionPtr,
  *          block_sddmm/inc/host_code.hpp:104-115
  *          (bsr_sddmm_multicore_naive / _CDA, :43-69)
+ *   SpGEMM C = A * B      A, B, C: BSR; a device path for the CPU routine
+ *          bsr_matrix<T>::spgemm, sparse_common/bsr_matrix.hpp:741-810
  *
  * Data layout is the reference's untilized host layout: dense matrices are
  * row-major, BSR blocks are R x C row-major in CSR order with int32 indptr
@@ -51,7 +53,7 @@
 extern "C" {
 #endif
 
-#define BSP_ABI_VERSION 2
+#define BSP_ABI_VERSION 3
 
 typedef enum bsp_status {
     BSP_OK = 0,
@@ -89,16 +91,19 @@ typedef struct bsp_plan bsp_plan;
 
 /* Schedule summary of a plan (for tests and the bench report). */
 typedef struct bsp_plan_info {
-    int32_t kind;        /* 1 = SpMM, 2 = SDDMM, 3 = fused attention pair */
+    int32_t kind;        /* 1 = SpMM, 2 = SDDMM, 3 = fused attention pair,
+                            4 = SpGEMM */
     int32_t tile_n;      /* SpMM: output columns per workgroup */
     int32_t n_tiles;     /* SpMM: N / tile_n */
-    int32_t n_items;     /* work items (row pieces / mask-row chunks) */
+    int32_t n_items;     /* work items (row pieces / mask-row chunks /
+                            SpGEMM output 32x32 sub-blocks) */
     int32_t n_entries;   /* 32x32 sub-block products listed in the schedule */
     int32_t n_split_rows;/* SpMM: rows cut into several pieces */
     int32_t n_slots;     /* SpMM: partial-result slots used by split rows */
     int32_t grid;        /* workgroups per launch */
     int32_t max_item_entries;
-    int32_t stages;      /* SpMM: depth of the LDS ring (entries in flight + 1) */
+    int32_t stages;      /* SpMM, SpGEMM: depth of the LDS ring (entries in
+                            flight + 1) */
     int32_t group;       /* SpMM: 32-row stripes of one block row per workgroup
                             (1; or 2, 4, 8 for blocks of R >= 64) */
     int32_t reserved;
@@ -174,6 +179,36 @@ int bsp_attention(const bsp_plan* plan, const uint16_t* mask_vals, const uint16_
                   const uint16_t* k, int64_t ldk, const uint16_t* v, int64_t ldv, void* out,
                   int64_t ldo, void* stream);
 
+/* ---- SpGEMM: C = A * B, A and B BSR, C BSR -----------------------------------
+ * The reference has this product only as a CPU routine (bsr_matrix<T>::spgemm,
+ * sparse_common/bsr_matrix.hpp:741-810, which the tests' golden uses); there is
+ * no device operator to replace.  Same contract: A is H x W in R x C blocks,
+ * B is W x N in C x BC blocks (A.W == B.H and A.C == B.R, as :742-743
+ * assert); C is H x N in R x BC blocks.  C(i, j) is stored iff some stored
+ * A(i, k) meets some stored B(k, j) -- decided by the structures, not the
+ * values -- with each block row's columns ascending (:786-801).  Duplicate
+ * blocks contribute once per stored copy.  R, C and BC multiples of 32.
+ *
+ * Symbolic phase, host only (no device): C's structure.  Call with NULL
+ * indptr/indices to get *nblocks, then with indptr[H/R + 1] and
+ * indices[*nblocks]. */
+int bsp_spgemm_symbolic(const bsp_bsr_desc* a, const bsp_bsr_desc* b, int64_t* nblocks,
+                        int32_t* indptr, int32_t* indices);
+
+/* Plan: the symbolic phase plus the per-sub-block product lists, uploaded to
+ * `device`.  bsp_spgemm_structure copies the plan's C structure (same two-call
+ * rule as bsp_spgemm_symbolic). */
+int bsp_spgemm_plan_create(bsp_plan** plan, const bsp_bsr_desc* a, const bsp_bsr_desc* b,
+                           int out_dtype, int device);
+int bsp_spgemm_structure(const bsp_plan* plan, int64_t* nblocks, int32_t* indptr,
+                         int32_t* indices);
+
+/* Numeric phase on `stream`.  a_vals: device, A.nblocks*R*C bf16; b_vals:
+ * device, B.nblocks*C*BC bf16 (both 16-byte aligned); out_vals: device,
+ * nblocks*R*BC, fp32 or bf16 as planned, every value written. */
+int bsp_spgemm(const bsp_plan* plan, const uint16_t* a_vals, const uint16_t* b_vals, void* out_vals,
+               void* stream);
+
 int bsp_plan_info_get(const bsp_plan* plan, bsp_plan_info* info);
 int bsp_plan_destroy(bsp_plan* plan);
 
@@ -210,6 +245,15 @@ int bsp_host_spmm(const bsp_bsr_desc* a, const uint16_t* a_vals, const uint16_t*
  * (K x N), both row-major bf16; out_vals receives nblocks*R*C values. */
 int bsp_host_sddmm(const bsp_bsr_desc* mask, const uint16_t* mask_vals, const uint16_t* x,
                    const uint16_t* y, int64_t K, void* out_vals, int out_dtype, int device);
+
+/* bsp_host_spgemm: bsr_matrix<T>::spgemm (sparse_common/bsr_matrix.hpp
+ * :741-810) with host arrays and the device doing the products: a_vals
+ * (A.nblocks*R*C bf16), b_vals (B.nblocks*C*BC bf16).  The caller sizes the
+ * output from bsp_spgemm_symbolic: out_indptr[H/R + 1], out_indices[nblocks],
+ * out_vals[nblocks*R*BC] (fp32 or bf16). */
+int bsp_host_spgemm(const bsp_bsr_desc* a, const uint16_t* a_vals, const bsp_bsr_desc* b,
+                    const uint16_t* b_vals, int32_t* out_indptr, int32_t* out_indices,
+                    void* out_vals, int out_dtype, int device);
 
 #ifdef __cplusplus
 }

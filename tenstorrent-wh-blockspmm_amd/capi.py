@@ -16,7 +16,7 @@ import numpy as np
 PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = PKG_DIR / "libbsparse.so"
 
-ABI_VERSION = 2  # BSP_ABI_VERSION of include/bsparse.h
+ABI_VERSION = 3  # BSP_ABI_VERSION of include/bsparse.h
 BSP_OK = 0
 BSP_ERR_INVALID_ARGUMENT = 1
 BSP_ERR_BAD_STRUCTURE = 2
@@ -88,6 +88,11 @@ SIGNATURES = {
     "bsp_sddmm_schedule": (c_int, [_DESC_P, c_int64, c_int, _INFO_P, _I32P, _I32P, _I64P, _I32P]),
     "bsp_host_spmm": (c_int, [_DESC_P, c_void_p, c_void_p, c_int64, c_void_p, c_int, c_int]),
     "bsp_host_sddmm": (c_int, [_DESC_P, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int, c_int]),
+    "bsp_spgemm_symbolic": (c_int, [_DESC_P, _DESC_P, _I64P, _I32P, _I32P]),
+    "bsp_spgemm_plan_create": (c_int, [POINTER(c_void_p), _DESC_P, _DESC_P, c_int, c_int]),
+    "bsp_spgemm_structure": (c_int, [c_void_p, _I64P, _I32P, _I32P]),
+    "bsp_spgemm": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "bsp_host_spgemm": (c_int, [_DESC_P, c_void_p, _DESC_P, c_void_p, _I32P, _I32P, c_void_p, c_int, c_int]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -266,6 +271,45 @@ class AttentionPlan(_Plan):
                                    _ptr(v), ldv or d, _ptr(out), ldo or d, stream))
 
 
+def _structure(fn, nbrows: int, *args):
+    """Runs a two-call structure query (NULL arrays for the size, then the
+    arrays) and returns (indptr, indices)."""
+    n = c_int64(0)
+    null32 = ctypes.cast(None, _I32P)
+    check(fn(*args, ctypes.byref(n), null32, null32))
+    indptr = np.zeros(nbrows + 1, np.int32)
+    indices = np.zeros(max(n.value, 1), np.int32)
+    check(fn(*args, ctypes.byref(n), indptr.ctypes.data_as(_I32P), indices.ctypes.data_as(_I32P)))
+    return indptr, indices[: n.value]
+
+
+def spgemm_symbolic(a: Bsr, b: Bsr) -> Bsr:
+    """Structure of A * B (host only): a Bsr of H x B.W in R x B.C blocks."""
+    da, db = a.desc(), b.desc()
+    indptr, indices = _structure(load().bsp_spgemm_symbolic, a.nbrows, ctypes.byref(da), ctypes.byref(db))
+    return Bsr(a.H, b.W, a.R, b.C, indptr, indices)
+
+
+class SpgemmPlan(_Plan):
+    """Plan for C = A * B with A, B and C in BSR; `structure` is C's."""
+
+    def __init__(self, a: Bsr, b: Bsr, out_dtype="f32", device: int = 0):
+        super().__init__()
+        self.a, self.b, self.out_dtype = a, b, _dtype_code(out_dtype)
+        da, db = a.desc(), b.desc()
+        check(load().bsp_spgemm_plan_create(ctypes.byref(self._h), ctypes.byref(da), ctypes.byref(db),
+                                            self.out_dtype, device))
+        indptr, indices = _structure(load().bsp_spgemm_structure, a.nbrows, self.handle)
+        self.structure = Bsr(a.H, b.W, a.R, b.C, indptr, indices)
+
+    @property
+    def out_values(self) -> int:
+        return self.structure.nblocks * self.a.R * self.b.C
+
+    def run(self, a_vals, b_vals, out_vals, stream: Optional[int] = None) -> None:
+        check(load().bsp_spgemm(self.handle, _ptr(a_vals), _ptr(b_vals), _ptr(out_vals), stream))
+
+
 def _schedule(fn_name: str, bsr: Bsr, n: int, num_cus: int) -> dict:
     lib = load()
     fn = getattr(lib, fn_name)
@@ -322,3 +366,21 @@ def host_sddmm(mask: Bsr, mask_vals: np.ndarray, x: np.ndarray, y: np.ndarray, o
     check(load().bsp_host_sddmm(ctypes.byref(d), mask_vals.ctypes.data, x.ctypes.data, y.ctypes.data, K,
                                 out.ctypes.data, code, device))
     return out
+
+
+def host_spgemm(a: Bsr, a_vals: np.ndarray, b: Bsr, b_vals: np.ndarray, out_dtype="f32", device: int = 0):
+    """Blocking host-buffer SpGEMM (bsr_matrix<T>::spgemm's shape): returns
+    (structure Bsr, block values)."""
+    code = _dtype_code(out_dtype)
+    st = spgemm_symbolic(a, b)
+    a_vals = np.ascontiguousarray(a_vals, dtype=np.uint16)
+    b_vals = np.ascontiguousarray(b_vals, dtype=np.uint16)
+    indptr = np.zeros(a.nbrows + 1, np.int32)
+    indices = np.zeros(max(st.nblocks, 1), np.int32)
+    out = np.empty(max(st.nblocks * a.R * b.C, 1), np.float32 if code == DTYPE_F32 else np.uint16)
+    da, db = a.desc(), b.desc()
+    check(load().bsp_host_spgemm(ctypes.byref(da), a_vals.ctypes.data, ctypes.byref(db), b_vals.ctypes.data,
+                                 indptr.ctypes.data_as(_I32P), indices.ctypes.data_as(_I32P), out.ctypes.data,
+                                 code, device))
+    return Bsr(a.H, b.W, a.R, b.C, indptr, indices[: st.nblocks]), out[: st.nblocks * a.R * b.C]
+

@@ -13,7 +13,7 @@
 #include "bsparse.h"
 
 struct bsp_plan {
-    int kind = 0;  // 1 SpMM, 2 SDDMM, 3 fused attention pair
+    int kind = 0;  // 1 SpMM, 2 SDDMM, 3 fused attention pair, 4 SpGEMM
     int device = 0;
     int out_dtype = BSP_DTYPE_F32;
     int layout = BSP_ROW_MAJOR;
@@ -24,6 +24,11 @@ struct bsp_plan {
     int64_t* d_ent_off = nullptr;   // SDDMM: output offset per entry; SpMM: packed entries
     bsp::SpmmSplit* d_splits = nullptr;
     float* d_ws = nullptr;
+    // SpGEMM: B's block count and width, C's structure, product lists.
+    int64_t b_nblocks = 0, BC = 0;
+    std::vector<int32_t> out_indptr, out_indices;
+    uint64_t* d_terms = nullptr;
+    int32_t* d_xcd = nullptr;
 };
 
 namespace {
@@ -68,6 +73,10 @@ void free_plan_buffers(bsp_plan* p) {
     if (p->d_ent_off) (void)hipFree(p->d_ent_off);
     if (p->d_splits) (void)hipFree(p->d_splits);
     if (p->d_ws) (void)hipFree(p->d_ws);
+    if (p->d_terms) (void)hipFree(p->d_terms);
+    if (p->d_xcd) (void)hipFree(p->d_xcd);
+    p->d_terms = nullptr;
+    p->d_xcd = nullptr;
     p->d_wgs = nullptr;
     p->d_ent_row = nullptr;
     p->d_ent_off = nullptr;
@@ -429,6 +438,106 @@ int bsp_sddmm(const bsp_plan* p, const uint16_t* mask_vals, const uint16_t* x, i
     return BSP_OK;
 }
 
+int bsp_spgemm_symbolic(const bsp_bsr_desc* a, const bsp_bsr_desc* b, int64_t* nblocks, int32_t* indptr,
+                        int32_t* indices) {
+    if (!nblocks) return fail(BSP_ERR_INVALID_ARGUMENT, "nblocks is null");
+    std::vector<int32_t> ip, ix;
+    std::string msg;
+    int st = bsp::spgemm_symbolic(a, b, ip, ix, msg);
+    if (st != BSP_OK) return fail(st, msg);
+    *nblocks = (int64_t)ix.size();
+    if (indptr) std::memcpy(indptr, ip.data(), ip.size() * sizeof(int32_t));
+    if (indices && !ix.empty()) std::memcpy(indices, ix.data(), ix.size() * sizeof(int32_t));
+    return BSP_OK;
+}
+
+int bsp_spgemm_plan_create(bsp_plan** out, const bsp_bsr_desc* a, const bsp_bsr_desc* b, int out_dtype,
+                           int device) {
+    if (!out) return fail(BSP_ERR_INVALID_ARGUMENT, "plan output pointer is null");
+    *out = nullptr;
+    if (out_dtype != BSP_DTYPE_F32 && out_dtype != BSP_DTYPE_BF16)
+        return fail(BSP_ERR_INVALID_ARGUMENT, "out_dtype must be BSP_DTYPE_F32 or BSP_DTYPE_BF16");
+    bsp::SpgemmSchedule s;
+    std::string msg;
+    int st = bsp::build_spgemm_schedule(a, b, s, msg);
+    if (st != BSP_OK) return fail(st, msg);
+    st = check_device(device);
+    if (st != BSP_OK) return st;
+
+    DeviceGuard g(device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    bsp_plan* p = new bsp_plan();
+    p->kind = 4;
+    p->device = device;
+    p->out_dtype = out_dtype;
+    p->M = a->H;
+    p->K = a->W;
+    p->N = b->W;
+    p->R = a->R;
+    p->C = a->C;
+    p->BC = b->C;
+    p->nblocks = a->nblocks;
+    p->b_nblocks = b->nblocks;
+    p->out_indptr = std::move(s.indptr);
+    p->out_indices = std::move(s.indices);
+    bsp_plan_info& info = p->info;
+    info.kind = 4;
+    info.tile_n = bsp::kSub;
+    info.n_tiles = 1;
+    info.n_items = (int32_t)s.tasks.size();
+    info.n_entries = (int32_t)s.terms.size();
+    info.grid = s.grid;
+    info.max_item_entries = s.max_task_terms;
+    info.stages = bsp::kSpgemmStages;
+    info.group = 1;
+    hipError_t e = upload((bsp::SpgemmTask**)&p->d_wgs, s.tasks);
+    if (e == hipSuccess) e = upload(&p->d_terms, s.terms);
+    if (e == hipSuccess) e = upload(&p->d_xcd, s.xcd_begin);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        free_plan_buffers(p);
+        delete p;
+        return hip_fail(e, "SpGEMM plan upload");
+    }
+    *out = p;
+    return BSP_OK;
+}
+
+int bsp_spgemm_structure(const bsp_plan* p, int64_t* nblocks, int32_t* indptr, int32_t* indices) {
+    if (!p || p->kind != 4) return fail(BSP_ERR_INVALID_ARGUMENT, "not an SpGEMM plan");
+    if (!nblocks) return fail(BSP_ERR_INVALID_ARGUMENT, "nblocks is null");
+    *nblocks = (int64_t)p->out_indices.size();
+    if (indptr) std::memcpy(indptr, p->out_indptr.data(), p->out_indptr.size() * sizeof(int32_t));
+    if (indices && !p->out_indices.empty())
+        std::memcpy(indices, p->out_indices.data(), p->out_indices.size() * sizeof(int32_t));
+    return BSP_OK;
+}
+
+int bsp_spgemm(const bsp_plan* p, const uint16_t* a_vals, const uint16_t* b_vals, void* out_vals, void* stream) {
+    if (!p || p->kind != 4) return fail(BSP_ERR_INVALID_ARGUMENT, "not an SpGEMM plan");
+    if (p->out_indices.empty()) return BSP_OK;
+    if (!a_vals || !b_vals || !out_vals) return fail(BSP_ERR_INVALID_ARGUMENT, "null device pointer");
+    if (!aligned16(a_vals) || !aligned16(b_vals))
+        return fail(BSP_ERR_INVALID_ARGUMENT, "A and B values must be 16-byte aligned");
+    const size_t esz = p->out_dtype == BSP_DTYPE_BF16 ? 2 : 4;
+    if (((uintptr_t)out_vals % esz) != 0) return fail(BSP_ERR_INVALID_ARGUMENT, "output values misaligned");
+    DeviceGuard g(p->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    bsp::SpgemmArgs args{};
+    args.a = a_vals;
+    args.b = b_vals;
+    args.out = out_vals;
+    args.tasks = (const bsp::SpgemmTask*)p->d_wgs;
+    args.terms = p->d_terms;
+    args.xcd_begin = p->d_xcd;
+    args.lda = (int32_t)p->C;
+    args.ldb = (int32_t)p->BC;
+    args.ldo = (int32_t)p->BC;
+    hipError_t e = bsp::launch_spgemm(args, p->out_dtype == BSP_DTYPE_BF16, p->info.grid, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "SpGEMM launch");
+    return BSP_OK;
+}
+
 int bsp_plan_info_get(const bsp_plan* p, bsp_plan_info* info) {
     if (!p || !info) return fail(BSP_ERR_INVALID_ARGUMENT, "null plan or info");
     *info = p->info;
@@ -518,6 +627,52 @@ int bsp_host_sddmm(const bsp_bsr_desc* mask, const uint16_t* mask_vals, const ui
     bsp_plan_destroy(p);
     if (st != BSP_OK) return st;
     if (e != hipSuccess) return hip_fail(e, "bsp_host_sddmm");
+    return BSP_OK;
+}
+
+int bsp_host_spgemm(const bsp_bsr_desc* a, const uint16_t* a_vals, const bsp_bsr_desc* b,
+                    const uint16_t* b_vals, int32_t* out_indptr, int32_t* out_indices, void* out_vals,
+                    int out_dtype, int device) {
+    if (!out_indptr || (a && a->nblocks > 0 && !a_vals) || (b && b->nblocks > 0 && !b_vals))
+        return fail(BSP_ERR_INVALID_ARGUMENT, "null host pointer");
+    bsp_plan* p = nullptr;
+    int st = bsp_spgemm_plan_create(&p, a, b, out_dtype, device);
+    if (st != BSP_OK) return st;
+    int64_t nb = 0;
+    bsp_spgemm_structure(p, &nb, out_indptr, nullptr);
+    if (nb == 0) {
+        bsp_plan_destroy(p);
+        return BSP_OK;
+    }
+    if (!out_indices || !out_vals) {
+        bsp_plan_destroy(p);
+        return fail(BSP_ERR_INVALID_ARGUMENT, "null host pointer");
+    }
+    bsp_spgemm_structure(p, &nb, out_indptr, out_indices);
+    DeviceGuard g(device);
+    const size_t esz = out_dtype == BSP_DTYPE_BF16 ? 2 : 4;
+    const size_t a_n = (size_t)a->nblocks * a->R * a->C, b_n = (size_t)b->nblocks * b->R * b->C;
+    const size_t o_n = (size_t)nb * a->R * b->C;
+    uint16_t *da = nullptr, *db = nullptr;
+    void* dout = nullptr;
+    hipError_t e = hipMalloc((void**)&da, a_n * 2);
+    if (e == hipSuccess) e = hipMalloc((void**)&db, b_n * 2);
+    if (e == hipSuccess) e = hipMalloc(&dout, o_n * esz);
+    if (e == hipSuccess) e = hipMemcpy(da, a_vals, a_n * 2, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(db, b_vals, b_n * 2, hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+        st = bsp_spgemm(p, da, db, dout, nullptr);
+        if (st == BSP_OK) {
+            e = hipDeviceSynchronize();
+            if (e == hipSuccess) e = hipMemcpy(out_vals, dout, o_n * esz, hipMemcpyDeviceToHost);
+        }
+    }
+    if (da) (void)hipFree(da);
+    if (db) (void)hipFree(db);
+    if (dout) (void)hipFree(dout);
+    bsp_plan_destroy(p);
+    if (st != BSP_OK) return st;
+    if (e != hipSuccess) return hip_fail(e, "bsp_host_spgemm");
     return BSP_OK;
 }
 

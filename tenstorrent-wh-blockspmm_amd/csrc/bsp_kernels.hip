@@ -890,6 +890,118 @@ __global__ __launch_bounds__(256) void sddmm_kernel(SddmmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// SpGEMM numeric phase, C = A * B with A, B and C in BSR (C's structure and
+// the product lists come from the plan).  One wave per 32x32 output
+// sub-block: it walks the sub-block's products through a wave-private ring
+// of S LDS stages (2 KB of A, then 2 KB of B, loaded global->LDS), reads A's
+// rows and B's columns (transpose reads) as MFMA operands, and stores the
+// sub-block once.  The waves of a workgroup never wait for each other (no
+// barriers), so each leaves when its sub-block is done.  Workgroup g runs on
+// XCD g % 8; XCD x takes the tasks [xcd_begin[x], xcd_begin[x+1]), four per
+// workgroup in order, so it works through whole output block rows and keeps
+// the A blocks they share in its L2.
+namespace spgemm_detail {
+constexpr int kStage = 4096;  // A sub-block (2 KB) + B sub-block (2 KB)
+constexpr int kPer = 4;       // global->LDS loads per wave per product
+}  // namespace spgemm_detail
+
+template <int S, bool OUT_BF16>
+__global__ __launch_bounds__(256) void spgemm_kernel(SpgemmArgs p) {
+    using namespace spmm_detail;
+    using namespace spgemm_detail;
+    static_assert(kPer * (S - 1) < 64, "vmcnt budget");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[4 * S * kStage];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int xcd = blockIdx.x % kNumXcd, slot = blockIdx.x / kNumXcd;
+    const int32_t t = load_const(p.xcd_begin + xcd) + 4 * slot + wave;
+    if (t >= load_const(p.xcd_begin + xcd + 1)) return;
+    const SpgemmTask task = load_const(p.tasks + t);
+    const int n = task.t_end - task.t_begin;
+    const int l32 = lane & 31, q = lane >> 5;
+    const uint32_t lds_w = lds_address(smem) + wave * S * kStage;
+    const uint8_t* smem_w = smem + wave * S * kStage;
+
+    // Loads of one product (two 1 KB instructions each for A and B):
+    //   A: instruction h, lane L loads row 8*(2h + L/32) + L%8, 16-byte chunk
+    //      (L%32)/8 into byte 1024h + 16L: 512-byte segments of 8 rows, chunk
+    //      j of row i at (8j + i) * 16 inside its segment.
+    //   B: instruction h, lane L loads row 16h + L/4, chunk L%4 into byte
+    //      1024h + 16L: plain row-major rows of 64 bytes.
+    int64_t a_goff[2], b_goff[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        a_goff[h] = (int64_t)(8 * (2 * h + (lane >> 5)) + (lane & 7)) * p.lda + 8 * ((lane & 31) >> 3);
+        b_goff[h] = (int64_t)(16 * h + (lane >> 2)) * p.ldb + 8 * (lane & 3);
+    }
+    // Product words are read with scalar loads one product ahead (a vector
+    // load would make the compiler wait for every outstanding load, the ring
+    // included, before its first use).
+    const uint64_t* terms = p.terms + task.t_begin;
+    int ni = 0;                           // next product to issue
+    uint64_t nw = load_const(terms);      // its word (every task has a product)
+    auto issue = [&](int stage) {
+        const uint64_t w = nw;
+        if (++ni < n) nw = load_const(terms + ni);
+        const uint16_t* ab = p.a + (int64_t)(uint32_t)w * 32;
+        const uint16_t* bb = p.b + (int64_t)(uint32_t)(w >> 32) * 32;
+        const uint32_t st = lds_w + stage * kStage;
+        gl_lds16(ab + a_goff[0], st);
+        gl_lds16(ab + a_goff[1], st + 1024);
+        gl_lds16(bb + b_goff[0], st + 2048);
+        gl_lds16(bb + b_goff[1], st + 3072);
+    };
+    // Operand reads: A row l32, chunk 2*s + q; B column l32 by transpose
+    // reads of rows 16*s + 8*q + 4*h + (lane%16)/4, columns 16*(lane/16 % 2)
+    // + 4*(lane%4).
+    const int a_rd = (l32 >> 3) * 512 + (8 * q + (l32 & 7)) * 16;  // + 256 * s
+    int b_rd[2][2];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int g = lane >> 4;
+            const int r = 16 * s2 + 8 * (g >> 1) + 4 * h + ((lane & 15) >> 2);
+            const int col = 16 * (g & 1) + 4 * (lane & 3);
+            b_rd[s2][h] = 2048 + r * 64 + 2 * col;
+        }
+
+    f32x16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < S - 1; ++e)
+        if (e < n) issue(e);
+    int stage = 0;  // stage of product k
+    for (int k = 0; k < n; ++k) {
+        // Product k+S-1 goes into the stage product k-1 used: this wave's
+        // reads of it are complete once lgkmcnt is 0.
+        if (k + S - 1 < n) {
+            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            issue(stage == 0 ? S - 1 : stage - 1);
+        }
+        wait_stages<kPer, S - 1>(min(S - 1, n - 1 - k));  // product k landed
+        const uint8_t* st = smem_w + stage * kStage;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            const u32x4 av = *(const u32x4*)(st + a_rd + 256 * s2);
+            const u32x4 lo = ld_tr_b16(st + b_rd[s2][0]);
+            const u32x4 hi = ld_tr_b16(st + b_rd[s2][1]);
+            acc = mfma32(av, u32x4{lo.x, lo.y, hi.x, hi.y}, acc);
+        }
+        stage = stage == S - 1 ? 0 : stage + 1;
+    }
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int64_t idx = task.out_off + (int64_t)(8 * (v >> 2) + 4 * q + (v & 3)) * p.ldo + l32;
+        if (OUT_BF16)
+            store_out(&((uint16_t*)p.out)[idx], f32_to_bf16_rne(acc[v]));
+        else
+            store_out(&((float*)p.out)[idx], acc[v]);
+    }
+}
+
+// ---------------------------------------------------------------------------
 template <int NTW, int S, int G>
 static void launch_spmm_t(const SpmmArgs& a, bool out_bf16, int grid, int n_split, hipStream_t stream) {
     if constexpr (G == 1) {
@@ -976,6 +1088,15 @@ hipError_t launch_sddmm(const SddmmArgs& a, bool y_colmajor, bool out_bf16, int 
         else
             launch_sddmm_t<false, false>(a, grid, stream);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_spgemm(const SpgemmArgs& a, bool out_bf16, int grid, hipStream_t stream) {
+    if (grid <= 0) return hipSuccess;
+    if (out_bf16)
+        hipLaunchKernelGGL((spgemm_kernel<kSpgemmStages, true>), dim3(grid), dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL((spgemm_kernel<kSpgemmStages, false>), dim3(grid), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -49,6 +49,19 @@ struct SddmmArgs {
     int32_t K;
 };
 
+struct SpgemmArgs {
+    const uint16_t* a;          // A block values (bf16), R x C blocks
+    const uint16_t* b;          // B block values (bf16), C x BC blocks
+    void* out;                  // C block values (fp32 or bf16), R x BC blocks
+    const SpgemmTask* tasks;    // one per 32x32 output sub-block
+    const uint64_t* terms;      // per product: A offset / 32 (low 32 bits) | B offset / 32 (high)
+    const int32_t* xcd_begin;   // kNumXcd + 1 task boundaries
+    int32_t lda;                // row stride inside an A block (= C)
+    int32_t ldb;                // row stride inside a B block (= BC)
+    int32_t ldo;                // row stride inside an output block (= BC)
+    int32_t pad;
+};
+
 // Floats of partial-result scratch per (slot, tile): a 32 x tile_n block.
 inline int64_t spmm_partial_floats(int tile_n) { return (int64_t)tile_n * 32; }
 
@@ -107,5 +120,10 @@ hipError_t launch_attention(const AttentionArgs& a, int head_dim, bool out_bf16,
 
 hipError_t launch_sddmm(const SddmmArgs& a, bool y_colmajor, bool out_bf16, int grid,
                         hipStream_t stream);
+
+// Ring depth of the SpGEMM kernel (products in flight + 1 per wave; LDS per
+// workgroup = 16 KB * stages).
+constexpr int kSpgemmStages = 4;
+hipError_t launch_spgemm(const SpgemmArgs& a, bool out_bf16, int grid, hipStream_t stream);
 
 }  // namespace bsp

@@ -357,4 +357,170 @@ int build_sddmm_schedule(const bsp_bsr_desc* m, int64_t K, int num_cus, SddmmSch
     return BSP_OK;
 }
 
+namespace {
+
+int check_spgemm_operands(const bsp_bsr_desc* a, const bsp_bsr_desc* b, std::string& msg) {
+    int st = validate_bsr(a, msg);
+    if (st != BSP_OK) {
+        msg = "A: " + msg;
+        return st;
+    }
+    st = validate_bsr(b, msg);
+    if (st != BSP_OK) {
+        msg = "B: " + msg;
+        return st;
+    }
+    // The golden asserts these (sparse_common/bsr_matrix.hpp:742-743).
+    if (a->W != b->H || a->C != b->R) {
+        msg = "A's columns and block width must equal B's rows and block height";
+        return BSP_ERR_INVALID_ARGUMENT;
+    }
+    if (a->R % kSub || a->C % kSub || b->C % kSub) {
+        msg = "block sizes must be multiples of 32";
+        return BSP_ERR_UNSUPPORTED;
+    }
+    return BSP_OK;
+}
+
+// Walks block row i of C: calls emit(j, pairs) for each output column j in
+// ascending order with the (A block, B block) pairs of C(i, j) in the
+// golden's order.  mark/cnt/pos are nbc-sized scratch (mark starts at -1).
+template <class Emit>
+void spgemm_row(const bsp_bsr_desc* a, const bsp_bsr_desc* b, int64_t i, std::vector<int64_t>& mark,
+                std::vector<int32_t>& cnt, std::vector<int64_t>& pos, std::vector<int32_t>& cols,
+                std::vector<std::pair<int32_t, int32_t>>& pairs, bool want_pairs, Emit&& emit) {
+    cols.clear();
+    int64_t npairs = 0;
+    for (int64_t ai = a->indptr[i]; ai < a->indptr[i + 1]; ++ai) {
+        const int64_t k = a->indices[ai];
+        for (int64_t bi = b->indptr[k]; bi < b->indptr[k + 1]; ++bi) {
+            const int32_t j = b->indices[bi];
+            if (mark[j] != i) {
+                mark[j] = i;
+                cnt[j] = 0;
+                cols.push_back(j);
+            }
+            ++cnt[j];
+            ++npairs;
+        }
+    }
+    std::sort(cols.begin(), cols.end());
+    if (want_pairs) {
+        int64_t run = 0;
+        for (int32_t j : cols) {
+            pos[j] = run;
+            run += cnt[j];
+        }
+        pairs.resize(npairs);
+        for (int64_t ai = a->indptr[i]; ai < a->indptr[i + 1]; ++ai) {
+            const int64_t k = a->indices[ai];
+            for (int64_t bi = b->indptr[k]; bi < b->indptr[k + 1]; ++bi)
+                pairs[pos[b->indices[bi]]++] = {(int32_t)ai, (int32_t)bi};
+        }
+    }
+    int64_t start = 0;
+    for (int32_t j : cols) {
+        emit(j, want_pairs ? pairs.data() + start : nullptr, cnt[j]);
+        start += cnt[j];
+    }
+}
+
+}  // namespace
+
+int spgemm_symbolic(const bsp_bsr_desc* a, const bsp_bsr_desc* b, std::vector<int32_t>& indptr,
+                    std::vector<int32_t>& indices, std::string& msg) {
+    int st = check_spgemm_operands(a, b, msg);
+    if (st != BSP_OK) return st;
+    const int64_t nbr = a->H / a->R, nbc = b->W / b->C;
+    std::vector<int64_t> mark(nbc, -1), pos;
+    std::vector<int32_t> cnt(nbc), cols;
+    std::vector<std::pair<int32_t, int32_t>> pairs;
+    indptr.assign(nbr + 1, 0);
+    indices.clear();
+    for (int64_t i = 0; i < nbr; ++i) {
+        spgemm_row(a, b, i, mark, cnt, pos, cols, pairs, false,
+                   [&](int32_t j, const std::pair<int32_t, int32_t>*, int32_t) { indices.push_back(j); });
+        if ((int64_t)indices.size() > INT32_MAX) {
+            msg = "output has more than 2^31 - 1 blocks";
+            return BSP_ERR_UNSUPPORTED;
+        }
+        indptr[i + 1] = (int32_t)indices.size();
+    }
+    return BSP_OK;
+}
+
+int build_spgemm_schedule(const bsp_bsr_desc* a, const bsp_bsr_desc* b, SpgemmSchedule& s, std::string& msg) {
+    int st = check_spgemm_operands(a, b, msg);
+    if (st != BSP_OK) return st;
+    const int64_t R = a->R, C = a->C, BC = b->C;
+    // Sub-block offsets are kept / 32 in 32 bits.
+    if (a->nblocks * R * C / kSub > (int64_t)UINT32_MAX || b->nblocks * C * BC / kSub > (int64_t)UINT32_MAX) {
+        msg = "A or B has more than 2^37 values";
+        return BSP_ERR_UNSUPPORTED;
+    }
+    const int64_t nbr = a->H / R, nbc = b->W / BC;
+    const int64_t RS = R / kSub, CS = C / kSub, PS = BC / kSub;
+    std::vector<int64_t> mark(nbc, -1), pos(nbc);
+    std::vector<int32_t> cnt(nbc), cols;
+    std::vector<std::pair<int32_t, int32_t>> pairs;
+    s = SpgemmSchedule{};
+    s.indptr.assign(nbr + 1, 0);
+    bool too_big = false;
+    for (int64_t i = 0; i < nbr && !too_big; ++i) {
+        spgemm_row(a, b, i, mark, cnt, pos, cols, pairs, true,
+                   [&](int32_t j, const std::pair<int32_t, int32_t>* pr, int32_t np) {
+                       const int64_t ob = (int64_t)s.indices.size();
+                       s.indices.push_back(j);
+                       if ((int64_t)s.terms.size() + (int64_t)np * CS * RS * PS > INT32_MAX) {
+                           too_big = true;
+                           return;
+                       }
+                       for (int64_t ra = 0; ra < RS; ++ra)
+                           for (int64_t pb = 0; pb < PS; ++pb) {
+                               SpgemmTask t{};
+                               t.out_off = ob * R * BC + ra * kSub * BC + pb * kSub;
+                               t.t_begin = (int32_t)s.terms.size();
+                               for (int32_t n = 0; n < np; ++n)
+                                   for (int64_t cs = 0; cs < CS; ++cs) {
+                                       const uint64_t ao = (uint64_t)pr[n].first * R * C + ra * kSub * C + cs * kSub;
+                                       const uint64_t bo =
+                                           (uint64_t)pr[n].second * C * BC + cs * kSub * BC + pb * kSub;
+                                       s.terms.push_back(ao / kSub | (bo / kSub) << 32);
+                                   }
+                               t.t_end = (int32_t)s.terms.size();
+                               s.max_task_terms = std::max(s.max_task_terms, t.t_end - t.t_begin);
+                               s.tasks.push_back(t);
+                           }
+                   });
+        if ((int64_t)s.indices.size() > INT32_MAX) too_big = true;
+        s.indptr[i + 1] = (int32_t)s.indices.size();
+    }
+    if (too_big || (int64_t)s.tasks.size() > INT32_MAX) {
+        msg = "product too large for int32 schedule fields";
+        return BSP_ERR_UNSUPPORTED;
+    }
+    s.nblocks = (int64_t)s.indices.size();
+    // Contiguous task ranges of about equal cost per XCD (products, plus the
+    // store counted as two products), so that an XCD works through whole
+    // output block rows and keeps their A blocks in its L2.
+    const int64_t ntask = (int64_t)s.tasks.size();
+    int64_t total = 0;
+    for (const SpgemmTask& t : s.tasks) total += (t.t_end - t.t_begin) + 2;
+    s.xcd_begin.assign(kNumXcd + 1, (int32_t)ntask);
+    s.xcd_begin[0] = 0;
+    int64_t acc = 0, t = 0;
+    for (int x = 1; x < kNumXcd; ++x) {
+        const int64_t target = total * x / kNumXcd;
+        while (t < ntask && acc < target) {
+            acc += (s.tasks[t].t_end - s.tasks[t].t_begin) + 2;
+            ++t;
+        }
+        s.xcd_begin[x] = (int32_t)t;
+    }
+    int64_t per = 0;
+    for (int x = 0; x < kNumXcd; ++x) per = std::max<int64_t>(per, (s.xcd_begin[x + 1] - s.xcd_begin[x] + 3) / 4);
+    s.grid = (int32_t)(per * kNumXcd);
+    return BSP_OK;
+}
+
 }  // namespace bsp

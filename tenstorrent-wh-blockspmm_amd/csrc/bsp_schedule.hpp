@@ -96,6 +96,37 @@ struct SddmmSchedule {
 // Per-workgroup items in launch order; idle slots get an empty range.
 std::vector<SddmmItem> sddmm_wg_records(const SddmmSchedule& s);
 
+// One SpGEMM wave task: a 32x32 output sub-block and its run of products.
+struct SpgemmTask {
+    int64_t out_off;  // element offset of the sub-block in the output values
+    int32_t t_begin;  // products [t_begin, t_end) of the term array
+    int32_t t_end;
+};
+static_assert(sizeof(SpgemmTask) == 16, "SpgemmTask layout is shared with the kernels");
+
+// SpGEMM C = A * B with A, B and C in BSR.  The symbolic phase: C's structure
+// (block (i, j) present iff some stored A(i, k) meets some stored B(k, j),
+// columns ascending per row, as bsr_matrix<T>::spgemm builds it,
+// sparse_common/bsr_matrix.hpp:741-810) and, per 32x32 output sub-block, its
+// products in the golden's order (A's CSR order, then B's, then the inner
+// 32-column steps of the shared dimension).
+struct SpgemmSchedule {
+    int64_t nblocks = 0;             // output blocks
+    std::vector<int32_t> indptr;     // output block-row pointers (H/R + 1)
+    std::vector<int32_t> indices;    // output block columns (nblocks)
+    std::vector<SpgemmTask> tasks;   // one per output sub-block, in output order
+    std::vector<uint64_t> terms;     // A sub-block offset / 32 | (B sub-block offset / 32) << 32
+    std::vector<int32_t> xcd_begin;  // kNumXcd + 1 task boundaries: XCD x runs tasks [x], [x+1)
+    int32_t max_task_terms = 0;
+    int32_t grid = 0;                // workgroups (four tasks each, kNumXcd-interleaved)
+};
+
+// Output structure only (no product lists).
+int spgemm_symbolic(const bsp_bsr_desc* a, const bsp_bsr_desc* b, std::vector<int32_t>& indptr,
+                    std::vector<int32_t>& indices, std::string& msg);
+// Structure, product lists and the XCD split.
+int build_spgemm_schedule(const bsp_bsr_desc* a, const bsp_bsr_desc* b, SpgemmSchedule& s, std::string& msg);
+
 // Structural checks of sparse_common/bsr_matrix.hpp:246-252 / :610-616 plus
 // the CSR invariants the golden relies on implicitly.  On failure returns a
 // bsp_status and fills `msg`.

@@ -312,6 +312,19 @@ def workload_sddmm(M=4096, N=4096, K=256, density=0.10, seed=SEED_BASE + 2) -> d
     return {"mask": mask, "x": x, "y": y, "M": M, "N": N, "K": K}
 
 
+def workload_spgemm(n=8192, block=32, density=0.05, seed=SEED_BASE + 6) -> dict:
+    """A and B n x n, block x block blocks at uniform-random positions with
+    `density` each, values U[-1, 1] bf16 (A * B with 32x32 blocks at 5%: about
+    47% of the output blocks are stored, 0.64 block pairs each on average)."""
+    rng = np.random.default_rng(seed)
+    nnzb = int(round(density * (n // block) ** 2))
+    a = random_positions(n, n, block, block, nnzb, rng)
+    a.data = bf16_from_f32(uniform_f32(rng, nnzb * block * block))
+    b = random_positions(n, n, block, block, nnzb, rng)
+    b.data = bf16_from_f32(uniform_f32(rng, nnzb * block * block))
+    return {"a": a, "b": b, "n": n, "block": block, "density": density}
+
+
 def workload_spmm_skewed() -> dict:
     """A 16384x16384, 32x32 blocks, Zipf(1.2) rows capped at 512, 2% mean
     density; B 16384x1024; U[-1,1]."""

@@ -176,3 +176,48 @@ def golden_attention(mask, q, k, v):
     s = golden_sddmm(mask, q, k, y_colmajor=True)
     a = W.BsrArrays(mask.H, mask.W, mask.R, mask.C, mask.indptr, mask.indices, W.bf16_from_f32(s))
     return golden_spmm(a, v), a
+
+
+def block_pattern(s) -> np.ndarray:
+    """Stored-block counts per (block row, block column) (duplicates counted)."""
+    p = np.zeros((s.H // s.R, s.W // s.C), np.int64)
+    rows = np.repeat(np.arange(s.H // s.R), np.diff(s.indptr))
+    np.add.at(p, (rows, s.indices), 1)
+    return p
+
+
+def spgemm_k_eff(a, b, structure) -> np.ndarray:
+    """Reduction length per output value of A*B: the (A, B) block pairs that
+    meet at the output block times the shared block width C."""
+    pairs = block_pattern(a) @ block_pattern(b)
+    rows = np.repeat(np.arange(structure.H // structure.R), np.diff(structure.indptr))
+    per_block = pairs[rows, structure.indices] * a.C
+    return np.repeat(per_block, a.R * b.C)
+
+
+def golden_spgemm(a, b):
+    """(indptr, indices, fp32 values) of the oracle's BSR x BSR product."""
+    return orc.spgemm(a.indptr, a.indices, a.data, a.H, a.R, a.C, b.indptr, b.indices, b.data, b.W, b.C)
+
+
+def run_spgemm(a, b, out_dtype="f32", plan=None, poison=True):
+    """A*B on the GPU: (structure as capi.Bsr, values widened to fp32)."""
+    import torch
+    own = plan is None
+    if own:
+        plan = capi.SpgemmPlan(bsr_of(a), bsr_of(b), out_dtype)
+    da, db = _dev_u16(a.data), _dev_u16(b.data)
+    nv = plan.out_values
+    if out_dtype == "f32":
+        do = torch.full((max(nv, 1),), float("nan") if poison else 0.0, dtype=torch.float32, device="cuda")
+    else:
+        do = torch.full((max(nv, 1),), 0x7FC0 if poison else 0, dtype=torch.int16, device="cuda")
+    plan.run(da, db, do, stream=torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    out = do.cpu().numpy()[:nv]
+    st = plan.structure
+    if own:
+        plan.close()
+    if out_dtype == "f32":
+        return st, out
+    return st, W.bf16_to_f32(out.view(np.uint16))

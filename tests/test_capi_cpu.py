@@ -42,7 +42,7 @@ def test_library_links_hip_and_has_gfx950_code():
 
 def test_abi_version_and_status_strings():
     lib = capi.load()
-    assert lib.bsp_abi_version() == capi.ABI_VERSION == 2
+    assert lib.bsp_abi_version() == capi.ABI_VERSION == 3
     for code, text in [(0, b"ok"), (2, b"malformed BSR structure"), (3, b"unsupported")]:
         assert lib.bsp_status_string(code) == text
 
@@ -97,6 +97,12 @@ def test_null_arguments():
         capi.BSP_ERR_INVALID_ARGUMENT
     assert lib.bsp_attention(None, None, None, 64, None, 64, None, 64, None, 64, None) == \
         capi.BSP_ERR_INVALID_ARGUMENT
+    assert lib.bsp_spgemm_plan_create(None, ctypes.byref(_bsr(**GOOD).desc()), ctypes.byref(_bsr(**GOOD).desc()),
+                                      0, 0) == capi.BSP_ERR_INVALID_ARGUMENT
+    assert lib.bsp_spgemm(None, None, None, None, None) == capi.BSP_ERR_INVALID_ARGUMENT
+    assert lib.bsp_spgemm_structure(None, None, None, None) == capi.BSP_ERR_INVALID_ARGUMENT
+    assert lib.bsp_spgemm_symbolic(ctypes.byref(_bsr(**GOOD).desc()), ctypes.byref(_bsr(**GOOD).desc()), None,
+                                   None, None) == capi.BSP_ERR_INVALID_ARGUMENT
     assert lib.bsp_plan_destroy(None) == capi.BSP_OK
     g = _bsr(**GOOD)
     assert lib.bsp_host_spmm(ctypes.byref(g.desc()), None, None, 64, None, 0, 0) == \
@@ -302,3 +308,63 @@ def test_spmm_schedule_row_groups(monkeypatch, group, R, C, split):
               for s in range(RS) for t in range(CS)]
     assert sorted(seen) == sorted(expect)
     assert len(slots) == info["n_slots"]
+
+
+# ---------------------------------------------------------------------------
+# SpGEMM symbolic phase (structure of A * B), host only.
+def _rand(H, Wd, R, C, nblocks, seed):
+    s = W.random_positions(H, Wd, R, C, nblocks, np.random.default_rng(seed))
+    return s, capi.Bsr(s.H, s.W, s.R, s.C, s.indptr, s.indices)
+
+
+@pytest.mark.parametrize("R,C,BC,na,nb", [(32, 32, 32, 20, 20), (64, 32, 32, 9, 30), (32, 64, 96, 14, 7),
+                                          (128, 64, 32, 3, 25), (32, 32, 32, 0, 10), (32, 32, 32, 40, 44)])
+def test_spgemm_symbolic_matches_oracle_structure(R, C, BC, na, nb):
+    from helpers import orc
+    a, ab = _rand(8 * R, 8 * C, R, C, na, R + na)
+    b, bb = _rand(8 * C, 6 * BC, C, BC, nb, BC + nb)
+    a.data = np.zeros(a.nblocks * R * C, np.uint16)
+    b.data = np.zeros(b.nblocks * C * BC, np.uint16)
+    indptr, indices, _ = orc.spgemm(a.indptr, a.indices, a.data, a.H, R, C, b.indptr, b.indices, b.data, b.W, BC)
+    st = capi.spgemm_symbolic(ab, bb)
+    assert (st.H, st.W, st.R, st.C) == (a.H, b.W, R, BC)
+    np.testing.assert_array_equal(st.indptr, indptr)
+    np.testing.assert_array_equal(st.indices, indices)
+
+
+def test_spgemm_symbolic_duplicates_and_empty():
+    a = _bsr([0, 2, 2, 3, 3], [1, 1, 3])                 # duplicate column 1 in row 0
+    b = _bsr([0, 0, 2, 2, 3], [3, 0, 2])
+    st = capi.spgemm_symbolic(a, b)
+    np.testing.assert_array_equal(st.indptr, [0, 2, 2, 3, 3])
+    np.testing.assert_array_equal(st.indices, [0, 3, 2])
+    empty = _bsr([0, 0, 0, 0, 0], [])
+    assert capi.spgemm_symbolic(empty, b).nblocks == 0
+    assert capi.spgemm_symbolic(a, empty).nblocks == 0
+
+
+def test_spgemm_rejects_mismatched_and_unsupported_operands():
+    lib = capi.load()
+    a = _bsr(**GOOD)
+    n = ctypes.c_int64()
+    cases = [
+        (capi.Bsr(96, 128, 32, 32, np.zeros(4, np.int32), np.zeros(0, np.int32)), capi.BSP_ERR_INVALID_ARGUMENT,
+         "rows"),                                                          # B.H != A.W
+        (capi.Bsr(128, 128, 64, 32, np.zeros(3, np.int32), np.zeros(0, np.int32)), capi.BSP_ERR_INVALID_ARGUMENT,
+         "block height"),                                                  # B.R != A.C
+        (capi.Bsr(128, 96, 32, 48, np.zeros(5, np.int32), np.zeros(0, np.int32)), capi.BSP_ERR_UNSUPPORTED,
+         "multiples of 32"),                                               # BC = 48
+        (_bsr(**BAD[0][1]), capi.BSP_ERR_BAD_STRUCTURE, "B: indptr[0]"),
+    ]
+    for b, status, msg in cases:
+        assert lib.bsp_spgemm_symbolic(ctypes.byref(a.desc()), ctypes.byref(b.desc()), ctypes.byref(n), None,
+                                       None) == status
+        assert msg in capi.last_error()
+        h = ctypes.c_void_p()
+        assert lib.bsp_spgemm_plan_create(ctypes.byref(h), ctypes.byref(a.desc()), ctypes.byref(b.desc()), 0,
+                                          0) == status
+        assert not h
+    assert lib.bsp_spgemm_symbolic(ctypes.byref(_bsr(**BAD[1][1]).desc()), ctypes.byref(a.desc()),
+                                   ctypes.byref(n), None, None) == capi.BSP_ERR_BAD_STRUCTURE
+    assert capi.last_error().startswith("A: ")
+
