@@ -53,7 +53,8 @@ def parse_args():
     p.add_argument("--copy-calibration", action="store_true",
                    help="first run a 256 MiB device copy and a 256 MiB elementwise multiply (kernels of known traffic, "
                         "for scaling FETCH_SIZE / WRITE_SIZE counters)")
-    p.add_argument("--only", default="", help="comma list of sections to run: head (25%% fp32 only), sweep, sddmm, skewed, attention, large, host")
+    p.add_argument("--only", default="", help="comma list of sections to run: head (25%% fp32 only), sweep, sddmm, skewed, attention, spgemm, "
+                   "large, host")
     return p.parse_args()
 
 
@@ -193,6 +194,42 @@ def bench_attention(torch, capi, W, w, out_dtype, steps, warmup):
     nbytes = (float(m.data.nbytes + q.nbytes + k.nbytes + v.nbytes) + 4.0 * (m.nblocks + m.nbrows + 1)
               + float(m.H) * d * out_bytes)
     return t, flops, nbytes
+
+
+def bench_spgemm(torch, capi, W, a, b, out_dtype, steps, warmup):
+    """Times the SpGEMM numeric phase on (a, b); FLOPs are 2*R*C*BC per
+    (A block, B block) pair, bytes are A's and B's values and index arrays
+    plus C's values."""
+    plan = capi.SpgemmPlan(capi.Bsr(a.H, a.W, a.R, a.C, a.indptr, a.indices),
+                           capi.Bsr(b.H, b.W, b.R, b.C, b.indptr, b.indices), out_dtype)
+    out_bytes = 4 if out_dtype == "f32" else 2
+    nv = plan.out_values
+    per_copy = a.data.nbytes + b.data.nbytes + nv * out_bytes
+    ncopy = max(1, -(-ROTATE_BYTES // per_copy))
+    da0, db0 = dev_u16(torch, a.data), dev_u16(torch, b.data)
+    copies = []
+    for _ in range(ncopy):
+        do = torch.empty(max(nv, 1), dtype=torch.float32 if out_dtype == "f32" else torch.int16, device="cuda")
+        copies.append((da0.clone(), db0.clone(), do))
+
+    def launch(i, stream):
+        da, db, do = copies[i % ncopy]
+        plan.run(da, db, do, stream=stream)
+
+    t = Timer(torch, steps).run(launch, steps, warmup)
+    info = plan.info()
+    nblocks = plan.structure.nblocks
+    plan.close()
+    del copies
+    pa = np.zeros((a.nbrows, a.W // a.C), np.int64)
+    np.add.at(pa, (np.repeat(np.arange(a.nbrows), np.diff(a.indptr)), a.indices), 1)
+    pb = np.zeros((b.nbrows, b.W // b.C), np.int64)
+    np.add.at(pb, (np.repeat(np.arange(b.nbrows), np.diff(b.indptr)), b.indices), 1)
+    pairs = int((pa @ pb).sum())
+    flops = 2.0 * pairs * a.R * a.C * b.C
+    nbytes = (float(a.data.nbytes + b.data.nbytes) + 4.0 * (a.nblocks + a.nbrows + 1 + b.nblocks + b.nbrows + 1)
+              + float(nv) * out_bytes)
+    return t, flops, nbytes, info, {"pairs": pairs, "out_blocks": nblocks}
 
 
 def summarize(t, flops, nbytes, steps):
@@ -371,6 +408,17 @@ def main():
                             "pair_tflops": round((f1 + f2) / ((t1["launch_ms"] + t2["launch_ms"]) * 1e-3)
                                                  / 1e12, 3),
                             "fused": summarize(t3, f3, b3, steps)}
+
+    if not only or "spgemm" in only:
+        w = W.workload_spgemm()
+        rows = []
+        for od in ("f32", "bf16"):
+            t, fl, nb, info, extra = bench_spgemm(torch, capi, W, w["a"], w["b"], od, steps, warmup)
+            rows.append({"out": od, **summarize(t, fl, nb, steps), "grid": info["grid"],
+                         "sub_blocks": info["n_items"], "products": info["n_entries"], **extra})
+        out["spgemm"] = {"workload": "SpGEMM C=A*B, A and B 8192x8192, 32x32 blocks, 5% each (3277 blocks)",
+                         "nnzb": w["a"].nblocks, "runs": rows}
+        del w
 
     if not only or "large" in only:
         # The reference's own published configuration: M = N = K = 8192 with

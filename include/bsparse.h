@@ -204,8 +204,8 @@ int bsp_spgemm_structure(const bsp_plan* plan, int64_t* nblocks, int32_t* indptr
                          int32_t* indices);
 
 /* Numeric phase on `stream`.  a_vals: device, A.nblocks*R*C bf16; b_vals:
- * device, B.nblocks*C*BC bf16 (both 16-byte aligned); out_vals: device,
- * nblocks*R*BC, fp32 or bf16 as planned, every value written. */
+ * device, B.nblocks*C*BC bf16; out_vals: device, nblocks*R*BC, fp32 or bf16
+ * as planned, every value written.  All three 16-byte aligned. */
 int bsp_spgemm(const bsp_plan* plan, const uint16_t* a_vals, const uint16_t* b_vals, void* out_vals,
                void* stream);
 

@@ -891,18 +891,21 @@ __global__ __launch_bounds__(256) void sddmm_kernel(SddmmArgs p) {
 
 // ---------------------------------------------------------------------------
 // SpGEMM numeric phase, C = A * B with A, B and C in BSR (C's structure and
-// the product lists come from the plan).  One wave per 32x32 output
-// sub-block: it walks the sub-block's products through a wave-private ring
-// of S LDS stages (2 KB of A, then 2 KB of B, loaded global->LDS), reads A's
-// rows and B's columns (transpose reads) as MFMA operands, and stores the
-// sub-block once.  The waves of a workgroup never wait for each other (no
-// barriers), so each leaves when its sub-block is done.  Workgroup g runs on
-// XCD g % 8; XCD x takes the tasks [xcd_begin[x], xcd_begin[x+1]), four per
-// workgroup in order, so it works through whole output block rows and keeps
-// the A blocks they share in its L2.
+// the product lists come from the plan).  The unit of output is a 32x32
+// sub-block (a task) with its run of products; a wave takes a contiguous
+// run of tasks (at most 64) and streams all their products through one
+// wave-private ring of S LDS stages (2 KB of A, then 2 KB of B, loaded
+// global->LDS), so the ring stays full across sub-block boundaries.  At the
+// last product of a task the wave stores the sub-block and clears its
+// accumulators.  Waves never wait for each other (no barriers).  Run slot
+// (x * wg_per_xcd + j) * 4 + wave belongs to workgroup j * 8 + x, which runs
+// on XCD x; the plan puts there the runs of one region of the output (a
+// band of block rows crossed with a band of block columns), so the XCD's L2
+// holds the A and B blocks the region shares.
 namespace spgemm_detail {
-constexpr int kStage = 4096;  // A sub-block (2 KB) + B sub-block (2 KB)
-constexpr int kPer = 4;       // global->LDS loads per wave per product
+constexpr int kStage = kSpgemmStageBytes;  // A sub-block (2 KB) + B sub-block (2 KB)
+constexpr int kPer = 4;                    // global->LDS loads per wave per product
+constexpr int kWords = 128;                // product words held in registers (two per lane)
 }  // namespace spgemm_detail
 
 template <int S, bool OUT_BF16>
@@ -914,13 +917,47 @@ __global__ __launch_bounds__(256) void spgemm_kernel(SpgemmArgs p) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int xcd = blockIdx.x % kNumXcd, slot = blockIdx.x / kNumXcd;
-    const int32_t t = load_const(p.xcd_begin + xcd) + 4 * slot + wave;
-    if (t >= load_const(p.xcd_begin + xcd + 1)) return;
-    const SpgemmTask task = load_const(p.tasks + t);
-    const int n = task.t_end - task.t_begin;
+    const int id = (xcd * p.wg_per_xcd + slot) * 4 + wave;
+    const SpgemmRun run = load_const(p.runs + id);
+    const int32_t t0 = run.t0, t1 = run.t1, p0 = run.p0;
+    if (t0 >= t1) return;
+    const int n = run.p1 - p0;  // products of the run (>= 1 per task)
     const int l32 = lane & 31, q = lane >> 5;
     const uint32_t lds_w = lds_address(smem) + wave * S * kStage;
     const uint8_t* smem_w = smem + wave * S * kStage;
+
+    // Lane j holds task t0 + j (output offset, end of its products relative
+    // to the run) and product words kWords * c + 64 * h + j of the current
+    // chunk c, h = 0, 1.  All are loaded, and waited for, before the ring
+    // starts; a run of more than kWords products reloads the words in the
+    // (rare) issue that crosses a chunk and waits for them there.  No load is
+    // then pending anywhere in the loop (the compiler would otherwise wait
+    // for every outstanding load, the ring included, before a use).
+    uint32_t off_lo = 0, off_hi = 0;
+    int32_t t_end = 0;
+    if (t0 + lane < t1) {
+        const SpgemmTask tk = p.tasks[t0 + lane];
+        off_lo = (uint32_t)tk.out_off;
+        off_hi = (uint32_t)(tk.out_off >> 32);
+        t_end = tk.t_end - p0;
+    }
+    const uint64_t* terms = p.terms + p0;
+    uint32_t w_lo0 = 0, w_hi0 = 0, w_lo1 = 0, w_hi1 = 0;
+    auto fetch_words = [&](int base) {
+        if (base + lane < n) {
+            const uint64_t w = terms[base + lane];
+            w_lo0 = (uint32_t)w;
+            w_hi0 = (uint32_t)(w >> 32);
+        }
+        if (base + 64 + lane < n) {
+            const uint64_t w = terms[base + 64 + lane];
+            w_lo1 = (uint32_t)w;
+            w_hi1 = (uint32_t)(w >> 32);
+        }
+        __asm__ volatile("" : "+v"(w_lo0), "+v"(w_hi0), "+v"(w_lo1), "+v"(w_hi1));
+    };
+    fetch_words(0);
+    __asm__ volatile("" : "+v"(off_lo), "+v"(off_hi), "+v"(t_end));
 
     // Loads of one product (two 1 KB instructions each for A and B):
     //   A: instruction h, lane L loads row 8*(2h + L/32) + L%8, 16-byte chunk
@@ -928,76 +965,89 @@ __global__ __launch_bounds__(256) void spgemm_kernel(SpgemmArgs p) {
     //      j of row i at (8j + i) * 16 inside its segment.
     //   B: instruction h, lane L loads row 16h + L/4, chunk L%4 into byte
     //      1024h + 16L: plain row-major rows of 64 bytes.
-    int64_t a_goff[2], b_goff[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        a_goff[h] = (int64_t)(8 * (2 * h + (lane >> 5)) + (lane & 7)) * p.lda + 8 * ((lane & 31) >> 3);
-        b_goff[h] = (int64_t)(16 * h + (lane >> 2)) * p.ldb + 8 * (lane & 3);
-    }
-    // Product words are read with scalar loads one product ahead (a vector
-    // load would make the compiler wait for every outstanding load, the ring
-    // included, before its first use).
-    const uint64_t* terms = p.terms + task.t_begin;
-    int ni = 0;                           // next product to issue
-    uint64_t nw = load_const(terms);      // its word (every task has a product)
-    auto issue = [&](int stage) {
-        const uint64_t w = nw;
-        if (++ni < n) nw = load_const(terms + ni);
-        const uint16_t* ab = p.a + (int64_t)(uint32_t)w * 32;
-        const uint16_t* bb = p.b + (int64_t)(uint32_t)(w >> 32) * 32;
+    int64_t a_goff0, a_goff1, b_goff0, b_goff1;
+    a_goff0 = (int64_t)(8 * (lane >> 5) + (lane & 7)) * p.lda + 8 * ((lane & 31) >> 3);
+    a_goff1 = a_goff0 + (int64_t)16 * p.lda;
+    b_goff0 = (int64_t)(lane >> 2) * p.ldb + 8 * (lane & 3);
+    b_goff1 = b_goff0 + (int64_t)16 * p.ldb;
+    auto issue = [&](int e, int stage) {
+        if ((e & (kWords - 1)) == 0 && e > 0) fetch_words(e);
+        const bool h = (e & 64) != 0;
+        const uint32_t aw = __builtin_amdgcn_readlane(h ? w_lo1 : w_lo0, e & 63);
+        const uint32_t bw = __builtin_amdgcn_readlane(h ? w_hi1 : w_hi0, e & 63);
+        const uint16_t* ab = p.a + (int64_t)aw * 32;
+        const uint16_t* bb = p.b + (int64_t)bw * 32;
         const uint32_t st = lds_w + stage * kStage;
-        gl_lds16(ab + a_goff[0], st);
-        gl_lds16(ab + a_goff[1], st + 1024);
-        gl_lds16(bb + b_goff[0], st + 2048);
-        gl_lds16(bb + b_goff[1], st + 3072);
+        gl_lds16(ab + a_goff0, st);
+        gl_lds16(ab + a_goff1, st + 1024);
+        gl_lds16(bb + b_goff0, st + 2048);
+        gl_lds16(bb + b_goff1, st + 3072);
     };
     // Operand reads: A row l32, chunk 2*s + q; B column l32 by transpose
     // reads of rows 16*s + 8*q + 4*h + (lane%16)/4, columns 16*(lane/16 % 2)
-    // + 4*(lane%4).
+    // + 4*(lane%4) (the second k-step adds 16 rows = 1 KB).
     const int a_rd = (l32 >> 3) * 512 + (8 * q + (l32 & 7)) * 16;  // + 256 * s
-    int b_rd[2][2];
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int g = lane >> 4;
-            const int r = 16 * s2 + 8 * (g >> 1) + 4 * h + ((lane & 15) >> 2);
-            const int col = 16 * (g & 1) + 4 * (lane & 3);
-            b_rd[s2][h] = 2048 + r * 64 + 2 * col;
-        }
+    const int b_rd = 2048 + (8 * ((lane >> 4) >> 1) + ((lane & 15) >> 2)) * 64 +
+                     2 * (16 * ((lane >> 4) & 1) + 4 * (lane & 3));  // + 256 * h + 1024 * s
 
-    f32x16 acc;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
 #pragma unroll
     for (int e = 0; e < S - 1; ++e)
-        if (e < n) issue(e);
+        if (e < n) issue(e, e);
     int stage = 0;  // stage of product k
-    for (int k = 0; k < n; ++k) {
-        // Product k+S-1 goes into the stage product k-1 used: this wave's
-        // reads of it are complete once lgkmcnt is 0.
-        if (k + S - 1 < n) {
-            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            issue(stage == 0 ? S - 1 : stage - 1);
-        }
-        wait_stages<kPer, S - 1>(min(S - 1, n - 1 - k));  // product k landed
-        const uint8_t* st = smem_w + stage * kStage;
+    int k = 0;      // next product of the run
+    const int ntask = t1 - t0;
+    for (int ct = 0; ct < ntask; ++ct) {
+        const int kend = __builtin_amdgcn_readlane(t_end, ct);
+        f32x16 acc;
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-            const u32x4 av = *(const u32x4*)(st + a_rd + 256 * s2);
-            const u32x4 lo = ld_tr_b16(st + b_rd[s2][0]);
-            const u32x4 hi = ld_tr_b16(st + b_rd[s2][1]);
-            acc = mfma32(av, u32x4{lo.x, lo.y, hi.x, hi.y}, acc);
-        }
-        stage = stage == S - 1 ? 0 : stage + 1;
-    }
+        for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+        for (; k < kend; ++k) {
+            // Product k+S-1 goes into the stage product k-1 used: this wave's
+            // reads of it are complete once lgkmcnt is 0 (no scalar loads are
+            // in flight here, so the wait covers only those reads).
+            if (k + S - 1 < n) {
+                __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                issue(k + S - 1, stage == 0 ? S - 1 : stage - 1);
+            }
+            // Product k landed (stores in flight only make this wait longer:
+            // loads complete in order, so the count still covers product k).
+            wait_stages<kPer, S - 1>(min(S - 1, n - 1 - k));
+            const uint8_t* st = smem_w + stage * kStage;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const int64_t idx = task.out_off + (int64_t)(8 * (v >> 2) + 4 * q + (v & 3)) * p.ldo + l32;
-        if (OUT_BF16)
-            store_out(&((uint16_t*)p.out)[idx], f32_to_bf16_rne(acc[v]));
-        else
-            store_out(&((float*)p.out)[idx], acc[v]);
+            for (int s2 = 0; s2 < 2; ++s2) {
+                const u32x4 av = *(const u32x4*)(st + a_rd + 256 * s2);
+                const u32x4 lo = ld_tr_b16(st + b_rd + 1024 * s2);
+                const u32x4 hi = ld_tr_b16(st + b_rd + 1024 * s2 + 256);
+                acc = mfma32(av, u32x4{lo.x, lo.y, hi.x, hi.y}, acc);
+            }
+            stage = stage == S - 1 ? 0 : stage + 1;
+        }
+        // Store through the stage the task's last product used (free until
+        // the next issue, whose lgkmcnt wait covers these LDS accesses): the
+        // sub-block goes to LDS row-major, then out in 16-byte pieces, whole
+        // rows per group of lanes.
+        const int64_t off = (int64_t)(((uint64_t)__builtin_amdgcn_readlane(off_hi, ct) << 32) |
+                                      __builtin_amdgcn_readlane(off_lo, ct));
+        uint8_t* tile = (uint8_t*)smem_w + (stage == 0 ? S - 1 : stage - 1) * kStage;
+        constexpr int ESZ = OUT_BF16 ? 2 : 4;
+        constexpr int ROW = 32 * ESZ;          // bytes per tile row
+        constexpr int PIECES = 32 * ROW / 16;  // 16-byte pieces of the tile
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int r = 8 * (v >> 2) + 4 * q + (v & 3);
+            if (OUT_BF16)
+                *(uint16_t*)(tile + r * ROW + 2 * l32) = f32_to_bf16_rne(acc[v]);
+            else
+                *(float*)(tile + r * ROW + 4 * l32) = acc[v];
+        }
+#pragma unroll
+        for (int i = 0; i < PIECES / 64; ++i) {
+            const int c = 64 * i + lane;
+            const u32x4 val = *(const u32x4*)(tile + 16 * c);
+            const int r = c / (ROW / 16), col = (c % (ROW / 16)) * (16 / ESZ);
+            const int64_t idx = off + (int64_t)r * p.ldo + col;
+            store_out((u32x4*)((uint8_t*)p.out + idx * ESZ), val);
+        }
     }
 }
 
@@ -1091,12 +1141,22 @@ hipError_t launch_sddmm(const SddmmArgs& a, bool y_colmajor, bool out_bf16, int 
     return hipGetLastError();
 }
 
-hipError_t launch_spgemm(const SpgemmArgs& a, bool out_bf16, int grid, hipStream_t stream) {
-    if (grid <= 0) return hipSuccess;
+template <int S>
+static void launch_spgemm_t(const SpgemmArgs& a, bool out_bf16, int grid, hipStream_t stream) {
     if (out_bf16)
-        hipLaunchKernelGGL((spgemm_kernel<kSpgemmStages, true>), dim3(grid), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((spgemm_kernel<S, true>), dim3(grid), dim3(256), 0, stream, a);
     else
-        hipLaunchKernelGGL((spgemm_kernel<kSpgemmStages, false>), dim3(grid), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((spgemm_kernel<S, false>), dim3(grid), dim3(256), 0, stream, a);
+}
+
+hipError_t launch_spgemm(const SpgemmArgs& a, int stages, bool out_bf16, int grid, hipStream_t stream) {
+    if (grid <= 0) return hipSuccess;
+    switch (stages) {
+        case 2: launch_spgemm_t<2>(a, out_bf16, grid, stream); break;
+        case 3: launch_spgemm_t<3>(a, out_bf16, grid, stream); break;
+        case 4: launch_spgemm_t<4>(a, out_bf16, grid, stream); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -55,11 +55,11 @@ struct SpgemmArgs {
     void* out;                  // C block values (fp32 or bf16), R x BC blocks
     const SpgemmTask* tasks;    // one per 32x32 output sub-block
     const uint64_t* terms;      // per product: A offset / 32 (low 32 bits) | B offset / 32 (high)
-    const int32_t* xcd_begin;   // kNumXcd + 1 task boundaries
+    const SpgemmRun* runs;      // grid * 4 wave runs
     int32_t lda;                // row stride inside an A block (= C)
     int32_t ldb;                // row stride inside a B block (= BC)
     int32_t ldo;                // row stride inside an output block (= BC)
-    int32_t pad;
+    int32_t wg_per_xcd;         // workgroups per XCD (grid / kNumXcd)
 };
 
 // Floats of partial-result scratch per (slot, tile): a 32 x tile_n block.
@@ -121,9 +121,10 @@ hipError_t launch_attention(const AttentionArgs& a, int head_dim, bool out_bf16,
 hipError_t launch_sddmm(const SddmmArgs& a, bool y_colmajor, bool out_bf16, int grid,
                         hipStream_t stream);
 
-// Ring depth of the SpGEMM kernel (products in flight + 1 per wave; LDS per
-// workgroup = 16 KB * stages).
-constexpr int kSpgemmStages = 4;
-hipError_t launch_spgemm(const SpgemmArgs& a, bool out_bf16, int grid, hipStream_t stream);
+// Ring depths of the SpGEMM kernel (products in flight + 1 per wave; LDS per
+// workgroup = 16 KB * stages) and the default.
+inline bool spgemm_stages_supported(int s) { return s == 2 || s == 3 || s == 4; }
+constexpr int kSpgemmStages = 3;
+hipError_t launch_spgemm(const SpgemmArgs& a, int stages, bool out_bf16, int grid, hipStream_t stream);
 
 }  // namespace bsp

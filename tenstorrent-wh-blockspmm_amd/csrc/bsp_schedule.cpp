@@ -449,7 +449,8 @@ int spgemm_symbolic(const bsp_bsr_desc* a, const bsp_bsr_desc* b, std::vector<in
     return BSP_OK;
 }
 
-int build_spgemm_schedule(const bsp_bsr_desc* a, const bsp_bsr_desc* b, SpgemmSchedule& s, std::string& msg) {
+int build_spgemm_schedule(const bsp_bsr_desc* a, const bsp_bsr_desc* b, int num_cus, int stages, int rounds,
+                          SpgemmSchedule& s, std::string& msg) {
     int st = check_spgemm_operands(a, b, msg);
     if (st != BSP_OK) return st;
     const int64_t R = a->R, C = a->C, BC = b->C;
@@ -465,6 +466,7 @@ int build_spgemm_schedule(const bsp_bsr_desc* a, const bsp_bsr_desc* b, SpgemmSc
     std::vector<std::pair<int32_t, int32_t>> pairs;
     s = SpgemmSchedule{};
     s.indptr.assign(nbr + 1, 0);
+    std::vector<int32_t> task_row, task_col;  // output block row / column of each task
     bool too_big = false;
     for (int64_t i = 0; i < nbr && !too_big; ++i) {
         spgemm_row(a, b, i, mark, cnt, pos, cols, pairs, true,
@@ -490,6 +492,8 @@ int build_spgemm_schedule(const bsp_bsr_desc* a, const bsp_bsr_desc* b, SpgemmSc
                                t.t_end = (int32_t)s.terms.size();
                                s.max_task_terms = std::max(s.max_task_terms, t.t_end - t.t_begin);
                                s.tasks.push_back(t);
+                               task_row.push_back((int32_t)i);
+                               task_col.push_back(j);
                            }
                    });
         if ((int64_t)s.indices.size() > INT32_MAX) too_big = true;
@@ -500,26 +504,116 @@ int build_spgemm_schedule(const bsp_bsr_desc* a, const bsp_bsr_desc* b, SpgemmSc
         return BSP_ERR_UNSUPPORTED;
     }
     s.nblocks = (int64_t)s.indices.size();
-    // Contiguous task ranges of about equal cost per XCD (products, plus the
-    // store counted as two products), so that an XCD works through whole
-    // output block rows and keeps their A blocks in its L2.
     const int64_t ntask = (int64_t)s.tasks.size();
+    if (num_cus <= 0) num_cus = 256;
+    auto cost = [&](const SpgemmTask& t) -> int64_t { return (t.t_end - t.t_begin) + 2; };
     int64_t total = 0;
-    for (const SpgemmTask& t : s.tasks) total += (t.t_end - t.t_begin) + 2;
-    s.xcd_begin.assign(kNumXcd + 1, (int32_t)ntask);
-    s.xcd_begin[0] = 0;
-    int64_t acc = 0, t = 0;
-    for (int x = 1; x < kNumXcd; ++x) {
-        const int64_t target = total * x / kNumXcd;
-        while (t < ntask && acc < target) {
-            acc += (s.tasks[t].t_end - s.tasks[t].t_begin) + 2;
-            ++t;
+    for (const SpgemmTask& t : s.tasks) total += cost(t);
+
+    // XCD regions: the output block rows are cut into RG groups of about
+    // equal cost and, inside each row group, the output block columns into
+    // CG = 8 / RG groups; region x = rg * CG + cg runs on XCD x.  An XCD then
+    // reads the A blocks of its rows that meet its columns and the B blocks
+    // of its columns that meet its rows: about CG * |A| + RG * |B| in all
+    // (a split by rows alone reads B into every XCD's L2).  RG minimises
+    // that sum; BSP_SPGEMM_XCD_ROWS overrides it.
+    const int64_t bytes_a = a->nblocks * R * C, bytes_b = b->nblocks * C * BC;
+    int RG = 8;
+    for (int g : {4, 2, 1})
+        if ((kNumXcd / g) * bytes_a + g * bytes_b < (kNumXcd / RG) * bytes_a + RG * bytes_b) RG = g;
+    const int64_t rg_env = env_int("BSP_SPGEMM_XCD_ROWS", 0);
+    if (rg_env == 1 || rg_env == 2 || rg_env == 4 || rg_env == 8) RG = (int)rg_env;
+    const int CG = kNumXcd / RG;
+    std::vector<int64_t> row_cost(nbr, 0);
+    for (int64_t t = 0; t < ntask; ++t) row_cost[task_row[t]] += cost(s.tasks[t]);
+    std::vector<int32_t> row_group(nbr);
+    {
+        int64_t run = 0;
+        for (int64_t r = 0; r < nbr; ++r) {
+            row_group[r] = (int32_t)std::min<int64_t>(RG - 1, total ? run * RG / total : 0);
+            run += row_cost[r];
         }
-        s.xcd_begin[x] = (int32_t)t;
     }
-    int64_t per = 0;
-    for (int x = 0; x < kNumXcd; ++x) per = std::max<int64_t>(per, (s.xcd_begin[x + 1] - s.xcd_begin[x] + 3) / 4);
+    std::vector<int64_t> col_cost((size_t)RG * nbc, 0), group_total(RG, 0);
+    for (int64_t t = 0; t < ntask; ++t) {
+        const int g = row_group[task_row[t]];
+        col_cost[(size_t)g * nbc + task_col[t]] += cost(s.tasks[t]);
+        group_total[g] += cost(s.tasks[t]);
+    }
+    std::vector<int32_t> col_group((size_t)RG * nbc);
+    for (int g = 0; g < RG; ++g) {
+        int64_t run = 0;
+        for (int64_t c = 0; c < nbc; ++c) {
+            col_group[(size_t)g * nbc + c] =
+                (int32_t)std::min<int64_t>(CG - 1, group_total[g] ? run * CG / group_total[g] : 0);
+            run += col_cost[(size_t)g * nbc + c];
+        }
+    }
+    // Tasks (and their products) reordered by region, output order inside one.
+    std::vector<int32_t> region(ntask);
+    std::vector<int64_t> region_cost(kNumXcd, 0);
+    std::vector<int32_t> region_count(kNumXcd + 1, 0);
+    for (int64_t t = 0; t < ntask; ++t) {
+        const int g = row_group[task_row[t]];
+        region[t] = g * CG + col_group[(size_t)g * nbc + task_col[t]];
+        region_cost[region[t]] += cost(s.tasks[t]);
+        ++region_count[region[t] + 1];
+    }
+    for (int x = 0; x < kNumXcd; ++x) region_count[x + 1] += region_count[x];
+    {
+        std::vector<int32_t> next(region_count.begin(), region_count.end() - 1);
+        std::vector<SpgemmTask> tasks(ntask);
+        std::vector<uint64_t> terms;
+        terms.reserve(s.terms.size());
+        std::vector<int32_t> order(ntask);
+        for (int64_t t = 0; t < ntask; ++t) order[next[region[t]]++] = (int32_t)t;
+        for (int64_t u = 0; u < ntask; ++u) {
+            const SpgemmTask& o = s.tasks[order[u]];
+            tasks[u].out_off = o.out_off;
+            tasks[u].t_begin = (int32_t)terms.size();
+            terms.insert(terms.end(), s.terms.begin() + o.t_begin, s.terms.begin() + o.t_end);
+            tasks[u].t_end = (int32_t)terms.size();
+        }
+        s.tasks.swap(tasks);
+        s.terms.swap(terms);
+    }
+
+    // Wave runs: contiguous task ranges of one region of about equal cost
+    // (products, plus the store counted as two products), `rounds` times as
+    // many in all as waves fit the GPU, each at most kSpgemmRunTasks tasks;
+    // a region's share follows its cost.  Run slot (x * wg_per_xcd + j) * 4
+    // + wave belongs to a workgroup on XCD x and holds region x's runs.
+    rounds = std::min(16, std::max(1, rounds));
+    const int64_t nw = std::max<int64_t>(
+        1, std::min<int64_t>(ntask, (int64_t)rounds * num_cus * spgemm_waves_per_cu(stages)));
+    std::vector<std::vector<SpgemmRun>> region_runs(kNumXcd);
+    for (int x = 0; x < kNumXcd; ++x) {
+        const int64_t t_lo = region_count[x], t_hi = region_count[x + 1];
+        if (t_lo == t_hi) continue;
+        const int64_t want = std::max<int64_t>(1, total ? (nw * region_cost[x] + total - 1) / total : 1);
+        const int64_t target = std::max<int64_t>(1, (region_cost[x] + want - 1) / want);
+        int64_t acc = 0, begin = t_lo;
+        for (int64_t t = t_lo; t < t_hi; ++t) {
+            acc += cost(s.tasks[t]);
+            if (acc >= target || t + 1 - begin == kSpgemmRunTasks || t + 1 == t_hi) {
+                region_runs[x].push_back({(int32_t)begin, (int32_t)(t + 1), s.tasks[begin].t_begin, s.tasks[t].t_end});
+                acc = 0;
+                begin = t + 1;
+            }
+        }
+    }
+    int64_t per = 1;
+    s.pieces = 0;
+    for (int x = 0; x < kNumXcd; ++x) {
+        per = std::max<int64_t>(per, ((int64_t)region_runs[x].size() + 3) / 4);
+        s.pieces += (int32_t)region_runs[x].size();
+    }
+    s.wg_per_xcd = (int32_t)per;
     s.grid = (int32_t)(per * kNumXcd);
+    const int32_t pend = ntask ? s.tasks.back().t_end : 0;
+    s.runs.assign((size_t)s.grid * 4, SpgemmRun{(int32_t)ntask, (int32_t)ntask, pend, pend});
+    for (int x = 0; x < kNumXcd; ++x)
+        std::copy(region_runs[x].begin(), region_runs[x].end(), s.runs.begin() + (size_t)x * per * 4);
     return BSP_OK;
 }
 

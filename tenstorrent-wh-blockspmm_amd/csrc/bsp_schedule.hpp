@@ -104,6 +104,16 @@ struct SpgemmTask {
 };
 static_assert(sizeof(SpgemmTask) == 16, "SpgemmTask layout is shared with the kernels");
 
+// One SpGEMM wave run: tasks [t0, t1) and their products [p0, p1) (the
+// products of consecutive tasks are contiguous); t0 == t1 for an idle slot.
+struct SpgemmRun {
+    int32_t t0;
+    int32_t t1;
+    int32_t p0;
+    int32_t p1;
+};
+static_assert(sizeof(SpgemmRun) == 16, "SpgemmRun layout is shared with the kernels");
+
 // SpGEMM C = A * B with A, B and C in BSR.  The symbolic phase: C's structure
 // (block (i, j) present iff some stored A(i, k) meets some stored B(k, j),
 // columns ascending per row, as bsr_matrix<T>::spgemm builds it,
@@ -116,16 +126,28 @@ struct SpgemmSchedule {
     std::vector<int32_t> indices;    // output block columns (nblocks)
     std::vector<SpgemmTask> tasks;   // one per output sub-block, in output order
     std::vector<uint64_t> terms;     // A sub-block offset / 32 | (B sub-block offset / 32) << 32
-    std::vector<int32_t> xcd_begin;  // kNumXcd + 1 task boundaries: XCD x runs tasks [x], [x+1)
+    std::vector<SpgemmRun> runs;     // grid * 4 wave slots
     int32_t max_task_terms = 0;
-    int32_t grid = 0;                // workgroups (four tasks each, kNumXcd-interleaved)
+    int32_t pieces = 0;              // non-empty wave runs
+    int32_t grid = 0;                // workgroups, a multiple of kNumXcd
+    int32_t wg_per_xcd = 0;
 };
+
+// SpGEMM wave runs: contiguous task ranges of about equal cost, at most
+// kSpgemmRunTasks tasks each, `rounds` runs per resident wave (compute units
+// x waves that fit a compute unit's LDS at `stages` ring stages).
+constexpr int kSpgemmRunTasks = 64;
+constexpr int kSpgemmStageBytes = 4096;
+constexpr int kLdsBytesPerCu = 160 * 1024;
+inline int spgemm_waves_per_cu(int stages) { return 4 * (kLdsBytesPerCu / (4 * stages * kSpgemmStageBytes)); }
 
 // Output structure only (no product lists).
 int spgemm_symbolic(const bsp_bsr_desc* a, const bsp_bsr_desc* b, std::vector<int32_t>& indptr,
                     std::vector<int32_t>& indices, std::string& msg);
-// Structure, product lists and the XCD split.
-int build_spgemm_schedule(const bsp_bsr_desc* a, const bsp_bsr_desc* b, SpgemmSchedule& s, std::string& msg);
+// Structure, product lists and the wave runs for `num_cus` compute units and
+// a ring of `stages` stages.
+int build_spgemm_schedule(const bsp_bsr_desc* a, const bsp_bsr_desc* b, int num_cus, int stages, int rounds,
+                          SpgemmSchedule& s, std::string& msg);
 
 // Structural checks of sparse_common/bsr_matrix.hpp:246-252 / :610-616 plus
 // the CSR invariants the golden relies on implicitly.  On failure returns a

@@ -103,4 +103,35 @@ void bsr_sddmm_mi355x_f32(bsr_matrix<bfloat16>& sampling_mask, dense_matrix<bflo
 
 }  // namespace bsr_sddmm_host_code
 
+namespace bsr_spgemm_host_code {
+
+template <typename TO>
+static bsr_matrix<TO> run_spgemm(const bsr_matrix<bfloat16>& a, const bsr_matrix<bfloat16>& b, int dtype,
+                                 Device* device) {
+    check_dims(a.W == b.H && a.C == b.R, "A's columns and block width must match B's rows and block height");
+    check_dims(a.data.size() == a.nblocks * a.R * a.C && b.data.size() == b.nblocks * b.R * b.C,
+               "A and B values");
+    const bsp_bsr_desc da = desc_of(a), db = desc_of(b);
+    int64_t nb = 0;
+    check(bsp_spgemm_symbolic(&da, &db, &nb, nullptr, nullptr));
+    std::vector<int> indptr(a.H / a.R + 1), indices(nb);
+    std::vector<TO> vals((size_t)nb * a.R * b.C);
+    check(bsp_host_spgemm(&da, reinterpret_cast<const uint16_t*>(a.data.data()), &db,
+                          reinterpret_cast<const uint16_t*>(b.data.data()), indptr.data(), indices.data(),
+                          vals.data(), dtype, device ? device->ordinal : 0));
+    return bsr_matrix<TO>(std::move(vals), std::move(indptr), std::move(indices), a.H, b.W, a.R, b.C, (size_t)nb);
+}
+
+bsr_matrix<bfloat16> bsr_spgemm_mi355x(const bsr_matrix<bfloat16>& a, const bsr_matrix<bfloat16>& b,
+                                       Device* device) {
+    return run_spgemm<bfloat16>(a, b, BSP_DTYPE_BF16, device);
+}
+
+bsr_matrix<float> bsr_spgemm_mi355x_f32(const bsr_matrix<bfloat16>& a, const bsr_matrix<bfloat16>& b,
+                                        Device* device) {
+    return run_spgemm<float>(a, b, BSP_DTYPE_F32, device);
+}
+
+}  // namespace bsr_spgemm_host_code
+
 }  // namespace bsp_host

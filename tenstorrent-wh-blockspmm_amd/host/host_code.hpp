@@ -4,6 +4,9 @@
 //        (a, b, output, bcast_batch, nnz_blocks, M, N, K, R, C, B, device)
 // SDDMM: SDDMMHostCodeFunctionPtr, block_sddmm/inc/host_code.hpp:104-115
 //        (sampling_mask, c, d, output, M, N, K, R, C_block, B, device)
+// SpGEMM: bsr_matrix<T>::spgemm(const bsr_matrix<T>& B),
+//        sparse_common/bsr_matrix.hpp:741-810 (a CPU routine in the reference;
+//        here the products run on the device)
 // The reference passes an IDevice* from tt-metal's CreateDevice; here Device
 // names a HIP device ordinal.  Buffers are the reference's untilized host
 // layout (the reference tilizes at its call sites, test_block_spmm.cpp:77-78;
@@ -73,5 +76,18 @@ static std::pair<SDDMMHostCodeFunctionPtr, std::string> HostCodeRegistry[] = {
 };
 
 }  // namespace bsr_sddmm_host_code
+
+namespace bsr_spgemm_host_code {
+
+// a * b as a new BSR matrix (H x b.W in R x b.C blocks) with bf16 values, the
+// reference's spgemm result type; requires a.W == b.H and a.C == b.R.
+bsr_matrix<bfloat16> bsr_spgemm_mi355x(const bsr_matrix<bfloat16>& a, const bsr_matrix<bfloat16>& b,
+                                       Device* device);
+
+// Same with fp32 values (the golden's accumulator precision).
+bsr_matrix<float> bsr_spgemm_mi355x_f32(const bsr_matrix<bfloat16>& a, const bsr_matrix<bfloat16>& b,
+                                        Device* device);
+
+}  // namespace bsr_spgemm_host_code
 
 }  // namespace bsp_host

@@ -46,3 +46,17 @@ def test_sddmm_registry_on_gpu():
     p = _run([_tool("test_sddmm"), "-1", "0"], 300)
     assert p.returncode == 0, p.stdout[-3000:] + p.stderr[-2000:]
     assert "Passed: 17 / 17" in p.stdout
+
+
+def test_spgemm_cpu_only_structure_mode():
+    """test_spgemm <all> -1: the symbolic phase against the oracle's structure."""
+    p = _run([_tool("test_spgemm"), "-1", "-1"], 120)
+    assert p.returncode == 0, p.stdout + p.stderr
+    assert "Passed: 10 / 10" in p.stdout
+
+
+@pytest.mark.gpu
+def test_spgemm_host_mirror_on_gpu():
+    p = _run([_tool("test_spgemm"), "-1", "0"], 300)
+    assert p.returncode == 0, p.stdout[-3000:] + p.stderr[-2000:]
+    assert "Passed: 10 / 10" in p.stdout
