@@ -432,6 +432,7 @@ int bsp_sddmm(const bsp_plan* p, const uint16_t* mask_vals, const uint16_t* x, i
     args.ldy = ldy;
     args.ldo = (int32_t)p->C;
     args.K = (int32_t)p->K;
+    args.max_item_entries = p->info.max_item_entries;
     hipError_t e = bsp::launch_sddmm(args, p->layout == BSP_COL_MAJOR,
                                      p->out_dtype == BSP_DTYPE_BF16, p->info.grid,
                                      (hipStream_t)stream);

@@ -890,6 +890,124 @@ __global__ __launch_bounds__(256) void sddmm_kernel(SddmmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// SDDMM for K <= 256 in one shot.  A workgroup takes an item of up to four
+// output sub-blocks of one 32-row stripe, one per wave.  All its operands go
+// global->LDS at once: the X stripe (32 x K, shared, loaded by all waves) and
+// each wave's Y panel (K x 32, or 32 x K rows of Y^T).  One wait for the
+// wave's own loads and one barrier (for the other waves' parts of X), then
+// each wave runs its whole K-deep 32x32 product, multiplies by the mask
+// block and stores it.  No loop-carried loads, so nothing the compiler waits
+// for; LDS = 320 * K bytes, two workgroups per compute unit at K = 256.
+//   X (and Y^T) rows: 2K bytes, 16-byte chunk c of row r at slot
+//   c ^ (r % min(K/8, 16)) (conflict-free row reads);
+//   row-major Y panel: 64-byte rows, read with the transpose read.
+namespace sddmm_shot {
+template <int K>
+struct Layout {
+    static constexpr int NC = K / 8;                 // 16-byte chunks per row
+    static constexpr int SW = NC < 16 ? NC : 16;     // swizzle period
+    static constexpr int RP = 2 * K;                 // row pitch (bytes)
+    static constexpr int PANEL = 64 * K;             // 32 x K or K x 32 bf16
+    static constexpr int XI = PANEL / 1024;          // 1 KB loads per panel
+    static constexpr int LDS = 5 * PANEL;            // X + four Y panels
+};
+}  // namespace sddmm_shot
+
+template <int K, bool Y_COLMAJOR, bool OUT_BF16>
+__global__ __launch_bounds__(256, 2) void sddmm_shot_kernel(SddmmArgs p) {
+    using namespace spmm_detail;
+    using L = sddmm_shot::Layout<K>;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[L::LDS];
+    const SddmmItem it = load_const(p.wgs + blockIdx.x);
+    if (it.e_end <= it.e_begin) return;  // idle workgroup (uniform)
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l32 = lane & 31, q = lane >> 5;
+    const int e = it.e_begin + wave;
+    const bool has = e < it.e_end;  // uniform per wave
+    const uint32_t lds0 = lds_address(smem);
+    const uint32_t ylds = lds0 + (1 + wave) * L::PANEL;
+
+    // A 32-row panel (X stripe, or 32 rows of Y^T) into LDS, load t of it:
+    // slot 64t + lane holds row (64t + lane) / NC, chunk c ^ (row % SW).
+    auto rows_panel = [&](const uint16_t* base, int64_t ld, int t, uint32_t dst) {
+        const int slot = 64 * t + lane;
+        const int r = slot / L::NC;
+        const int c = (slot % L::NC) ^ (r % L::SW);
+        gl_lds16(base + (int64_t)r * ld + 8 * c, dst + 1024 * t);
+    };
+#pragma unroll
+    for (int j = 0; j < (L::XI + 3) / 4; ++j) {
+        const int t = wave + 4 * j;
+        if (t < L::XI) rows_panel(p.x + (int64_t)it.x_row0 * p.ldx, p.ldx, t, lds0);
+    }
+    if (has) {
+        const int32_t col = load_const(p.ent_col + e);
+        if (Y_COLMAJOR) {
+#pragma unroll
+            for (int t = 0; t < L::XI; ++t) rows_panel(p.y + (int64_t)col * p.ldy, p.ldy, t, ylds);
+        } else {
+            // K rows of 64 bytes: slot 64t + lane holds row slot / 4, chunk slot % 4.
+#pragma unroll
+            for (int t = 0; t < L::XI; ++t) {
+                const int slot = 64 * t + lane;
+                gl_lds16(p.y + (int64_t)(slot >> 2) * p.ldy + col + 8 * (slot & 3), ylds + 1024 * t);
+            }
+        }
+    }
+    // Mask values of this lane's 16 outputs, in flight with the operands.
+    int64_t off = 0;
+    uint32_t mk[16];
+    if (has) {
+        off = load_const(p.ent_off + e);
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+            mk[v] = p.mask[off + (int64_t)(8 * (v >> 2) + 4 * q + (v & 3)) * p.ldo + l32];
+    }
+    wait_vmcnt<0>();
+    barrier_no_fence();
+    if (!has) return;
+
+    const uint8_t* xs = smem;
+    const uint8_t* ys = smem + (1 + wave) * L::PANEL;
+    // Row reads: row l32, logical chunk 4*ks + 2*s2 + q.
+    auto row_read = [&](const uint8_t* panel, int ch) {
+        return *(const u32x4*)(panel + l32 * L::RP + 16 * (ch ^ (l32 % L::SW)));
+    };
+    f32x16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < K / 32; ++ks)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            const int ch = 4 * ks + 2 * s2 + q;
+            const u32x4 a = row_read(xs, ch);
+            u32x4 b;
+            if (Y_COLMAJOR) {
+                b = row_read(ys, ch);
+            } else {
+                const int g = lane >> 4;
+                const int r = 32 * ks + 16 * s2 + 8 * q + ((lane & 15) >> 2);
+                const int cb = 2 * (16 * (g & 1) + 4 * (lane & 3));
+                const u32x4 lo = ld_tr_b16(ys + r * 64 + cb);
+                const u32x4 hi = ld_tr_b16(ys + (r + 4) * 64 + cb);
+                b = u32x4{lo.x, lo.y, hi.x, hi.y};
+            }
+            acc = mfma32(a, b, acc);
+        }
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const float val = acc[v] * bf16_to_f32((uint16_t)mk[v]);
+        const int64_t idx = off + (int64_t)(8 * (v >> 2) + 4 * q + (v & 3)) * p.ldo + l32;
+        if (OUT_BF16)
+            store_out(&((uint16_t*)p.out)[idx], f32_to_bf16_rne(val));
+        else
+            store_out(&((float*)p.out)[idx], val);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // SpGEMM numeric phase, C = A * B with A, B and C in BSR (C's structure and
 // the product lists come from the plan).  The unit of output is a 32x32
 // sub-block (a task) with its run of products; a wave takes a contiguous
@@ -1124,9 +1242,33 @@ static void launch_sddmm_t(const SddmmArgs& a, int grid, hipStream_t stream) {
         hipLaunchKernelGGL((sddmm_kernel<Y_COLMAJOR, OUT_BF16, false>), dim3(grid), dim3(256), 0, stream, a);
 }
 
+template <int K>
+static void launch_sddmm_shot(const SddmmArgs& a, bool y_colmajor, bool out_bf16, int grid, hipStream_t stream) {
+    if (y_colmajor) {
+        if (out_bf16)
+            hipLaunchKernelGGL((sddmm_shot_kernel<K, true, true>), dim3(grid), dim3(256), 0, stream, a);
+        else
+            hipLaunchKernelGGL((sddmm_shot_kernel<K, true, false>), dim3(grid), dim3(256), 0, stream, a);
+    } else {
+        if (out_bf16)
+            hipLaunchKernelGGL((sddmm_shot_kernel<K, false, true>), dim3(grid), dim3(256), 0, stream, a);
+        else
+            hipLaunchKernelGGL((sddmm_shot_kernel<K, false, false>), dim3(grid), dim3(256), 0, stream, a);
+    }
+}
+
 hipError_t launch_sddmm(const SddmmArgs& a, bool y_colmajor, bool out_bf16, int grid,
                         hipStream_t stream) {
     if (grid <= 0) return hipSuccess;
+    if (sddmm_shot_supported(a.K, a.max_item_entries)) {
+        switch (a.K) {
+            case 32: launch_sddmm_shot<32>(a, y_colmajor, out_bf16, grid, stream); break;
+            case 64: launch_sddmm_shot<64>(a, y_colmajor, out_bf16, grid, stream); break;
+            case 128: launch_sddmm_shot<128>(a, y_colmajor, out_bf16, grid, stream); break;
+            default: launch_sddmm_shot<256>(a, y_colmajor, out_bf16, grid, stream); break;
+        }
+        return hipGetLastError();
+    }
     if (y_colmajor) {
         if (out_bf16)
             launch_sddmm_t<true, true>(a, grid, stream);

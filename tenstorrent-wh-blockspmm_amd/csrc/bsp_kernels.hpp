@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstdlib>
 
 #include "bsp_schedule.hpp"
 
@@ -47,7 +48,16 @@ struct SddmmArgs {
     int64_t ldy;
     int32_t ldo;              // row stride inside an output / mask block (= C)
     int32_t K;
+    int32_t max_item_entries; // longest item of the plan (entries per workgroup)
+    int32_t pad;
 };
+
+// The one-shot SDDMM kernel: K of 32, 64, 128 or 256 and items of at most
+// four entries (one per wave).
+inline bool sddmm_shot_supported(int K, int max_item_entries) {
+    return (K == 32 || K == 64 || K == 128 || K == 256) && max_item_entries <= 4 &&
+           std::getenv("BSP_SDDMM_LOOP") == nullptr;
+}
 
 struct SpgemmArgs {
     const uint16_t* a;          // A block values (bf16), R x C blocks
