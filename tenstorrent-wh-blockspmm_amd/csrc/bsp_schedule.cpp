@@ -130,13 +130,11 @@ std::vector<int32_t> xcd_tile_map(const std::vector<int64_t>& item_cost, int n_t
     }
     const int tpg = n_tiles / col_groups;
     std::vector<std::vector<int32_t>> bins(kNumXcd);
-    const int64_t pair = env_int("BSP_SPMM_PAIR", 0);
     for (int rg = 0; rg < row_groups; ++rg)
         for (int cg = 0; cg < col_groups; ++cg) {
             auto& b = bins[rg * col_groups + cg];
             for (int32_t u : rows[rg])
                 for (int t = cg * tpg; t < (cg + 1) * tpg; ++t) b.push_back(u * n_tiles + t);
-            if (pair > 0 && (int64_t)b.size() > pair) std::reverse(b.begin() + pair, b.end());
         }
     size_t maxlen = 0;
     for (auto& b : bins) maxlen = std::max(maxlen, b.size());
