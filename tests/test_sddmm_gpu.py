@@ -133,3 +133,21 @@ def test_small_vectors_fixture():
     m = W.BsrArrays(M, N, R, C, v["sddmm_indptr"], v["sddmm_indices"], v["sddmm_mask"])
     assert_parity(run_sddmm(m, v["sddmm_x"], v["sddmm_y"]), v["sddmm_golden"], v["sddmm_x"].shape[1],
                   "fixture")
+
+
+@pytest.mark.parametrize("layout", ["row", "col"])
+@pytest.mark.parametrize("K", [32, 64, 128, 256])
+def test_one_shot_and_looped_kernels(K, layout, monkeypatch):
+    """K in {32, 64, 128, 256} runs the one-shot kernel; BSP_SDDMM_LOOP forces
+    the looped kernel on the same inputs.  Both are held to the oracle."""
+    rng = np.random.default_rng(K + (layout == "col"))
+    mask = with_values(W.random_positions(512, 1024, 32, 32, 90, rng), "RAND", seed=K)
+    x = W.dense_content(512, K, "RAND", rng)
+    y = W.dense_content(K, 1024, "RAND", rng)
+    yy, lay = (y, None) if layout == "row" else (np.ascontiguousarray(y.T), capi.COL_MAJOR)
+    gold = golden_sddmm(mask, x, y)
+    shot = run_sddmm(mask, x, yy, y_layout=lay)
+    monkeypatch.setenv("BSP_SDDMM_LOOP", "1")
+    looped = run_sddmm(mask, x, yy, y_layout=lay)
+    assert_parity(shot, gold, K, f"one-shot K={K} {layout}")
+    assert_parity(looped, gold, K, f"looped K={K} {layout}")
