@@ -103,7 +103,7 @@ typedef struct bsp_plan_info {
     int32_t grid;        /* workgroups per launch */
     int32_t max_item_entries;
     int32_t stages;      /* SpMM, SpGEMM: depth of the LDS ring (entries in
-                            flight + 1) */
+                            flight + 1); SDDMM: 1 = one-shot kernel, 0 = looped */
     int32_t group;       /* SpMM: 32-row stripes of one block row per workgroup
                             (1; or 2, 4, 8 for blocks of R >= 64) */
     int32_t reserved;

@@ -115,6 +115,15 @@ def load(path: Optional[Path] = None, force_reload: bool = False) -> ctypes.CDLL
         raise ImportError(
             f"{p} not found: build it with __graft_entry__.build() "
             "(the HIP kernels are the only implementation)")
+    # One HIP runtime per process: torch loads its own libamdhip64 (by the
+    # name libamdhip64.so, through its RPATH), so if this library came first
+    # with ROCm's libamdhip64.so.7, the process would hold two runtimes and
+    # torch would find no GPU.  Loaded after torch, this library's
+    # libamdhip64.so.7 resolves to torch's copy (same soname).
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(str(p))
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)  # AttributeError if a declared symbol is missing

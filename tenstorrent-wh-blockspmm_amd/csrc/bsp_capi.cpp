@@ -30,6 +30,7 @@ struct bsp_plan {
     uint64_t* d_terms = nullptr;
     bsp::SpgemmRun* d_runs = nullptr;  // wave runs
     int32_t wg_per_xcd = 0;
+    int32_t sddmm_one_shot = 0;  // SDDMM: the one-shot kernel runs this plan
 };
 
 namespace {
@@ -390,6 +391,9 @@ int bsp_sddmm_plan_create(bsp_plan** out, const bsp_bsr_desc* mask, int64_t K, i
     p->C = mask->C;
     p->nblocks = mask->nblocks;
     fill_info_sddmm(s, &p->info);
+    // BSP_SDDMM_LOOP selects the looped kernel for every K (for comparison).
+    p->sddmm_one_shot = bsp::sddmm_shot_supported(K, s.max_item_entries) && !std::getenv("BSP_SDDMM_LOOP");
+    p->info.stages = p->sddmm_one_shot ? 1 : 0;
     hipError_t e = upload((bsp::SddmmItem**)&p->d_wgs, bsp::sddmm_wg_records(s));
     if (e == hipSuccess) e = upload(&p->d_ent_row, s.ent_col);
     if (e == hipSuccess) e = upload(&p->d_ent_off, s.ent_off);
@@ -432,7 +436,7 @@ int bsp_sddmm(const bsp_plan* p, const uint16_t* mask_vals, const uint16_t* x, i
     args.ldy = ldy;
     args.ldo = (int32_t)p->C;
     args.K = (int32_t)p->K;
-    args.max_item_entries = p->info.max_item_entries;
+    args.one_shot = p->sddmm_one_shot;
     hipError_t e = bsp::launch_sddmm(args, p->layout == BSP_COL_MAJOR,
                                      p->out_dtype == BSP_DTYPE_BF16, p->info.grid,
                                      (hipStream_t)stream);

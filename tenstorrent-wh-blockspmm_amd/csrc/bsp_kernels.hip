@@ -661,7 +661,26 @@ __global__ __launch_bounds__(256) void spmm_reduce_kernel(SpmmArgs p) {
     for (int nt = 0; nt < NTW; ++nt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[nt][v] = 0.0f;
-    for (int pc = 0; pc < sp.npieces; ++pc) {
+    // Pieces are added in order; the loads of up to four pieces are issued
+    // together so their round trips overlap.
+    constexpr int AHEAD = NTW == 1 ? 4 : 2;
+    int pc = 0;
+    for (; pc + AHEAD <= sp.npieces; pc += AHEAD) {
+        float v4[AHEAD][NTW * 16];
+#pragma unroll
+        for (int j = 0; j < AHEAD; ++j) {
+            const float* src = p.ws + ((int64_t)(sp.base + pc + j) * p.n_tiles + tile) * PF;
+#pragma unroll
+            for (int i = 0; i < NTW * 16; ++i) v4[j][i] = src[i * 256 + tid];
+        }
+#pragma unroll
+        for (int j = 0; j < AHEAD; ++j)
+#pragma unroll
+            for (int nt = 0; nt < NTW; ++nt)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[nt][v] += v4[j][nt * 16 + v];
+    }
+    for (; pc < sp.npieces; ++pc) {
         const float* src = p.ws + ((int64_t)(sp.base + pc) * p.n_tiles + tile) * PF;
 #pragma unroll
         for (int nt = 0; nt < NTW; ++nt)
@@ -1260,7 +1279,7 @@ static void launch_sddmm_shot(const SddmmArgs& a, bool y_colmajor, bool out_bf16
 hipError_t launch_sddmm(const SddmmArgs& a, bool y_colmajor, bool out_bf16, int grid,
                         hipStream_t stream) {
     if (grid <= 0) return hipSuccess;
-    if (sddmm_shot_supported(a.K, a.max_item_entries)) {
+    if (a.one_shot) {
         switch (a.K) {
             case 32: launch_sddmm_shot<32>(a, y_colmajor, out_bf16, grid, stream); break;
             case 64: launch_sddmm_shot<64>(a, y_colmajor, out_bf16, grid, stream); break;

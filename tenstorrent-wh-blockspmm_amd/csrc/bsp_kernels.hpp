@@ -4,7 +4,6 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
-#include <cstdlib>
 
 #include "bsp_schedule.hpp"
 
@@ -48,15 +47,14 @@ struct SddmmArgs {
     int64_t ldy;
     int32_t ldo;              // row stride inside an output / mask block (= C)
     int32_t K;
-    int32_t max_item_entries; // longest item of the plan (entries per workgroup)
+    int32_t one_shot;         // 1: sddmm_shot_kernel (chosen at plan creation)
     int32_t pad;
 };
 
-// The one-shot SDDMM kernel: K of 32, 64, 128 or 256 and items of at most
-// four entries (one per wave).
-inline bool sddmm_shot_supported(int K, int max_item_entries) {
-    return (K == 32 || K == 64 || K == 128 || K == 256) && max_item_entries <= 4 &&
-           std::getenv("BSP_SDDMM_LOOP") == nullptr;
+// The one-shot SDDMM kernel takes K of 32, 64, 128 or 256 and items of at
+// most four entries (one per wave).
+inline bool sddmm_shot_supported(int64_t K, int max_item_entries) {
+    return (K == 32 || K == 64 || K == 128 || K == 256) && max_item_entries <= 4;
 }
 
 struct SpgemmArgs {

@@ -368,3 +368,24 @@ def test_spgemm_rejects_mismatched_and_unsupported_operands():
                                    ctypes.byref(n), None, None) == capi.BSP_ERR_BAD_STRUCTURE
     assert capi.last_error().startswith("A: ")
 
+
+
+@pytest.mark.gpu
+def test_library_first_then_torch_shares_one_hip_runtime():
+    """A process that creates a plan before torch touches the GPU must still
+    find the GPU in torch: the binding loads torch's HIP runtime first, so
+    the library binds to it (a second runtime would leave torch with none)."""
+    import sys
+    code = (
+        "import sys; sys.path.insert(0, %r)\n"
+        "import __graft_entry__ as e\n"
+        "capi = e.load_package().capi\n"
+        "import numpy as np\n"
+        "b = capi.Bsr(64, 64, 32, 32, np.array([0, 1, 2], np.int32), np.array([0, 1], np.int32))\n"
+        "plan = capi.SpmmPlan(b, 64, 'f32')\n"
+        "import torch\n"
+        "x = torch.ones(4, device='cuda')\n"
+        "torch.cuda.synchronize()\n"
+        "print('ok', float(x.sum()))\n" % str(REPO))
+    p = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert p.returncode == 0 and "ok 4.0" in p.stdout, p.stdout[-2000:] + p.stderr[-2000:]

@@ -9,7 +9,7 @@ fp32 golden, every output value written (poisoned with NaN first).
 import numpy as np
 import pytest
 
-from helpers import (W, assert_parity, capi, golden_sddmm, run_sddmm, with_values)
+from helpers import (W, assert_parity, bsr_of, capi, golden_sddmm, run_sddmm, with_values)
 
 pytestmark = pytest.mark.gpu
 
@@ -146,8 +146,15 @@ def test_one_shot_and_looped_kernels(K, layout, monkeypatch):
     y = W.dense_content(K, 1024, "RAND", rng)
     yy, lay = (y, None) if layout == "row" else (np.ascontiguousarray(y.T), capi.COL_MAJOR)
     gold = golden_sddmm(mask, x, y)
-    shot = run_sddmm(mask, x, yy, y_layout=lay)
+    kind = capi.ROW_MAJOR if lay is None else lay
+    plan = capi.SddmmPlan(bsr_of(mask), K, kind)
+    assert plan.info()["stages"] == 1  # one-shot kernel
+    shot = run_sddmm(mask, x, yy, y_layout=lay, plan=plan)
+    plan.close()
     monkeypatch.setenv("BSP_SDDMM_LOOP", "1")
-    looped = run_sddmm(mask, x, yy, y_layout=lay)
+    plan = capi.SddmmPlan(bsr_of(mask), K, kind)
+    assert plan.info()["stages"] == 0  # looped kernel
+    looped = run_sddmm(mask, x, yy, y_layout=lay, plan=plan)
+    plan.close()
     assert_parity(shot, gold, K, f"one-shot K={K} {layout}")
     assert_parity(looped, gold, K, f"looped K={K} {layout}")
