@@ -134,7 +134,7 @@ int bsp_spmm_plan_create(bsp_plan** plan, const bsp_bsr_desc* a, int64_t N,
 /* Launch on `stream` (a hipStream_t; NULL = the device's null stream).
  * a_vals: device, nblocks*R*C bf16 (16-byte aligned).
  * b:      device, bf16, K x N in b_layout with leading dimension ldb
- *         (16-byte aligned, ldb a multiple of 8).
+ *         (16-byte aligned, ldb a multiple of 8 and below 2^26).
  * c:      device, M x N row-major with leading dimension ldc, fp32 or bf16 as
  *         planned; every element is written (block rows without nonzeros get
  *         zeros, which the reference obtains by zeroing the output first,
@@ -173,7 +173,7 @@ int bsp_attention_plan_create(bsp_plan** plan, const bsp_bsr_desc* mask, int64_t
 
 /* mask_vals: device, nblocks*R*C bf16.  q: queries x head_dim, k and v:
  * keys x head_dim, all bf16 row-major (16-byte aligned, leading dimensions
- * multiples of 8).  out: queries x head_dim row-major, fp32 or bf16 as
+ * multiples of 8, ldk and ldv below 2^26).  out: queries x head_dim row-major, fp32 or bf16 as
  * planned; every element is written. */
 int bsp_attention(const bsp_plan* plan, const uint16_t* mask_vals, const uint16_t* q, int64_t ldq,
                   const uint16_t* k, int64_t ldk, const uint16_t* v, int64_t ldv, void* out,

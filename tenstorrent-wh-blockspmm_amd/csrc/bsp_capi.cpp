@@ -105,6 +105,10 @@ int check_device(int device) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// The kernels address one 32-row panel of a dense operand with 32-bit byte
+// offsets from the panel's first row: 32 rows must span less than 4 GB.
+constexpr int64_t kMaxLeadingDim = int64_t(1) << 26;
+
 void fill_info_spmm(const bsp::SpmmSchedule& s, bsp_plan_info* info) {
     std::memset(info, 0, sizeof(*info));
     info->kind = 1;
@@ -303,6 +307,7 @@ int bsp_spmm(const bsp_plan* p, const uint16_t* a_vals, const uint16_t* b, int64
         return fail(BSP_ERR_INVALID_ARGUMENT, "null device pointer");
     if (ldb < p->N || ldc < p->N) return fail(BSP_ERR_INVALID_ARGUMENT, "ldb and ldc must be >= N");
     if (ldb % 8 != 0) return fail(BSP_ERR_INVALID_ARGUMENT, "ldb must be a multiple of 8");
+    if (ldb >= kMaxLeadingDim) return fail(BSP_ERR_UNSUPPORTED, "ldb must be below 2^26");
     if (!aligned16(b) || (a_vals && !aligned16(a_vals)))
         return fail(BSP_ERR_INVALID_ARGUMENT, "A values and B must be 16-byte aligned");
     const size_t esz = p->out_dtype == BSP_DTYPE_BF16 ? 2 : 4;
@@ -339,6 +344,8 @@ int bsp_attention(const bsp_plan* p, const uint16_t* mask_vals, const uint16_t* 
         return fail(BSP_ERR_INVALID_ARGUMENT, "leading dimensions must be >= head_dim");
     if (ldq % 8 || ldk % 8 || ldv % 8)
         return fail(BSP_ERR_INVALID_ARGUMENT, "ldq, ldk and ldv must be multiples of 8");
+    if (ldk >= kMaxLeadingDim || ldv >= kMaxLeadingDim)
+        return fail(BSP_ERR_UNSUPPORTED, "ldk and ldv must be below 2^26");
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || (mask_vals && !aligned16(mask_vals)))
         return fail(BSP_ERR_INVALID_ARGUMENT, "mask values, Q, K and V must be 16-byte aligned");
     const size_t esz = p->out_dtype == BSP_DTYPE_BF16 ? 2 : 4;

@@ -110,6 +110,20 @@ __device__ __forceinline__ void gl_lds16(const void* g, uint32_t lds_wave_base) 
         : "memory");
 }
 
+// The same load with a wave-uniform 64-bit base in SGPRs and a per-lane
+// 32-bit byte offset (the global saddr form): half the address data of the
+// 64-bit form, and the per-lane offset stays loop-invariant, so issuing a
+// product's loads needs no vector address arithmetic.
+__device__ __forceinline__ void gl_lds16_s(uint32_t voff_bytes, const void* sbase, uint32_t lds_wave_base) {
+    const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_wave_base);
+    __asm__ volatile(
+        "s_mov_b32 m0, %2\n\t"
+        "global_load_lds_dwordx4 %0, %1"
+        :
+        : "v"(voff_bytes), "s"(sbase), "s"(lds)
+        : "memory");
+}
+
 // Workgroup barrier without a memory fence (a fence would wait for all
 // outstanding loads); the empty asm statements keep the compiler from moving
 // memory accesses across it.
@@ -231,26 +245,61 @@ __device__ __forceinline__ void run_ring(int n, Issue&& issue, Read&& read, Mult
         if (k + S < n) issue(k + S, stage);
         stage = stage == S - 1 ? 0 : stage + 1;
     };
+    // The same step while entry k+S exists: a fixed wait and an unconditional
+    // issue, so the steady state carries no branches for the ring's tail
+    // (scalar instructions are the per-entry cost of this loop).
+    auto sync_full = [&](int k) {
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        wait_vmcnt<PER * (S - 2)>();
+        barrier_no_fence();
+        issue(k + S, stage);
+        stage = stage == S - 1 ? 0 : stage + 1;
+    };
     int k = 0;
+    // The scheduler would otherwise hoist the MFMAs above the LDS reads they
+    // do not depend on; the reads must be in flight while the MFMAs run.
+    auto fence_sched = [] { __builtin_amdgcn_sched_barrier(0); };
     if constexpr (OVERLAP) {
         Ops o1;
+        for (; k + S + 1 < n; k += 2) {
+            sync_full(k);
+            read(stage, o1);
+            fence_sched();
+            multiply(o0);
+            fence_sched();
+            sync_full(k + 1);
+            read(stage, o0);
+            fence_sched();
+            multiply(o1);
+            fence_sched();
+        }
         for (; k + 2 < n; k += 2) {
             sync(k);
             read(stage, o1);
+            fence_sched();
             multiply(o0);
+            fence_sched();
             sync(k + 1);
             read(stage, o0);
+            fence_sched();
             multiply(o1);
+            fence_sched();
         }
         if (k + 1 < n) {
             sync(k);
             read(stage, o1);
+            fence_sched();
             multiply(o0);
             multiply(o1);
         } else {
             multiply(o0);
         }
     } else {
+        for (; k + S < n; ++k) {
+            multiply(o0);
+            sync_full(k);
+            read(stage, o0);
+        }
         for (; k + 1 < n; ++k) {
             multiply(o0);
             sync(k);
@@ -259,6 +308,33 @@ __device__ __forceinline__ void run_ring(int n, Issue&& issue, Read&& read, Mult
         multiply(o0);
     }
 }
+
+// The entry words of a work item held in lanes: lane j has word 64c + j of
+// the current chunk c (first row of B in the low 32 bits, A offset / 32 in
+// the high).  They are loaded, and waited for, before the ring starts; an
+// item of more than 64 entries reloads at each chunk boundary (inside the
+// issue that crosses it) and waits there.  A scalar load per entry would put
+// the scalar cache's latency on every step of the ring.
+struct EntryWords {
+    const int64_t* ents;
+    int n;
+    uint32_t lo = 0, hi = 0;
+    __device__ __forceinline__ EntryWords(const int64_t* e, int n_, int lane) : ents(e), n(n_) { fetch(0, lane); }
+    __device__ __forceinline__ void fetch(int base, int lane) {
+        if (base + lane < n) {
+            const int64_t w = ents[base + lane];
+            lo = (uint32_t)w;
+            hi = (uint32_t)((uint64_t)w >> 32);
+        }
+        __asm__ volatile("" : "+v"(lo), "+v"(hi));
+    }
+    // Words of entry e (e increasing from call to call).
+    __device__ __forceinline__ void get(int e, int lane, uint32_t& b_word, uint32_t& a_word) {
+        if ((e & 63) == 0 && e > 0) fetch(e, lane);
+        b_word = __builtin_amdgcn_readlane(lo, e & 63);
+        a_word = __builtin_amdgcn_readlane(hi, e & 63);
+    }
+};
 
 // The 32 x TN slice of row-major B (rows brow..brow+31, columns n0..) in LDS:
 // row k at k*2*TN bytes, its 16-byte chunk c at slot c ^ 4*(k % 4).  Each of
@@ -269,7 +345,8 @@ struct BSlice {
     static constexpr int ROW_BYTES = 2 * TN;
     static constexpr int BYTES = 32 * ROW_BYTES;
     static constexpr int BI = BYTES / 1024 / 4;
-    int64_t goff[BI];  // element offsets of this lane's chunks from the slice's first row
+    uint32_t voff[BI];  // byte offsets of this lane's chunks from the slice's first row
+                        // (32 rows of B span less than 4 GB: ldb < 2^26, checked by the host)
 
     __device__ __forceinline__ BSlice(int wave, int lane, int n0, int N, int64_t ldb) {
 #pragma unroll
@@ -279,13 +356,13 @@ struct BSlice {
             const int slot = (byte % ROW_BYTES) / 16;
             // Columns past N (a partial last tile) read a valid chunk; they are not stored.
             const int col = min(n0 + 8 * (slot ^ (4 * (r & 3))), N - 8);
-            goff[j] = (int64_t)r * ldb + col;
+            voff[j] = (uint32_t)(2 * ((int64_t)r * ldb + col));
         }
     }
     __device__ __forceinline__ void issue(const uint16_t* b, int64_t ldb, uint32_t brow, uint32_t lds_wave) const {
         const uint16_t* bpan = b + (int64_t)brow * ldb;
 #pragma unroll
-        for (int j = 0; j < BI; ++j) gl_lds16(bpan + goff[j], lds_wave + j * 1024);
+        for (int j = 0; j < BI; ++j) gl_lds16_s(voff[j], bpan, lds_wave + j * 1024);
     }
 };
 
@@ -365,15 +442,15 @@ __global__ __launch_bounds__(256) void spmm_kernel(SpmmArgs p) {
 
     // Loads of one entry, per wave: lanes 0-31 fetch A segment `wave` (lane
     // 8*j + i loads A[8*wave + i][8*j .. +7]) and the wave's pieces of the B slice.
-    const int a_goff = (8 * wave + (lane & 7)) * p.lda + 8 * ((lane & 31) >> 3);
+    const uint32_t a_voff = 2 * ((8 * wave + (lane & 7)) * p.lda + 8 * ((lane & 31) >> 3));
     const uint32_t a_lds = lds0 + wave * 512;
     const uint32_t b_lds = lds0 + B_RING + wave * Slice::BI * 1024;
     // Entry words: low 32 bits = first row of B, high 32 bits = A offset / 32.
-    const uint32_t* words = (const uint32_t*)(p.ents + it.e_begin);
+    EntryWords words(p.ents + it.e_begin, it.e_end - it.e_begin, lane);
     auto issue = [&](int e, int stage) {
-        const uint32_t bw = load_const(words + 2 * e);
-        const uint32_t aw = load_const(words + 2 * e + 1);
-        if (lane < 32) gl_lds16(p.a + (int64_t)aw * 32 + a_goff, a_lds + stage * kA_BYTES);
+        uint32_t bw, aw;
+        words.get(e, lane, bw, aw);
+        if (lane < 32) gl_lds16_s(a_voff, p.a + (int64_t)aw * 32, a_lds + stage * kA_BYTES);
         bsl.issue(p.b, p.ldb, bw, b_lds + stage * Slice::BYTES);
     };
 
@@ -446,22 +523,22 @@ __global__ __launch_bounds__(256, 2) void spmm_group_kernel(SpmmArgs p) {
     // A of one entry: 4*RW segments of 512 bytes (sub-block L/4, rows
     // 8*(L%4) .. +7); segment L lands at L*512, and wave w's load j covers
     // segments 2*(w*AI + j) and 2*(w*AI + j) + 1.
-    int64_t a_goff[AI];
+    uint32_t a_voff[AI];  // byte offsets from the group's first A sub-block
 #pragma unroll
     for (int j = 0; j < AI; ++j) {
         const int L = 2 * (wave * AI + j) + (lane >> 5);
-        a_goff[j] = (int64_t)(L >> 2) * 32 * p.lda + (8 * (L & 3) + (lane & 7)) * p.lda + 8 * ((lane & 31) >> 3);
+        a_voff[j] = 2 * ((L >> 2) * 32 * p.lda + (8 * (L & 3) + (lane & 7)) * p.lda + 8 * ((lane & 31) >> 3));
     }
     const uint32_t a_lds = lds0 + wave * AI * 1024;
     const uint32_t b_lds = lds0 + B_RING + wave * Slice::BI * 1024;
     // Entry words: first row of B | A offset of the group's first stripe / 32.
-    const uint32_t* words = (const uint32_t*)(p.ents + it.e_begin);
+    EntryWords words(p.ents + it.e_begin, it.e_end - it.e_begin, lane);
     auto issue = [&](int e, int stage) {
-        const uint32_t bw = load_const(words + 2 * e);
-        const uint32_t aw = load_const(words + 2 * e + 1);
+        uint32_t bw, aw;
+        words.get(e, lane, bw, aw);
         const uint16_t* ablk = p.a + (int64_t)aw * 32;
 #pragma unroll
-        for (int j = 0; j < AI; ++j) gl_lds16(ablk + a_goff[j], a_lds + stage * A_BYTES + j * 1024);
+        for (int j = 0; j < AI; ++j) gl_lds16_s(a_voff[j], ablk, a_lds + stage * A_BYTES + j * 1024);
         bsl.issue(p.b, p.ldb, bw, b_lds + stage * Slice::BYTES);
     };
 
@@ -559,12 +636,12 @@ __global__ __launch_bounds__(256) void attention_kernel(AttentionArgs pa) {
     // K blocks and the stripe's Q rows in LDS as 16-byte chunks (c, row r) at
     // (32c + r) * 16, so that the operand of step s of row l32 (chunk 2s + q)
     // is one conflict-free ds_read_b128.  Wave w loads chunks [w*DK, (w+1)*DK).
-    int64_t k_goff[KI];
+    uint32_t k_voff[KI];  // byte offsets from the block's first key row
     int64_t q_goff[KI];
 #pragma unroll
     for (int j = 0; j < KI; ++j) {
         const int ci = wave * DK + j * K_LANES + (lane & (K_LANES - 1));
-        k_goff[j] = (int64_t)(ci & 31) * pa.ldk + 8 * (ci >> 5);
+        k_voff[j] = (uint32_t)(2 * ((int64_t)(ci & 31) * pa.ldk + 8 * (ci >> 5)));
         q_goff[j] = (int64_t)(ci & 31) * pa.ldq + 8 * (ci >> 5);
     }
     const int n = it.e_end - it.e_begin;
@@ -581,19 +658,19 @@ __global__ __launch_bounds__(256) void attention_kernel(AttentionArgs pa) {
     // Q^T operands of the stripe: lane (query l32, half q) holds
     // Q[row][16s + 8q .. +7] for every 16-deep step s of the head dimension.
     u32x4 qv[DK / 16];
-    const int a_goff = (8 * wave + (lane & 7)) * p.lda + 8 * ((lane & 31) >> 3);
+    const uint32_t a_voff = 2 * ((8 * wave + (lane & 7)) * p.lda + 8 * ((lane & 31) >> 3));
     const uint32_t a_lds = lds0 + wave * 512;
     const uint32_t k_lds = lds0 + K_RING + wave * DK * 16;
     const uint32_t b_lds = lds0 + B_RING + wave * Slice::BI * 1024;
-    const uint32_t* words = (const uint32_t*)(p.ents + it.e_begin);
+    EntryWords words(p.ents + it.e_begin, n, lane);
     auto issue = [&](int e, int stage) {
-        const uint32_t bw = load_const(words + 2 * e);  // first key of the block
-        const uint32_t aw = load_const(words + 2 * e + 1);
-        if (lane < 32) gl_lds16(p.a + (int64_t)aw * 32 + a_goff, a_lds + stage * kA_BYTES);
+        uint32_t bw, aw;  // first key of the block, mask block offset / 32
+        words.get(e, lane, bw, aw);
+        if (lane < 32) gl_lds16_s(a_voff, p.a + (int64_t)aw * 32, a_lds + stage * kA_BYTES);
         const uint16_t* kblk = pa.k + (int64_t)bw * pa.ldk;
 #pragma unroll
         for (int j = 0; j < KI; ++j)
-            if (lane < K_LANES) gl_lds16(kblk + k_goff[j], k_lds + stage * K_BYTES + j * K_LANES * 16);
+            if (lane < K_LANES) gl_lds16_s(k_voff[j], kblk, k_lds + stage * K_BYTES + j * K_LANES * 16);
         bsl.issue(p.b, p.ldb, bw, b_lds + stage * Slice::BYTES);
     };
 
