@@ -110,7 +110,14 @@ std::vector<int32_t> xcd_lpt_map(const std::vector<int64_t>& unit_cost, int widt
     return map;
 }
 
-std::vector<int32_t> xcd_tile_map(const std::vector<int64_t>& item_cost, int n_tiles, int col_groups) {
+void pair_rounds(std::vector<int32_t>& bin, int cus_per_xcd) {
+    const int64_t len = (int64_t)bin.size();
+    if (cus_per_xcd <= 0 || len <= cus_per_xcd || len > 2 * (int64_t)cus_per_xcd) return;
+    std::reverse(bin.begin() + cus_per_xcd, bin.end());
+}
+
+std::vector<int32_t> xcd_tile_map(const std::vector<int64_t>& item_cost, int n_tiles, int col_groups,
+                                  int cus_per_xcd) {
     if (col_groups < 1 || kNumXcd % col_groups != 0 || n_tiles % col_groups != 0) col_groups = 1;
     const int row_groups = kNumXcd / col_groups;
     const int64_t nitems = (int64_t)item_cost.size();
@@ -135,6 +142,7 @@ std::vector<int32_t> xcd_tile_map(const std::vector<int64_t>& item_cost, int n_t
             auto& b = bins[rg * col_groups + cg];
             for (int32_t u : rows[rg])
                 for (int t = cg * tpg; t < (cg + 1) * tpg; ++t) b.push_back(u * n_tiles + t);
+            pair_rounds(b, cus_per_xcd);
         }
     size_t maxlen = 0;
     for (auto& b : bins) maxlen = std::max(maxlen, b.size());
@@ -296,7 +304,11 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
     cg = env_int("BSP_SPMM_XCD_COLS", cg);
     if (cg < 1 || kNumXcd % cg != 0 || s.n_tiles % cg != 0) cg = 1;
     s.xcd_col_groups = (int32_t)cg;
-    s.wgmap = xcd_tile_map(cost, s.n_tiles, (int)cg);
+    // Heavy-with-light pairing on a compute unit pays once rows carry a few
+    // entries each (at about one entry per row the store dominates and the
+    // plain longest-first order measured faster).
+    const int pair_cus = (int)env_int("BSP_SPMM_PAIR_CUS", mean >= 4 ? num_cus / kNumXcd : 0);
+    s.wgmap = xcd_tile_map(cost, s.n_tiles, (int)cg, pair_cus);
     return BSP_OK;
 }
 

@@ -173,7 +173,17 @@ int build_sddmm_schedule(const bsp_bsr_desc* mask, int64_t K, int num_cus, Sddmm
 // column group's tiles, longest first.  Each XCD then reads only its column
 // slice of B, which stays in its L2.  Returns item * n_tiles + tile per
 // workgroup id (workgroup g runs on XCD g % kNumXcd), -1 for idle slots.
-std::vector<int32_t> xcd_tile_map(const std::vector<int64_t>& item_cost, int n_tiles, int col_groups);
+// When an XCD's list fills between one and two workgroups per compute unit,
+// its second round is reversed (pair_rounds).
+std::vector<int32_t> xcd_tile_map(const std::vector<int64_t>& item_cost, int n_tiles, int col_groups,
+                                  int cus_per_xcd);
+
+// The XCD's dispatcher gives its j-th workgroup to compute unit j % C (C =
+// compute units per XCD) while every workgroup is resident, so workgroups j
+// and j + C share a unit.  On a longest-first list of C < len <= 2C entries,
+// reversing the second round pairs the heaviest with the lightest, which
+// evens out the work per compute unit (the two share its load path).
+void pair_rounds(std::vector<int32_t>& bin, int cus_per_xcd);
 
 // Spreads weighted units over the XCDs (longest first onto the least-loaded
 // XCD), then lays them out so that workgroup id g runs on XCD g % kNumXcd in

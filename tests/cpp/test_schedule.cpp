@@ -1,0 +1,355 @@
+// Host scheduler checks (tenstorrent-wh-blockspmm_amd/csrc/bsp_schedule.cpp),
+// built with g++ from the scheduler's source alone: no device and no HIP.
+//
+// For SpMM, SDDMM and SpGEMM plans over generated structures (uniform,
+// skewed, duplicate columns, empty rows, large and non-square blocks) it
+// checks that the work lists the kernels walk are exact: every product of the
+// reference's loops (block_spmm/inc/bsr_matrix.hpp:954-1000,
+// sparse_common/bsr_matrix.hpp:816-857 and :741-810) appears once, in the
+// reference's order within a row, with the right operand offsets; that the
+// workgroup maps hold every unit once on the XCD its column group names; and
+// that a compute unit's two workgroups pair a heavy row with a light one.
+//
+//   test_schedule          exit status 0 when every check passes
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <map>
+#include <random>
+#include <set>
+#include <string>
+#include <vector>
+
+#include "bsp_schedule.hpp"
+
+using namespace bsp;
+
+namespace {
+
+int g_fail = 0;
+
+void expect(bool ok, const std::string& what) {
+    if (!ok) {
+        ++g_fail;
+        if (g_fail < 40) std::printf("  FAIL: %s\n", what.c_str());
+    }
+}
+
+struct Bsr {
+    int64_t H, W, R, C;
+    std::vector<int32_t> indptr, indices;
+    bsp_bsr_desc desc() const {
+        return {H, W, R, C, (int64_t)indices.size(), indptr.data(), indices.data()};
+    }
+};
+
+// Uniform distinct positions, columns ascending per row.
+Bsr uniform(int64_t H, int64_t W, int64_t R, int64_t C, int64_t nnzb, uint32_t seed) {
+    std::mt19937 rng(seed);
+    const int64_t nbr = H / R, nbc = W / C;
+    std::vector<int64_t> all(nbr * nbc);
+    for (int64_t i = 0; i < (int64_t)all.size(); ++i) all[i] = i;
+    std::shuffle(all.begin(), all.end(), rng);
+    all.resize(nnzb);
+    std::sort(all.begin(), all.end());
+    Bsr b{H, W, R, C, std::vector<int32_t>(nbr + 1, 0), {}};
+    for (int64_t f : all) {
+        ++b.indptr[f / nbc + 1];
+        b.indices.push_back((int32_t)(f % nbc));
+    }
+    for (int64_t i = 0; i < nbr; ++i) b.indptr[i + 1] += b.indptr[i];
+    return b;
+}
+
+// Rows drawn with a cubic skew; columns random with repeats (duplicates and
+// unsorted columns, as the reference's FILL_COL produces).
+Bsr skewed(int64_t H, int64_t W, int64_t R, int64_t C, int64_t nnzb, uint32_t seed) {
+    std::mt19937 rng(seed);
+    std::uniform_real_distribution<double> u(0.0, 1.0);
+    const int64_t nbr = H / R, nbc = W / C;
+    std::vector<std::vector<int32_t>> rows(nbr);
+    for (int64_t k = 0; k < nnzb; ++k) {
+        const double x = u(rng);
+        rows[std::min<int64_t>(nbr - 1, (int64_t)(nbr * x * x * x))].push_back((int32_t)(rng() % nbc));
+    }
+    Bsr b{H, W, R, C, std::vector<int32_t>(nbr + 1, 0), {}};
+    for (int64_t i = 0; i < nbr; ++i) {
+        b.indptr[i + 1] = b.indptr[i] + (int32_t)rows[i].size();
+        b.indices.insert(b.indices.end(), rows[i].begin(), rows[i].end());
+    }
+    return b;
+}
+
+void check_spmm(const Bsr& a, int64_t N, int cus, const std::string& name) {
+    SpmmSchedule s;
+    std::string msg;
+    const bsp_bsr_desc d = a.desc();
+    const int st = build_spmm_schedule(&d, N, cus, s, msg);
+    expect(st == BSP_OK, name + ": build " + msg);
+    if (st != BSP_OK) return;
+    const int64_t RS = a.R / kSub, CS = a.C / kSub, G = s.group;
+    expect(G >= 1 && RS % G == 0, name + ": group divides R/32");
+    // Entries: per group of stripes, the blocks of the row in CSR order and
+    // their 32-column steps; B row and A sub-block offset of each.
+    std::vector<int32_t> want_row;
+    std::vector<int64_t> want_off;
+    std::vector<int64_t> stripe_begin;
+    for (int64_t sr = 0; sr < a.H / kSub; sr += G) {
+        stripe_begin.push_back((int64_t)want_row.size());
+        const int64_t i = sr / RS, sub = sr % RS;
+        for (int64_t blk = a.indptr[i]; blk < a.indptr[i + 1]; ++blk)
+            for (int64_t t = 0; t < CS; ++t) {
+                want_row.push_back((int32_t)(a.indices[blk] * a.C + kSub * t));
+                want_off.push_back(blk * a.R * a.C + kSub * sub * a.C + kSub * t);
+            }
+    }
+    stripe_begin.push_back((int64_t)want_row.size());
+    expect(s.ent_row == want_row, name + ": entry B rows");
+    expect(s.ent_off == want_off, name + ": entry A offsets");
+    const std::vector<int64_t> packed = spmm_packed_entries(s);
+    bool pk = packed.size() == want_row.size();
+    for (size_t e = 0; pk && e < packed.size(); ++e)
+        pk = (uint32_t)packed[e] == (uint32_t)want_row[e] && (packed[e] >> 32) == want_off[e] / kSub;
+    expect(pk, name + ": packed entries");
+    // Items partition each stripe group's entries in order; split pieces
+    // stay within the split limit and own consecutive slots.
+    std::map<int32_t, std::vector<const SpmmItem*>> by_row;
+    for (const SpmmItem& it : s.items) by_row[it.row].push_back(&it);
+    int64_t covered = 0;
+    for (auto& [row, its] : by_row) {
+        expect(row % G == 0, name + ": item row aligned to the group");
+        const int64_t gi = row / G;
+        int64_t at = stripe_begin[gi];
+        for (size_t k = 0; k < its.size(); ++k) {
+            expect(its[k]->e_begin == at, name + ": items contiguous");
+            at = its[k]->e_end;
+            covered += its[k]->e_end - its[k]->e_begin;
+            if (its.size() > 1) {
+                expect(its[k]->slot == its[0]->base + (int32_t)k, name + ": piece slots consecutive");
+                expect(its[k]->npieces == (int32_t)its.size(), name + ": piece count");
+                expect(its[k]->e_end - its[k]->e_begin <= s.split_limit, name + ": piece within the limit");
+            } else {
+                expect(its[k]->slot == -1, name + ": whole row has no slot");
+            }
+        }
+        expect(at == stripe_begin[gi + 1], name + ": items end at the stripe group's end");
+    }
+    expect(covered == (int64_t)want_row.size(), name + ": items cover every entry once");
+    // Workgroup map: every (item, tile) once; the tile's column group names
+    // the XCD's column group; all tiles of a column group of one item share
+    // an XCD.
+    const int64_t nunits = (int64_t)s.items.size() * s.n_tiles;
+    expect(s.wgmap.size() % kNumXcd == 0, name + ": grid multiple of 8");
+    std::vector<int> seen(nunits, 0);
+    std::vector<int> xcd_of(nunits, -1);
+    const int cg = s.xcd_col_groups, tpg = s.n_tiles / cg;
+    for (size_t g = 0; g < s.wgmap.size(); ++g) {
+        const int32_t u = s.wgmap[g];
+        if (u < 0) continue;
+        expect(u < nunits, name + ": unit in range");
+        if (u >= nunits) continue;
+        ++seen[u];
+        xcd_of[u] = (int)(g % kNumXcd);
+        expect((int)(g % kNumXcd) % cg == (u % s.n_tiles) / tpg, name + ": tile on its column group's XCD");
+    }
+    bool once = true;
+    for (int64_t u = 0; u < nunits; ++u) once = once && seen[u] == 1;
+    expect(once, name + ": every unit mapped once");
+    for (size_t it = 0; it < s.items.size(); ++it)
+        for (int t = 1; t < s.n_tiles; ++t)
+            if (t / tpg == (t - 1) / tpg)
+                expect(xcd_of[it * s.n_tiles + t] == xcd_of[it * s.n_tiles + t - 1], name + ": item's tiles share an XCD");
+    const std::vector<SpmmWg> recs = spmm_wg_records(s);
+    bool rec_ok = recs.size() == s.wgmap.size();
+    for (size_t g = 0; rec_ok && g < recs.size(); ++g) {
+        const int32_t u = s.wgmap[g];
+        if (u < 0) {
+            rec_ok = recs[g].row == -1;
+            continue;
+        }
+        const SpmmItem& it = s.items[u / s.n_tiles];
+        rec_ok = recs[g].row == it.row && recs[g].e_begin == it.e_begin && recs[g].e_end == it.e_end &&
+                 recs[g].slot == it.slot && recs[g].tile == u % s.n_tiles;
+    }
+    expect(rec_ok, name + ": workgroup records follow the map");
+    const std::vector<SpmmSplit> splits = spmm_splits(s);
+    expect((int64_t)splits.size() == s.n_split_rows, name + ": one split record per split stripe");
+    std::printf("%-34s items %5zu tiles %d grid %5zu split rows %3d group %d\n", name.c_str(), s.items.size(),
+                s.n_tiles, s.wgmap.size(), s.n_split_rows, s.group);
+}
+
+// The pairing of a compute unit's two workgroups: on a longest-first XCD
+// list of C < len <= 2C units, the first round (slots j < C) stays longest
+// first and the second round runs shortest first, so slot j's partner at
+// j + C is the (len - 1 - j)-th longest.
+void check_pairing() {
+    std::vector<int32_t> bin(48);
+    for (int i = 0; i < 48; ++i) bin[i] = i;
+    pair_rounds(bin, 32);
+    bool ok = true;
+    for (int j = 0; j < 32; ++j) ok = ok && bin[j] == j;
+    for (int j = 0; j < 16; ++j) ok = ok && bin[32 + j] == 47 - j;
+    expect(ok, "pair_rounds: second round reversed");
+    std::vector<int32_t> one(32), three(65);
+    for (int i = 0; i < 32; ++i) one[i] = i;
+    for (int i = 0; i < 65; ++i) three[i] = i;
+    std::vector<int32_t> one0 = one, three0 = three;
+    pair_rounds(one, 32);
+    pair_rounds(three, 32);
+    expect(one == one0 && three == three0, "pair_rounds: one round or more than two left alone");
+    // Through the map: 64 items of distinct costs on one column group give
+    // each XCD 8 items x 4 tiles = 32 units for 4 compute units per XCD,
+    // outside the window; 16 units (4 items x 4 tiles) against 8 units per
+    // XCD are paired: per XCD, unit costs fall over the first 8 slots and
+    // rise over the next 8.
+    std::vector<int64_t> cost(32);
+    for (int i = 0; i < 32; ++i) cost[i] = 1000 - 7 * i;
+    const std::vector<int32_t> map = xcd_tile_map(cost, 4, 1, 8);
+    bool shape = map.size() == 16 * kNumXcd;
+    for (int x = 0; shape && x < kNumXcd; ++x) {
+        std::vector<int64_t> c;
+        for (int j = 0; j < 16; ++j) c.push_back(cost[map[j * kNumXcd + x] / 4]);
+        for (int j = 1; j < 8; ++j) shape = shape && c[j] <= c[j - 1];
+        for (int j = 9; j < 16; ++j) shape = shape && c[j] >= c[j - 1];
+        // partners: the heaviest with the lightest
+        shape = shape && c[0] == *std::max_element(c.begin(), c.end()) &&
+                c[8] == *std::min_element(c.begin(), c.end());
+    }
+    expect(shape, "xcd_tile_map: heavy units paired with light ones");
+    std::printf("%-34s %s\n", "pairing", "checked");
+}
+
+void check_sddmm(const Bsr& m, int64_t K, int cus, const std::string& name) {
+    SddmmSchedule s;
+    std::string msg;
+    const bsp_bsr_desc d = m.desc();
+    const int st = build_sddmm_schedule(&d, K, cus, s, msg);
+    expect(st == BSP_OK, name + ": build " + msg);
+    if (st != BSP_OK) return;
+    const int64_t RS = m.R / kSub, CS = m.C / kSub;
+    std::vector<int32_t> want_col;
+    std::vector<int64_t> want_off, want_x;
+    for (int64_t sr = 0; sr < m.H / kSub; ++sr) {
+        const int64_t i = sr / RS, sub = sr % RS;
+        for (int64_t blk = m.indptr[i]; blk < m.indptr[i + 1]; ++blk)
+            for (int64_t t = 0; t < CS; ++t) {
+                want_col.push_back((int32_t)(m.indices[blk] * m.C + kSub * t));
+                want_off.push_back(blk * m.R * m.C + kSub * sub * m.C + kSub * t);
+                want_x.push_back(sr * kSub);
+            }
+    }
+    expect(s.ent_col == want_col, name + ": entry Y columns");
+    expect(s.ent_off == want_off, name + ": entry output offsets");
+    // Every output sub-block once (the offsets are distinct and tile the
+    // output values).
+    std::set<int64_t> offs(want_off.begin(), want_off.end());
+    expect((int64_t)offs.size() == (int64_t)want_off.size() &&
+               (int64_t)want_off.size() == (int64_t)m.indices.size() * RS * CS,
+           name + ": sub-blocks distinct");
+    int64_t at = 0;
+    bool items_ok = true;
+    for (const SddmmItem& it : s.items) {
+        items_ok = items_ok && it.e_begin == at && it.e_end > it.e_begin && it.e_end - it.e_begin <= s.chunk;
+        for (int32_t e = it.e_begin; items_ok && e < it.e_end; ++e) items_ok = want_x[e] == it.x_row0;
+        at = it.e_end;
+    }
+    expect(items_ok && at == (int64_t)want_col.size(), name + ": items partition the entries by X rows");
+    std::vector<int> seen(s.items.size(), 0);
+    for (int32_t u : s.wgmap)
+        if (u >= 0 && u < (int32_t)s.items.size()) ++seen[u];
+    expect(std::all_of(seen.begin(), seen.end(), [](int v) { return v == 1; }) && s.wgmap.size() % kNumXcd == 0,
+           name + ": every item mapped once");
+    std::printf("%-34s items %5zu chunk %d grid %5zu\n", name.c_str(), s.items.size(), s.chunk, s.wgmap.size());
+}
+
+void check_spgemm(const Bsr& a, const Bsr& b, int cus, const std::string& name) {
+    SpgemmSchedule s;
+    std::string msg;
+    const bsp_bsr_desc da = a.desc(), db = b.desc();
+    const int st = build_spgemm_schedule(&da, &db, cus, 3, 2, s, msg);
+    expect(st == BSP_OK, name + ": build " + msg);
+    if (st != BSP_OK) return;
+    const int64_t R = a.R, C = a.C, BC = b.C, RS = R / kSub, CS = C / kSub, PS = BC / kSub;
+    // Brute force: per output block row, the columns reached and the
+    // (A block, B block) pairs in A's then B's CSR order.
+    std::vector<int32_t> indptr{0}, indices;
+    std::vector<uint64_t> terms;
+    std::vector<SpgemmTask> tasks;
+    for (int64_t i = 0; i < a.H / R; ++i) {
+        std::map<int32_t, std::vector<std::pair<int32_t, int32_t>>> row;
+        for (int32_t ai = a.indptr[i]; ai < a.indptr[i + 1]; ++ai) {
+            const int32_t k = a.indices[ai];
+            for (int32_t bi = b.indptr[k]; bi < b.indptr[k + 1]; ++bi) row[b.indices[bi]].push_back({ai, bi});
+        }
+        for (auto& [j, pairs] : row) {
+            const int64_t ob = (int64_t)indices.size();
+            indices.push_back(j);
+            for (int64_t ra = 0; ra < RS; ++ra)
+                for (int64_t pb = 0; pb < PS; ++pb) {
+                    SpgemmTask t{ob * R * BC + ra * kSub * BC + pb * kSub, (int32_t)terms.size(), 0};
+                    for (auto& [ai, bi] : pairs)
+                        for (int64_t cs = 0; cs < CS; ++cs) {
+                            const uint64_t ao = (uint64_t)ai * R * C + ra * kSub * C + cs * kSub;
+                            const uint64_t bo = (uint64_t)bi * C * BC + cs * kSub * BC + pb * kSub;
+                            terms.push_back(ao / kSub | (bo / kSub) << 32);
+                        }
+                    t.t_end = (int32_t)terms.size();
+                    tasks.push_back(t);
+                }
+        }
+        indptr.push_back((int32_t)indices.size());
+    }
+    expect(s.indptr == indptr && s.indices == indices, name + ": output structure");
+    // The schedule orders tasks by XCD region; each output sub-block must
+    // still be one task holding its products in the golden's order.
+    std::map<int64_t, std::vector<uint64_t>> want, got;
+    for (const SpgemmTask& t : tasks) want[t.out_off].assign(terms.begin() + t.t_begin, terms.begin() + t.t_end);
+    bool tk = s.tasks.size() == tasks.size() && s.terms.size() == terms.size();
+    for (const SpgemmTask& t : s.tasks) {
+        tk = tk && t.t_begin <= t.t_end && t.t_end <= (int32_t)s.terms.size() && !got.count(t.out_off);
+        if (tk) got[t.out_off].assign(s.terms.begin() + t.t_begin, s.terms.begin() + t.t_end);
+    }
+    expect(tk && got == want, name + ": each sub-block's products, in order");
+    // Wave runs: grid * 4 slots, each task in exactly one run, the run's
+    // products those of its tasks.
+    expect(s.grid % kNumXcd == 0 && (int64_t)s.runs.size() == (int64_t)s.grid * 4, name + ": run slots");
+    std::vector<int> seen(s.tasks.size(), 0);
+    bool runs_ok = true;
+    for (const SpgemmRun& r : s.runs) {
+        if (r.t0 == r.t1) continue;
+        runs_ok = runs_ok && r.t0 < r.t1 && r.t1 <= (int32_t)s.tasks.size() && r.t1 - r.t0 <= kSpgemmRunTasks &&
+                  r.p0 == s.tasks[r.t0].t_begin && r.p1 == s.tasks[r.t1 - 1].t_end;
+        for (int32_t t = r.t0; runs_ok && t < r.t1; ++t) ++seen[t];
+    }
+    expect(runs_ok && std::all_of(seen.begin(), seen.end(), [](int v) { return v == 1; }),
+           name + ": runs cover every task once");
+    std::printf("%-34s out blocks %5lld tasks %6zu products %7zu grid %d\n", name.c_str(), (long long)s.nblocks,
+                s.tasks.size(), s.terms.size(), s.grid);
+}
+
+}  // namespace
+
+int main() {
+    const int cus = 256;
+    check_pairing();
+    check_spmm(uniform(4096, 4096, 32, 32, 4096, 1), 512, cus, "spmm 4096^2 25% N=512");
+    check_spmm(uniform(4096, 4096, 32, 32, 819, 2), 512, cus, "spmm 4096^2 5% N=512");
+    check_spmm(uniform(4096, 4096, 32, 32, 164, 3), 512, cus, "spmm 4096^2 1% N=512");
+    check_spmm(uniform(4096, 4096, 32, 32, 4096, 4), 160, cus, "spmm partial tile N=160");
+    check_spmm(skewed(16384, 16384, 32, 32, 5243, 5), 1024, cus, "spmm skewed, duplicates");
+    check_spmm(uniform(8192, 8192, 256, 256, 256, 6), 8192, cus, "spmm 256x256 blocks (row groups)");
+    check_spmm(uniform(2048, 1024, 64, 128, 60, 7), 256, cus, "spmm 64x128 blocks");
+    check_spmm(skewed(1024, 2048, 128, 64, 40, 8), 96, cus, "spmm 128x64 blocks, skewed");
+    check_spmm(uniform(1024, 1024, 32, 32, 0, 9), 256, cus, "spmm empty");
+    check_sddmm(uniform(4096, 4096, 32, 32, 1638, 10), 256, cus, "sddmm 4096^2 10% K=256");
+    check_sddmm(skewed(2048, 2048, 64, 32, 300, 11), 128, cus, "sddmm 64x32 blocks, skewed");
+    check_sddmm(uniform(1024, 1024, 128, 128, 20, 12), 64, cus, "sddmm 128x128 blocks");
+    check_spgemm(uniform(2048, 2048, 32, 32, 300, 13), uniform(2048, 2048, 32, 32, 300, 14), cus,
+                 "spgemm 2048^2 7% x 7%");
+    check_spgemm(skewed(1024, 512, 64, 32, 80, 15), uniform(512, 768, 32, 96, 30, 16), cus,
+                 "spgemm 64x32 x 32x96, duplicates");
+    check_spgemm(uniform(512, 512, 128, 128, 6, 17), uniform(512, 256, 128, 64, 5, 18), cus,
+                 "spgemm 128x128 x 128x64");
+    std::printf("%s (%d failed checks)\n", g_fail ? "FAIL" : "PASS", g_fail);
+    return g_fail ? 1 : 0;
+}

@@ -22,6 +22,17 @@ def _run(args, timeout):
     return p
 
 
+def test_scheduler_work_lists():
+    """tests/cpp/test_schedule: the host scheduler's SpMM, SDDMM and SpGEMM
+    work lists and workgroup maps (built from the scheduler's source with g++;
+    make rebuilds it when the source changed)."""
+    subprocess.run(["make", "-s", "-C", str(REPO / "tests" / "cpp"), "_build/test_schedule"], check=True,
+                   capture_output=True)
+    p = _run([str(BUILD / "test_schedule")], 120)
+    assert p.returncode == 0, p.stdout + p.stderr
+    assert "PASS (0 failed checks)" in p.stdout
+
+
 def test_sddmm_cpu_only_structure_mode():
     """test_sddmm <all> -1: the reference's device-free mode (structure only)."""
     p = _run([_tool("test_sddmm"), "-1", "-1"], 120)
