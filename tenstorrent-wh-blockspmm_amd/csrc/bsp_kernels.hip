@@ -994,6 +994,11 @@ __global__ __launch_bounds__(256) void sddmm_kernel(SddmmArgs p) {
 // each wave runs its whole K-deep 32x32 product, multiplies by the mask
 // block and stores it.  No loop-carried loads, so nothing the compiler waits
 // for; LDS = 320 * K bytes, two workgroups per compute unit at K = 256.
+// MASK16 (mask values 16-byte aligned): the wave fetches its 32x32 mask
+// sub-block row-wise, two 16-byte loads per lane in flight with the operands
+// (sixteen 2-byte loads per lane cost 1.4 us of 8.7 at the 10% workload);
+// after the products it stages them in its own Y panel, free by then, and
+// reads them back in the accumulator's layout with the transpose read.
 //   X (and Y^T) rows: 2K bytes, 16-byte chunk c of row r at slot
 //   c ^ (r % min(K/8, 16)) (conflict-free row reads);
 //   row-major Y panel: 64-byte rows, read with the transpose read.
@@ -1009,7 +1014,7 @@ struct Layout {
 };
 }  // namespace sddmm_shot
 
-template <int K, bool Y_COLMAJOR, bool OUT_BF16>
+template <int K, bool Y_COLMAJOR, bool OUT_BF16, bool MASK16>
 __global__ __launch_bounds__(256, 2) void sddmm_shot_kernel(SddmmArgs p) {
     using namespace spmm_detail;
     using L = sddmm_shot::Layout<K>;
@@ -1023,6 +1028,25 @@ __global__ __launch_bounds__(256, 2) void sddmm_shot_kernel(SddmmArgs p) {
     const bool has = e < it.e_end;  // uniform per wave
     const uint32_t lds0 = lds_address(smem);
     const uint32_t ylds = lds0 + (1 + wave) * L::PANEL;
+
+    // Mask values: (MASK16) 16-byte chunks c = lane, lane + 64 of the
+    // row-major 32x32 sub-block (row c / 4, columns 8 * (c % 4) ..), issued
+    // first so their fetch overlaps the operands' issue (nothing uses them
+    // before the products); otherwise this lane's 16 outputs, after the
+    // operands.
+    int64_t off = 0;
+    uint32_t mk[16];
+    u32x4 mraw[2];
+    if (has) off = load_const(p.ent_off + e);
+    if constexpr (MASK16) {
+        if (has) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int c = lane + 64 * h;
+                mraw[h] = *(const u32x4*)(p.mask + off + (int64_t)(c >> 2) * p.ldo + 8 * (c & 3));
+            }
+        }
+    }
 
     // A 32-row panel (X stripe, or 32 rows of Y^T) into LDS, load t of it:
     // slot 64t + lane holds row (64t + lane) / NC, chunk c ^ (row % SW).
@@ -1051,14 +1075,12 @@ __global__ __launch_bounds__(256, 2) void sddmm_shot_kernel(SddmmArgs p) {
             }
         }
     }
-    // Mask values of this lane's 16 outputs, in flight with the operands.
-    int64_t off = 0;
-    uint32_t mk[16];
-    if (has) {
-        off = load_const(p.ent_off + e);
+    if constexpr (!MASK16) {
+        if (has) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v)
-            mk[v] = p.mask[off + (int64_t)(8 * (v >> 2) + 4 * q + (v & 3)) * p.ldo + l32];
+            for (int v = 0; v < 16; ++v)
+                mk[v] = p.mask[off + (int64_t)(8 * (v >> 2) + 4 * q + (v & 3)) * p.ldo + l32];
+        }
     }
     wait_vmcnt<0>();
     barrier_no_fence();
@@ -1092,6 +1114,24 @@ __global__ __launch_bounds__(256, 2) void sddmm_shot_kernel(SddmmArgs p) {
             }
             acc = mfma32(a, b, acc);
         }
+    if constexpr (MASK16) {
+        // The products have consumed this wave's Y panel: stage the mask
+        // sub-block there (row-major, 64-byte rows) and read back rows
+        // 8i + 4q .. +3 of column l32 (the accumulator's values 4i .. 4i+3).
+        uint8_t* mt = smem + (1 + wave) * L::PANEL;
+        *(u32x4*)(mt + 16 * lane) = mraw[0];
+        *(u32x4*)(mt + 16 * (lane + 64)) = mraw[1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = 8 * i + 4 * q + ((lane & 15) >> 2);
+            const int col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+            const u32x4 r = ld_tr_b16(mt + row * 64 + 2 * col);
+            mk[4 * i + 0] = r.x & 0xffffu;
+            mk[4 * i + 1] = r.x >> 16;
+            mk[4 * i + 2] = r.y & 0xffffu;
+            mk[4 * i + 3] = r.y >> 16;
+        }
+    }
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
         const float val = acc[v] * bf16_to_f32((uint16_t)mk[v]);
@@ -1338,19 +1378,27 @@ static void launch_sddmm_t(const SddmmArgs& a, int grid, hipStream_t stream) {
         hipLaunchKernelGGL((sddmm_kernel<Y_COLMAJOR, OUT_BF16, false>), dim3(grid), dim3(256), 0, stream, a);
 }
 
-template <int K>
-static void launch_sddmm_shot(const SddmmArgs& a, bool y_colmajor, bool out_bf16, int grid, hipStream_t stream) {
+template <int K, bool MASK16>
+static void launch_sddmm_shot_m(const SddmmArgs& a, bool y_colmajor, bool out_bf16, int grid, hipStream_t stream) {
     if (y_colmajor) {
         if (out_bf16)
-            hipLaunchKernelGGL((sddmm_shot_kernel<K, true, true>), dim3(grid), dim3(256), 0, stream, a);
+            hipLaunchKernelGGL((sddmm_shot_kernel<K, true, true, MASK16>), dim3(grid), dim3(256), 0, stream, a);
         else
-            hipLaunchKernelGGL((sddmm_shot_kernel<K, true, false>), dim3(grid), dim3(256), 0, stream, a);
+            hipLaunchKernelGGL((sddmm_shot_kernel<K, true, false, MASK16>), dim3(grid), dim3(256), 0, stream, a);
     } else {
         if (out_bf16)
-            hipLaunchKernelGGL((sddmm_shot_kernel<K, false, true>), dim3(grid), dim3(256), 0, stream, a);
+            hipLaunchKernelGGL((sddmm_shot_kernel<K, false, true, MASK16>), dim3(grid), dim3(256), 0, stream, a);
         else
-            hipLaunchKernelGGL((sddmm_shot_kernel<K, false, false>), dim3(grid), dim3(256), 0, stream, a);
+            hipLaunchKernelGGL((sddmm_shot_kernel<K, false, false, MASK16>), dim3(grid), dim3(256), 0, stream, a);
     }
+}
+
+template <int K>
+static void launch_sddmm_shot(const SddmmArgs& a, bool y_colmajor, bool out_bf16, int grid, hipStream_t stream) {
+    if (((uintptr_t)a.mask & 15u) == 0)
+        launch_sddmm_shot_m<K, true>(a, y_colmajor, out_bf16, grid, stream);
+    else
+        launch_sddmm_shot_m<K, false>(a, y_colmajor, out_bf16, grid, stream);
 }
 
 hipError_t launch_sddmm(const SddmmArgs& a, bool y_colmajor, bool out_bf16, int grid,

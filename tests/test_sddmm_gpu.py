@@ -158,3 +158,44 @@ def test_one_shot_and_looped_kernels(K, layout, monkeypatch):
     plan.close()
     assert_parity(shot, gold, K, f"one-shot K={K} {layout}")
     assert_parity(looped, gold, K, f"looped K={K} {layout}")
+
+
+@pytest.mark.parametrize("out_dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("layout", ["row", "col"])
+@pytest.mark.parametrize("K", [64, 256])
+def test_one_shot_mask_alignment(K, layout, out_dtype):
+    """The one-shot kernel reads a 16-byte-aligned mask with row-wise vector
+    loads staged through LDS, any other with one load per value: the same
+    mask at an aligned address and two bytes past one gives the same bits,
+    held to the oracle (64x32 blocks: mask rows strided by C = 32 and 64)."""
+    import torch
+    rng = np.random.default_rng(K + 7 * (layout == "col"))
+    for R, C in ((32, 32), (64, 64)):
+        mask = with_values(W.random_positions(512, 1024, R, C, 40, rng), "RAND", seed=K + R)
+        x = W.dense_content(512, K, "RAND", rng)
+        y = W.dense_content(K, 1024, "RAND", rng)
+        yy, lay = (y, capi.ROW_MAJOR) if layout == "row" else (np.ascontiguousarray(y.T), capi.COL_MAJOR)
+        plan = capi.SddmmPlan(bsr_of(mask), K, lay, out_dtype)
+        assert plan.info()["stages"] == 1  # one-shot kernel
+        nv = mask.nblocks * R * C
+        dev = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint16).view(np.int16)).cuda()
+        dx, dy = dev(x), dev(yy)
+        aligned = dev(mask.data)
+        shifted = torch.zeros(nv + 8, dtype=torch.int16, device="cuda")
+        shifted[1:nv + 1] = aligned
+        unaligned = shifted[1:nv + 1]
+        assert aligned.data_ptr() % 16 == 0 and unaligned.data_ptr() % 16 == 2
+        outs = []
+        for dm in (aligned, unaligned):
+            if out_dtype == "f32":
+                do = torch.full((nv,), float("nan"), dtype=torch.float32, device="cuda")
+            else:
+                do = torch.full((nv,), 0x7FC0, dtype=torch.int16, device="cuda")
+            plan.run(dm, dx, dy, do, ldy=1024 if layout == "row" else K,
+                     stream=torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            outs.append(do.cpu().numpy())
+        plan.close()
+        np.testing.assert_array_equal(outs[0].view(np.uint8), outs[1].view(np.uint8))
+        got = outs[0] if out_dtype == "f32" else W.bf16_to_f32(outs[0].view(np.uint16))
+        assert_parity(got, golden_sddmm(mask, x, y), K, f"mask alignment K={K} {layout} R={R} {out_dtype}")
