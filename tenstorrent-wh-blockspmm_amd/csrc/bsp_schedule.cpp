@@ -341,31 +341,115 @@ int build_sddmm_schedule(const bsp_bsr_desc* m, int64_t K, int num_cus, SddmmSch
     q = std::min<int64_t>(64, std::max<int64_t>(1, q));  // the kernel holds an item's entries in one wave
     s.chunk = (int32_t)q;
 
-    s.items.clear();
-    s.ent_col.clear();
-    s.ent_off.clear();
-    s.ent_col.reserve(total);
-    s.ent_off.reserve(total);
-    s.max_item_entries = 0;
-    std::vector<int64_t> cost;
-    for (int64_t sr = 0; sr < nsr; ++sr) {
-        const int64_t i = sr / RS, sub = sr % RS;
-        const int32_t e0 = (int32_t)s.ent_col.size();
-        for (int64_t blk = m->indptr[i]; blk < m->indptr[i + 1]; ++blk) {
-            for (int64_t t = 0; t < CS; ++t) {
-                s.ent_col.push_back((int32_t)((int64_t)m->indices[blk] * m->C + kSub * t));
-                s.ent_off.push_back(blk * m->R * m->C + kSub * sub * m->C + kSub * t);
+    // Items and the workgroup map for `bands` contiguous bands of mask
+    // columns: XCD x = row_group * bands + band runs the items of its row
+    // group's stripes that fall in its band (one band: items longest first
+    // over all XCDs).  An item is a run of at most q entries of one stripe
+    // and one band.
+    const int64_t ncol32 = m->W / kSub;
+    auto build = [&](int64_t bands, SddmmSchedule& o) {
+        o.chunk = (int32_t)q;
+        o.items.clear();
+        o.ent_col.clear();
+        o.ent_off.clear();
+        o.ent_col.reserve(total);
+        o.ent_off.reserve(total);
+        o.max_item_entries = 0;
+        std::vector<int64_t> cost;
+        std::vector<int32_t> item_band, item_stripe;
+        std::vector<int64_t> stripe_cost(nsr, 0);
+        std::vector<std::pair<int32_t, int64_t>> ents;
+        for (int64_t sr = 0; sr < nsr; ++sr) {
+            const int64_t i = sr / RS, sub = sr % RS;
+            ents.clear();
+            for (int64_t blk = m->indptr[i]; blk < m->indptr[i + 1]; ++blk)
+                for (int64_t t = 0; t < CS; ++t)
+                    ents.push_back({(int32_t)((int64_t)m->indices[blk] * m->C + kSub * t),
+                                    blk * m->R * m->C + kSub * sub * m->C + kSub * t});
+            for (int64_t band = 0; band < bands; ++band) {
+                const int32_t e0 = (int32_t)o.ent_col.size();
+                for (const auto& [col, off] : ents)
+                    if ((col / kSub) * bands / ncol32 == band) {
+                        o.ent_col.push_back(col);
+                        o.ent_off.push_back(off);
+                    }
+                const int32_t e1 = (int32_t)o.ent_col.size();
+                for (int32_t b = e0; b < e1; b += (int32_t)q) {
+                    const int32_t b1 = std::min<int32_t>(e1, b + (int32_t)q);
+                    o.items.push_back({(int32_t)(sr * kSub), b, b1, 0});
+                    cost.push_back((b1 - b) + 1);
+                    item_band.push_back((int32_t)band);
+                    item_stripe.push_back((int32_t)sr);
+                    stripe_cost[sr] += (b1 - b) + 1;
+                    o.max_item_entries = std::max<int32_t>(o.max_item_entries, b1 - b);
+                }
             }
         }
-        const int32_t e1 = (int32_t)s.ent_col.size();
-        for (int32_t b = e0; b < e1; b += (int32_t)q) {
-            const int32_t b1 = std::min<int32_t>(e1, b + (int32_t)q);
-            s.items.push_back({(int32_t)(sr * kSub), b, b1, 0});
-            cost.push_back((b1 - b) + 1);
-            s.max_item_entries = std::max<int32_t>(s.max_item_entries, b1 - b);
+        if (bands == 1) {
+            o.wgmap = xcd_lpt_map(cost, 1);
+            return;
+        }
+        // Stripes longest first onto the least-loaded of 8 / bands row groups.
+        const int rgs = (int)(kNumXcd / bands);
+        std::vector<int32_t> order(nsr);
+        std::iota(order.begin(), order.end(), 0);
+        std::stable_sort(order.begin(), order.end(),
+                         [&](int32_t x, int32_t y) { return stripe_cost[x] > stripe_cost[y]; });
+        std::vector<int32_t> stripe_rg(nsr, 0);
+        std::vector<int64_t> load(rgs, 0);
+        for (int32_t sr : order) {
+            const int g = (int)(std::min_element(load.begin(), load.end()) - load.begin());
+            stripe_rg[sr] = g;
+            load[g] += stripe_cost[sr];
+        }
+        std::vector<std::vector<int32_t>> bins(kNumXcd);
+        for (size_t u = 0; u < o.items.size(); ++u)
+            bins[stripe_rg[item_stripe[u]] * bands + item_band[u]].push_back((int32_t)u);
+        size_t maxlen = 0;
+        for (auto& b : bins) {
+            std::stable_sort(b.begin(), b.end(), [&](int32_t x, int32_t y) { return cost[x] > cost[y]; });
+            maxlen = std::max(maxlen, b.size());
+        }
+        o.wgmap.assign(maxlen * kNumXcd, -1);
+        for (int x = 0; x < kNumXcd; ++x)
+            for (size_t j = 0; j < bins[x].size(); ++j) o.wgmap[j * kNumXcd + x] = bins[x][j];
+    };
+    // The band count: the fewest rounds of resident workgroups (the one-shot
+    // kernel fits 160 KB / (320 K) per compute unit), then the least data the
+    // busiest XCD's L2 must fetch (its distinct X stripes and Y column blocks,
+    // 64 K bytes each).  A banded mask (rows that reach nearby columns only)
+    // gains; a uniform one mostly does not.
+    const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(8, (160 * 1024) / (320 * K)));
+    const int64_t slots = per_cu * num_cus;
+    int64_t best_bands = 1, best_rounds = 0, best_bytes = 0;
+    const int64_t forced = env_int("BSP_SDDMM_XCD_COLS", 0);
+    for (int64_t bands : {1, 2, 4}) {
+        if (forced && bands != forced) continue;
+        if (bands > 1 && ncol32 < 2 * bands) continue;
+        SddmmSchedule t;
+        build(bands, t);
+        const int64_t rounds = ((int64_t)t.wgmap.size() + slots - 1) / slots;
+        int64_t worst = 0;
+        for (int x = 0; x < kNumXcd; ++x) {
+            std::vector<char> xs(nsr, 0), ys(ncol32, 0);
+            int64_t n = 0;
+            for (size_t j = x; j < t.wgmap.size(); j += kNumXcd) {
+                const int32_t u = t.wgmap[j];
+                if (u < 0) continue;
+                const SddmmItem& it = t.items[u];
+                if (!xs[it.x_row0 / kSub]) xs[it.x_row0 / kSub] = 1, ++n;
+                for (int32_t e = it.e_begin; e < it.e_end; ++e)
+                    if (!ys[t.ent_col[e] / kSub]) ys[t.ent_col[e] / kSub] = 1, ++n;
+            }
+            worst = std::max(worst, n * 64 * K);
+        }
+        if (bands == 1 || forced || rounds < best_rounds || (rounds == best_rounds && worst < best_bytes)) {
+            best_bands = bands;
+            best_rounds = rounds;
+            best_bytes = worst;
         }
     }
-    s.wgmap = xcd_lpt_map(cost, 1);
+    build(best_bands, s);
     return BSP_OK;
 }
 

@@ -18,6 +18,7 @@
 #include <random>
 #include <set>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "bsp_schedule.hpp"
@@ -74,6 +75,26 @@ Bsr skewed(int64_t H, int64_t W, int64_t R, int64_t C, int64_t nnzb, uint32_t se
     }
     Bsr b{H, W, R, C, std::vector<int32_t>(nbr + 1, 0), {}};
     for (int64_t i = 0; i < nbr; ++i) {
+        b.indptr[i + 1] = b.indptr[i] + (int32_t)rows[i].size();
+        b.indices.insert(b.indices.end(), rows[i].begin(), rows[i].end());
+    }
+    return b;
+}
+
+// Causal block bands at offsets 0..-(bands-1) plus `extra` random blocks
+// below the band (the fused attention pair's mask shape), columns ascending.
+Bsr banded(int64_t n, int64_t blk, int bands, int extra, uint32_t seed) {
+    std::mt19937 rng(seed);
+    const int64_t nb = n / blk;
+    std::vector<std::set<int32_t>> rows(nb);
+    for (int64_t i = 0; i < nb; ++i)
+        for (int d = 0; d < bands && i - d >= 0; ++d) rows[i].insert((int32_t)(i - d));
+    for (int k = 0; k < extra; ++k) {
+        const int64_t i = rng() % nb;
+        if (i > bands) rows[i].insert((int32_t)(rng() % (i - bands)));
+    }
+    Bsr b{n, n, blk, blk, std::vector<int32_t>(nb + 1, 0), {}};
+    for (int64_t i = 0; i < nb; ++i) {
         b.indptr[i + 1] = b.indptr[i] + (int32_t)rows[i].size();
         b.indices.insert(b.indices.end(), rows[i].begin(), rows[i].end());
     }
@@ -238,8 +259,21 @@ void check_sddmm(const Bsr& m, int64_t K, int cus, const std::string& name) {
                 want_x.push_back(sr * kSub);
             }
     }
-    expect(s.ent_col == want_col, name + ": entry Y columns");
-    expect(s.ent_off == want_off, name + ": entry output offsets");
+    // Within a stripe the entries may be grouped by column band (the map's
+    // XCD split); across the list, each (X rows, Y column, output offset)
+    // triple appears once.
+    std::vector<std::tuple<int64_t, int32_t, int64_t>> want_t, got_t;
+    for (size_t e = 0; e < want_col.size(); ++e) want_t.emplace_back(want_x[e], want_col[e], want_off[e]);
+    bool sizes = s.ent_col.size() == want_col.size() && s.ent_off.size() == want_off.size();
+    expect(sizes, name + ": entry count");
+    if (!sizes) return;
+    std::vector<int64_t> ent_x(s.ent_col.size(), -1);
+    for (const SddmmItem& it : s.items)
+        for (int32_t e = it.e_begin; e < it.e_end && e < (int32_t)ent_x.size(); ++e) ent_x[e] = it.x_row0;
+    for (size_t e = 0; e < s.ent_col.size(); ++e) got_t.emplace_back(ent_x[e], s.ent_col[e], s.ent_off[e]);
+    std::sort(want_t.begin(), want_t.end());
+    std::sort(got_t.begin(), got_t.end());
+    expect(want_t == got_t, name + ": entries (X rows, Y column, output offset) once each");
     // Every output sub-block once (the offsets are distinct and tile the
     // output values).
     std::set<int64_t> offs(want_off.begin(), want_off.end());
@@ -249,11 +283,23 @@ void check_sddmm(const Bsr& m, int64_t K, int cus, const std::string& name) {
     int64_t at = 0;
     bool items_ok = true;
     for (const SddmmItem& it : s.items) {
-        items_ok = items_ok && it.e_begin == at && it.e_end > it.e_begin && it.e_end - it.e_begin <= s.chunk;
-        for (int32_t e = it.e_begin; items_ok && e < it.e_end; ++e) items_ok = want_x[e] == it.x_row0;
+        items_ok = items_ok && it.e_begin == at && it.e_end > it.e_begin && it.e_end - it.e_begin <= s.chunk &&
+                   it.x_row0 % kSub == 0 && it.x_row0 < m.H;
         at = it.e_end;
     }
-    expect(items_ok && at == (int64_t)want_col.size(), name + ": items partition the entries by X rows");
+    expect(items_ok && at == (int64_t)want_col.size(), name + ": items partition the entries");
+    // An entry's output sub-block lies in its item's X rows: the block row
+    // of ent_off is x_row0's.
+    bool rows_ok = true;
+    for (const SddmmItem& it : s.items)
+        for (int32_t e = it.e_begin; e < it.e_end; ++e) {
+            const int64_t blk = s.ent_off[e] / (m.R * m.C);
+            const int64_t sub = (s.ent_off[e] % (m.R * m.C)) / (kSub * m.C);
+            int64_t row = 0;
+            while (row + 1 < (int64_t)m.indptr.size() && m.indptr[row + 1] <= blk) ++row;
+            rows_ok = rows_ok && row * m.R + sub * kSub == it.x_row0;
+        }
+    expect(rows_ok, name + ": each entry in its item's stripe");
     std::vector<int> seen(s.items.size(), 0);
     for (int32_t u : s.wgmap)
         if (u >= 0 && u < (int32_t)s.items.size()) ++seen[u];
@@ -344,6 +390,7 @@ int main() {
     check_sddmm(uniform(4096, 4096, 32, 32, 1638, 10), 256, cus, "sddmm 4096^2 10% K=256");
     check_sddmm(skewed(2048, 2048, 64, 32, 300, 11), 128, cus, "sddmm 64x32 blocks, skewed");
     check_sddmm(uniform(1024, 1024, 128, 128, 20, 12), 64, cus, "sddmm 128x128 blocks");
+    check_sddmm(banded(8192, 32, 8, 655, 20), 128, cus, "sddmm banded 8192^2 (column bands)");
     check_spgemm(uniform(2048, 2048, 32, 32, 300, 13), uniform(2048, 2048, 32, 32, 300, 14), cus,
                  "spgemm 2048^2 7% x 7%");
     check_spgemm(skewed(1024, 512, 64, 32, 80, 15), uniform(512, 768, 32, 96, 30, 16), cus,
