@@ -117,7 +117,7 @@ void pair_rounds(std::vector<int32_t>& bin, int cus_per_xcd) {
 }
 
 std::vector<int32_t> xcd_tile_map(const std::vector<int64_t>& item_cost, int n_tiles, int col_groups,
-                                  int cus_per_xcd) {
+                                  int cus_per_xcd, bool row_bands) {
     if (col_groups < 1 || kNumXcd % col_groups != 0 || n_tiles % col_groups != 0) col_groups = 1;
     const int row_groups = kNumXcd / col_groups;
     const int64_t nitems = (int64_t)item_cost.size();
@@ -126,14 +126,22 @@ std::vector<int32_t> xcd_tile_map(const std::vector<int64_t>& item_cost, int n_t
     std::stable_sort(order.begin(), order.end(),
                      [&](int32_t a, int32_t b) { return item_cost[a] > item_cost[b]; });
     std::vector<std::vector<int32_t>> rows(row_groups);
-    using Load = std::pair<int64_t, int>;
-    std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
-    for (int g = 0; g < row_groups; ++g) heap.push({0, g});
-    for (int32_t u : order) {
-        Load l = heap.top();
-        heap.pop();
-        rows[l.second].push_back(u);
-        heap.push({l.first + item_cost[u], l.second});
+    if (row_bands) {
+        // Contiguous runs of items (rows in order), equal in count (the
+        // workgroups an XCD must hold at once).
+        for (int64_t u = 0; u < nitems; ++u) rows[u * row_groups / std::max<int64_t>(1, nitems)].push_back((int32_t)u);
+        for (auto& r : rows)
+            std::stable_sort(r.begin(), r.end(), [&](int32_t a, int32_t b) { return item_cost[a] > item_cost[b]; });
+    } else {
+        using Load = std::pair<int64_t, int>;
+        std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
+        for (int g = 0; g < row_groups; ++g) heap.push({0, g});
+        for (int32_t u : order) {
+            Load l = heap.top();
+            heap.pop();
+            rows[l.second].push_back(u);
+            heap.push({l.first + item_cost[u], l.second});
+        }
     }
     const int tpg = n_tiles / col_groups;
     std::vector<std::vector<int32_t>> bins(kNumXcd);
@@ -308,7 +316,47 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
     // entries each (at about one entry per row the store dominates and the
     // plain longest-first order measured faster).
     const int pair_cus = (int)env_int("BSP_SPMM_PAIR_CUS", mean >= 4 ? num_cus / kNumXcd : 0);
-    s.wgmap = xcd_tile_map(cost, s.n_tiles, (int)cg, pair_cus);
+    s.wgmap = xcd_tile_map(cost, s.n_tiles, (int)cg, pair_cus, false);
+    // Rows in contiguous bands per XCD instead (a banded structure, whose
+    // nearby rows read nearby rows of B): kept when the busiest XCD then
+    // reads fewer distinct 32-row panels of B (per tile) and carries at most
+    // 10% more work than under the longest-first map.  (Banded attention
+    // mask, O = S*V: 6.9 -> 6.6 us; a uniform structure keeps the
+    // longest-first map.)
+    if (kNumXcd / cg > 1) {
+        const std::vector<int32_t> banded = xcd_tile_map(cost, s.n_tiles, (int)cg, pair_cus, true);
+        auto busiest = [&](const std::vector<int32_t>& map) {
+            int64_t worst = 0;
+            std::vector<int32_t> seen;
+            for (int x = 0; x < kNumXcd; ++x) {
+                seen.clear();
+                for (size_t j = x; j < map.size(); j += kNumXcd) {
+                    const int32_t u = map[j];
+                    if (u < 0) continue;
+                    const SpmmItem& it = s.items[u / s.n_tiles];
+                    for (int32_t e = it.e_begin; e < it.e_end; ++e)
+                        seen.push_back((s.ent_row[e] / kSub) * s.n_tiles + u % s.n_tiles);
+                }
+                std::sort(seen.begin(), seen.end());
+                worst = std::max<int64_t>(worst, std::unique(seen.begin(), seen.end()) - seen.begin());
+            }
+            return worst;
+        };
+        auto heaviest = [&](const std::vector<int32_t>& map) {
+            int64_t worst = 0;
+            for (int x = 0; x < kNumXcd; ++x) {
+                int64_t c = 0;
+                for (size_t j = x; j < map.size(); j += kNumXcd)
+                    if (map[j] >= 0) c += cost[map[j] / s.n_tiles];
+                worst = std::max(worst, c);
+            }
+            return worst;
+        };
+        const int64_t force = env_int("BSP_SPMM_ROW_BANDS", -1);
+        const bool fewer = busiest(banded) < busiest(s.wgmap);
+        const bool balanced = heaviest(banded) * 10 <= heaviest(s.wgmap) * 11;  // within 10%
+        if (force == 1 || (force != 0 && fewer && balanced)) s.wgmap = banded;
+    }
     return BSP_OK;
 }
 

@@ -174,9 +174,10 @@ int build_sddmm_schedule(const bsp_bsr_desc* mask, int64_t K, int num_cus, Sddmm
 // slice of B, which stays in its L2.  Returns item * n_tiles + tile per
 // workgroup id (workgroup g runs on XCD g % kNumXcd), -1 for idle slots.
 // When an XCD's list fills between one and two workgroups per compute unit,
-// its second round is reversed (pair_rounds).
+// its second round is reversed (pair_rounds).  row_bands: the row groups are
+// contiguous runs of items (rows in order) of about equal cost instead.
 std::vector<int32_t> xcd_tile_map(const std::vector<int64_t>& item_cost, int n_tiles, int col_groups,
-                                  int cus_per_xcd);
+                                  int cus_per_xcd, bool row_bands = false);
 
 // The XCD's dispatcher gives its j-th workgroup to compute unit j % C (C =
 // compute units per XCD) while every workgroup is resident, so workgroups j

@@ -387,6 +387,7 @@ int main() {
     check_spmm(uniform(2048, 1024, 64, 128, 60, 7), 256, cus, "spmm 64x128 blocks");
     check_spmm(skewed(1024, 2048, 128, 64, 40, 8), 96, cus, "spmm 128x64 blocks, skewed");
     check_spmm(uniform(1024, 1024, 32, 32, 0, 9), 256, cus, "spmm empty");
+    check_spmm(banded(8192, 32, 8, 655, 19), 128, cus, "spmm banded 8192^2 (row bands)");
     check_sddmm(uniform(4096, 4096, 32, 32, 1638, 10), 256, cus, "sddmm 4096^2 10% K=256");
     check_sddmm(skewed(2048, 2048, 64, 32, 300, 11), 128, cus, "sddmm 64x32 blocks, skewed");
     check_sddmm(uniform(1024, 1024, 128, 128, 20, 12), 64, cus, "sddmm 128x128 blocks");
