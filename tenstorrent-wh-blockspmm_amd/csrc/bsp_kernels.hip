@@ -309,6 +309,55 @@ __device__ __forceinline__ void run_ring(int n, Issue&& issue, Read&& read, Mult
     }
 }
 
+// The ring of run_ring (one operand set) with each entry's operands and
+// products in two halves (the two 16-deep k-steps): step k multiplies half 0
+// of entry k, syncs (entry k+1 landed, stage k % S free, entry k+S issued),
+// reads half 0 of entry k+1 into the registers half 0 has just released,
+// multiplies half 1 of entry k, then reads half 1 of entry k+1.  The LDS
+// reads of one entry thus run under the other's products without a second
+// operand set.
+template <int S, int PER, class Ops, class Issue, class Read, class Multiply, class Landed>
+__device__ __forceinline__ void run_ring_halves(int n, Issue&& issue, Read&& read, Multiply&& multiply,
+                                                Landed&& landed) {
+    static_assert(PER * (S - 2) < 64, "vmcnt budget");
+    if (n <= 0) return;
+#pragma unroll
+    for (int e = 0; e < S - 1; ++e)
+        if (e < n) issue(e, e);
+    Ops o;
+    wait_stages<PER, S - 2>(n - 1);  // entry 0 landed
+    barrier_no_fence();
+    landed();
+    if (S - 1 < n) issue(S - 1, S - 1);
+    read(0, o, 0);
+    read(0, o, 1);
+    int stage = 0;
+    auto fence_sched = [] { __builtin_amdgcn_sched_barrier(0); };
+    auto step = [&](int k, bool full) {
+        multiply(o, 0);
+        fence_sched();
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (full || k <= n - S)
+            wait_vmcnt<PER * (S - 2)>();
+        else
+            wait_stages<PER, S - 2>(n - 2 - k);
+        barrier_no_fence();
+        if (full || k + S < n) issue(k + S, stage);
+        stage = stage == S - 1 ? 0 : stage + 1;
+        read(stage, o, 0);
+        fence_sched();
+        multiply(o, 1);
+        fence_sched();
+        read(stage, o, 1);
+        fence_sched();
+    };
+    int k = 0;
+    for (; k + S < n; ++k) step(k, true);
+    for (; k + 1 < n; ++k) step(k, false);
+    multiply(o, 0);
+    multiply(o, 1);
+}
+
 // The entry words of a work item held in lanes: lane j has word 64c + j of
 // the current chunk c (first row of B in the low 32 bits, A offset / 32 in
 // the high).  They are loaded, and waited for, before the ring starts; an
@@ -392,13 +441,16 @@ struct BReads {
     }
     __device__ __forceinline__ void read(const uint8_t* bs, u32x4 (&o)[2][NT]) const {
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2)
+        for (int s2 = 0; s2 < 2; ++s2) read_half(bs, o, s2);
+    }
+    // The operands of k-step s2 only.
+    __device__ __forceinline__ void read_half(const uint8_t* bs, u32x4 (&o)[2][NT], int s2) const {
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                const u32x4 lo = ld_tr_b16(bs + rd[s2][0][nt]);
-                const u32x4 hi = ld_tr_b16(bs + rd[s2][1][nt]);
-                o[s2][nt] = u32x4{lo.x, lo.y, hi.x, hi.y};
-            }
+        for (int nt = 0; nt < NT; ++nt) {
+            const u32x4 lo = ld_tr_b16(bs + rd[s2][0][nt]);
+            const u32x4 hi = ld_tr_b16(bs + rd[s2][1][nt]);
+            o[s2][nt] = u32x4{lo.x, lo.y, hi.x, hi.y};
+        }
     }
 };
 
@@ -588,6 +640,113 @@ __global__ __launch_bounds__(256, 2) void spmm_group_kernel(SpmmArgs p) {
             for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) mine[v * 256 + (wc * NT + nt) * 64 + lane] = acc[i][nt][v];
+        } else {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+                store_tile32<OUT_BF16>(p, acc[i][nt], (int64_t)(it.row + st) * 32,
+                                       (int64_t)it.tile * Slice::TN + (wc * NT + nt) * 32 + l32, q);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// SpMM over 8-stripe row groups (R = 256) with a 256-column tile: a
+// workgroup owns a 256 x 256 output tile, and each wave (wr, wc) of a 2 x 2
+// grid holds 4 stripes x 4 32-column tiles, so a wave's LDS reads per entry
+// (4 A sub-blocks, 4 B tiles: 16 KB) feed 32 MFMAs, twice the products per
+// byte of the 128-column group kernel's 2 x 4.  The 256 accumulators per lane
+// fill the register file shared with the AGPRs, so one workgroup per compute
+// unit (four waves, one per SIMD), with a deeper ring (S stages of 16 KB of A
+// and 16 KB of B) and one operand set (two would spill), read in halves
+// under the other half's products (run_ring_halves).  Ring, B slice and entry
+// words are the single-stripe kernel's; split pieces leave their partials in
+// the 256-column single-stripe layout (tile t's column l at the slot's
+// ((t % 2) * 16 + v) * 256 + (t / 2) * 64 + l), which spmm_reduce_kernel<2>
+// adds.
+template <int S, bool OUT_BF16>
+__global__ __launch_bounds__(256, 1) void spmm_group_wide_kernel(SpmmArgs p) {
+    using namespace spmm_detail;
+    using Slice = BSlice<2>;
+    constexpr int RW = 8, SR = 4, NT = 4;
+    constexpr int A_BYTES = RW * kA_BYTES;
+    constexpr int AI = RW / 2;  // A load instructions per wave (two 512-byte segments each)
+    constexpr int PER = AI + Slice::BI;
+    constexpr int B_RING = S * A_BYTES;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[S * (A_BYTES + Slice::BYTES)];
+
+    const SpmmWg it = load_const(p.wgs + blockIdx.x);
+    if (it.row < 0) return;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31, q = lane >> 5;
+    const int wr = wave >> 1, wc = wave & 1;
+    const uint32_t lds0 = lds_address(smem);
+    const Slice bsl(wave, lane, it.tile * Slice::TN, p.N, p.ldb);
+    const BReads<Slice::TN, NT> brd(lane, wc * NT * 32, false);
+
+    // A of one entry: 32 segments of 512 bytes (sub-block L/4, rows
+    // 8*(L%4) .. +7); segment L lands at L*512, and wave w's load j covers
+    // segments 2*(w*AI + j) and 2*(w*AI + j) + 1.
+    uint32_t a_voff[AI];
+#pragma unroll
+    for (int j = 0; j < AI; ++j) {
+        const int L = 2 * (wave * AI + j) + (lane >> 5);
+        a_voff[j] = 2 * ((L >> 2) * 32 * p.lda + (8 * (L & 3) + (lane & 7)) * p.lda + 8 * ((lane & 31) >> 3));
+    }
+    const uint32_t a_lds = lds0 + wave * AI * 1024;
+    const uint32_t b_lds = lds0 + B_RING + wave * Slice::BI * 1024;
+    EntryWords words(p.ents + it.e_begin, it.e_end - it.e_begin, lane);
+    auto issue = [&](int e, int stage) {
+        uint32_t bw, aw;
+        words.get(e, lane, bw, aw);
+        const uint16_t* ablk = p.a + (int64_t)aw * 32;
+#pragma unroll
+        for (int j = 0; j < AI; ++j) gl_lds16_s(a_voff[j], ablk, a_lds + stage * A_BYTES + j * 1024);
+        bsl.issue(p.b, p.ldb, bw, b_lds + stage * Slice::BYTES);
+    };
+
+    const int a_rd = (l32 >> 3) * 512 + (8 * q + (l32 & 7)) * 16;  // + s * 256 + sub-block * 2 KB
+    f32x16 acc[SR][NT];
+#pragma unroll
+    for (int i = 0; i < SR; ++i)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][nt][v] = 0.0f;
+
+    struct Operands {
+        u32x4 a[SR][2];
+        u32x4 b[2][NT];
+    };
+    run_ring_halves<S, PER, Operands>(
+        it.e_end - it.e_begin, issue,
+        [&](int stage, Operands& o, int h) {
+            const uint8_t* as = smem + stage * A_BYTES;
+#pragma unroll
+            for (int i = 0; i < SR; ++i) o.a[i][h] = *(const u32x4*)(as + (wr * SR + i) * kA_BYTES + 256 * h + a_rd);
+            brd.read_half(smem + B_RING + stage * Slice::BYTES, o.b, h);
+        },
+        [&](const Operands& o, int h) {
+#pragma unroll
+            for (int i = 0; i < SR; ++i)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) acc[i][nt] = mfma32(o.a[i][h], o.b[h][nt], acc[i][nt]);
+        },
+        [] {});
+
+#pragma unroll
+    for (int i = 0; i < SR; ++i) {
+        const int st = wr * SR + i;  // stripe within the group
+        if (it.slot >= 0) {
+            const int slot = it.base + st * it.npieces + (it.slot - it.base);
+            float* mine = p.ws + ((int64_t)slot * p.n_tiles + it.tile) * (2 * 16 * 256);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const int t = wc * NT + nt;  // 32-column tile within the 256
+#pragma unroll
+                for (int v = 0; v < 16; ++v) mine[((t & 1) * 16 + v) * 256 + (t >> 1) * 64 + lane] = acc[i][nt][v];
+            }
         } else {
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt)
@@ -1313,6 +1472,11 @@ static void launch_spmm_t(const SpmmArgs& a, bool out_bf16, int grid, int n_spli
             hipLaunchKernelGGL((spmm_kernel<NTW, S, true>), dim3(grid), dim3(256), 0, stream, a);
         else
             hipLaunchKernelGGL((spmm_kernel<NTW, S, false>), dim3(grid), dim3(256), 0, stream, a);
+    } else if constexpr (G == 8 && NTW == 2) {
+        if (out_bf16)
+            hipLaunchKernelGGL((spmm_group_wide_kernel<S, true>), dim3(grid), dim3(256), 0, stream, a);
+        else
+            hipLaunchKernelGGL((spmm_group_wide_kernel<S, false>), dim3(grid), dim3(256), 0, stream, a);
     } else {
         if (out_bf16)
             hipLaunchKernelGGL((spmm_group_kernel<G, S, true>), dim3(grid), dim3(256), 0, stream, a);

@@ -308,3 +308,25 @@ def test_row_group_chosen_for_large_blocks():
     sub = W.BsrArrays(rows, a.W, 256, 256, np.ascontiguousarray(a.indptr[:rows // 256 + 1]),
                       a.indices[:nb], a.data[:nb * 65536])
     assert_parity(got[:rows], golden_spmm(sub, w["b"]), spmm_k_eff(sub), "8192^3 R=256 prefix")
+
+
+@pytest.mark.parametrize("split", [0, 3])
+@pytest.mark.parametrize("out_dtype", ["f32", "bf16"])
+def test_row_group_wide_tile(monkeypatch, split, out_dtype):
+    """256 x 256 blocks on the 256-column tile (the wide 8-stripe group
+    kernel), forced on a small shape: with and without split rows (whose
+    pieces the reduce kernel adds in the 256-column layout), both outputs,
+    held to the oracle, and the same bits on a second run."""
+    monkeypatch.setenv("BSP_SPMM_GROUP", "8")
+    monkeypatch.setenv("BSP_SPMM_WIDE_GROUP", "2")
+    monkeypatch.setenv("BSP_SPMM_SPLIT", str(split or 100000))
+    w = W.spmm_workload(2048, 2048, 512, 256, 256, 0.3, seed=90 + split)
+    plan = capi.SpmmPlan(bsr_of(w["a"]), 512, out_dtype)
+    info = plan.info()
+    assert info["group"] == 8 and info["tile_n"] == 256
+    assert (info["n_split_rows"] > 0) == bool(split)
+    got = run_spmm(w["a"], w["b"], out_dtype, plan=plan)
+    again = run_spmm(w["a"], w["b"], out_dtype, plan=plan)
+    plan.close()
+    assert_parity(got, golden_spmm(w["a"], w["b"]), spmm_k_eff(w["a"]), f"wide group split={split} {out_dtype}")
+    np.testing.assert_array_equal(got, again)
