@@ -16,6 +16,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstdlib>
 
 #include "bsp_kernels.hpp"
 
@@ -79,10 +80,13 @@ __device__ __forceinline__ T load_const(const T* ptr) {
 // multiplied.  Stage s holds (in an A array and a B array)
 //   - the entry's 32x32 A sub-block (2 KB, shared by the four waves) as four
 //     512-byte segments, segment w = rows 8w..8w+7, its 16-byte chunk
-//     8*j + r%8 = A[8w + r%8][8*j .. 8*j+7].  Wave w loads segment w from 512
-//     contiguous bytes (a 32x32 block), and the A operand of k-step s for lane
-//     (r, q) is the chunk 8*(2s+q) + r%8 of segment r/8: each 8-lane group of
-//     the ds_read_b128 reads 128 contiguous bytes;
+//     8*(j ^ (w % 2)) + r%8 = A[8w + r%8][8*j .. 8*j+7] (a_load_offset,
+//     a_read_offset).  Wave w loads segment w from 512 contiguous bytes (a
+//     32x32 block), and the A operand of k-step s for lane (r, q) is chunk
+//     2s+q of row r: each 8-lane group of the ds_read_b128 reads 128
+//     contiguous bytes, and the XOR puts rows r and r+8 (same chunk) 128
+//     bytes apart, so that each 16-lane quarter covers all 64 banks of the
+//     LDS (without it, the segments 512 bytes apart hit the same 32 banks);
 //   - the 32 x TN slice of row-major B (64*TN bytes), row k at k*2*TN bytes,
 //     its 16-byte chunk c stored at slot c ^ 4*(k % 4) (spreads the rows one
 //     transpose read touches over the LDS banks).
@@ -93,6 +97,20 @@ __device__ __forceinline__ T load_const(const T* ptr) {
 namespace spmm_detail {
 
 constexpr int kA_BYTES = 2048;
+
+// Element offset, from the sub-block's first element, of what lane `lane`
+// of a 512-byte segment load fetches for segment g (rows 8g..8g+7) of a 32x32
+// A sub-block with row stride lda: it lands at slot lane % 32 = 8*c' + r of
+// the segment, holding row 8g + r, chunk c' ^ (g % 2).
+__device__ __forceinline__ int a_load_offset(int g, int lane, int lda) {
+    return (8 * g + (lane & 7)) * lda + 8 * (((lane & 31) >> 3) ^ (g & 1));
+}
+// Byte offset in the sub-block of lane (l32, q)'s A operand of k-step 0 (chunk
+// q of row l32); k-step s adds 256 bytes (chunk 2s + q: (2s + q) ^ b = 2s + (q ^ b)).
+__device__ __forceinline__ int a_read_offset(int l32, int q) {
+    const int g = l32 >> 3;
+    return g * 512 + (8 * (q ^ (g & 1)) + (l32 & 7)) * 16;
+}
 
 // Direct global->LDS load of 16 bytes per lane: lane L's bytes land at
 // lds_wave_base + 16*L (lds_wave_base is wave-uniform).  Issued as inline asm
@@ -387,13 +405,13 @@ struct EntryWords {
 
 // The 32 x TN slice of row-major B (rows brow..brow+31, columns n0..) in LDS:
 // row k at k*2*TN bytes, its 16-byte chunk c at slot c ^ 4*(k % 4).  Each of
-// the four waves loads BI = TN/64 pieces of 1 KB.
-template <int NTW>
+// the NW waves loads BI = 64 * TN / 1024 / NW pieces of 1 KB.
+template <int NTW, int NW = 4>
 struct BSlice {
     static constexpr int TN = 128 * NTW;
     static constexpr int ROW_BYTES = 2 * TN;
     static constexpr int BYTES = 32 * ROW_BYTES;
-    static constexpr int BI = BYTES / 1024 / 4;
+    static constexpr int BI = BYTES / 1024 / NW;
     uint32_t voff[BI];  // byte offsets of this lane's chunks from the slice's first row
                         // (32 rows of B span less than 4 GB: ldb < 2^26, checked by the host)
 
@@ -494,7 +512,7 @@ __global__ __launch_bounds__(256) void spmm_kernel(SpmmArgs p) {
 
     // Loads of one entry, per wave: lanes 0-31 fetch A segment `wave` (lane
     // 8*j + i loads A[8*wave + i][8*j .. +7]) and the wave's pieces of the B slice.
-    const uint32_t a_voff = 2 * ((8 * wave + (lane & 7)) * p.lda + 8 * ((lane & 31) >> 3));
+    const uint32_t a_voff = 2 * a_load_offset(wave, lane, p.lda);
     const uint32_t a_lds = lds0 + wave * 512;
     const uint32_t b_lds = lds0 + B_RING + wave * Slice::BI * 1024;
     // Entry words: low 32 bits = first row of B, high 32 bits = A offset / 32.
@@ -506,7 +524,7 @@ __global__ __launch_bounds__(256) void spmm_kernel(SpmmArgs p) {
         bsl.issue(p.b, p.ldb, bw, b_lds + stage * Slice::BYTES);
     };
 
-    const int a_rd = (l32 >> 3) * 512 + (8 * q + (l32 & 7)) * 16;  // + s * 256
+    const int a_rd = a_read_offset(l32, q);  // + s * 256
     f32x16 acc[NTW];
 #pragma unroll
     for (int i = 0; i < NTW; ++i)
@@ -579,7 +597,7 @@ __global__ __launch_bounds__(256, 2) void spmm_group_kernel(SpmmArgs p) {
 #pragma unroll
     for (int j = 0; j < AI; ++j) {
         const int L = 2 * (wave * AI + j) + (lane >> 5);
-        a_voff[j] = 2 * ((L >> 2) * 32 * p.lda + (8 * (L & 3) + (lane & 7)) * p.lda + 8 * ((lane & 31) >> 3));
+        a_voff[j] = 2 * ((L >> 2) * 32 * p.lda + a_load_offset(L & 3, lane, p.lda));
     }
     const uint32_t a_lds = lds0 + wave * AI * 1024;
     const uint32_t b_lds = lds0 + B_RING + wave * Slice::BI * 1024;
@@ -594,7 +612,7 @@ __global__ __launch_bounds__(256, 2) void spmm_group_kernel(SpmmArgs p) {
         bsl.issue(p.b, p.ldb, bw, b_lds + stage * Slice::BYTES);
     };
 
-    const int a_rd = (l32 >> 3) * 512 + (8 * q + (l32 & 7)) * 16;  // + s * 256 + sub-block * 2 KB
+    const int a_rd = a_read_offset(l32, q);  // + s * 256 + sub-block * 2 KB
     f32x16 acc[SR][NT];
 #pragma unroll
     for (int i = 0; i < SR; ++i)
@@ -651,25 +669,29 @@ __global__ __launch_bounds__(256, 2) void spmm_group_kernel(SpmmArgs p) {
 
 // ---------------------------------------------------------------------------
 // SpMM over 8-stripe row groups (R = 256) with a 256-column tile: a
-// workgroup owns a 256 x 256 output tile, and each wave (wr, wc) of a 2 x 2
-// grid holds 4 stripes x 4 32-column tiles, so a wave's LDS reads per entry
-// (4 A sub-blocks, 4 B tiles: 16 KB) feed 32 MFMAs, twice the products per
-// byte of the 128-column group kernel's 2 x 4.  The 256 accumulators per lane
-// fill the register file shared with the AGPRs, so one workgroup per compute
-// unit (four waves, one per SIMD), with a deeper ring (S stages of 16 KB of A
-// and 16 KB of B) and one operand set (two would spill), read in halves
-// under the other half's products (run_ring_halves).  Ring, B slice and entry
-// words are the single-stripe kernel's; split pieces leave their partials in
-// the 256-column single-stripe layout (tile t's column l at the slot's
+// workgroup owns a 256 x 256 output tile, one workgroup per compute unit,
+// with a deep ring (S stages of 16 KB of A and 16 KB of B).  NW = 8 waves
+// (two per SIMD) in a 2 x 4 grid each hold 4 stripes x 2 32-column tiles
+// (128 accumulators per lane); NW = 4 waves (one per SIMD) in a 2 x 2 grid
+// hold 4 x 4 (256 accumulators, the whole register file shared with the
+// AGPRs), which halves the LDS bytes read per product but leaves no second
+// wave to hide a wave's waits behind: eight waves measure 6% faster.  Either
+// way one operand set per wave, read in halves under the other half's
+// products (run_ring_halves).  Ring, B slice and entry words are the
+// single-stripe kernel's; split pieces leave their partials in the
+// 256-column single-stripe layout (tile t's column l at the slot's
 // ((t % 2) * 16 + v) * 256 + (t / 2) * 64 + l), which spmm_reduce_kernel<2>
 // adds.
-template <int S, bool OUT_BF16>
-__global__ __launch_bounds__(256, 1) void spmm_group_wide_kernel(SpmmArgs p) {
+template <int S, bool OUT_BF16, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void spmm_group_wide_kernel(SpmmArgs p) {
     using namespace spmm_detail;
-    using Slice = BSlice<2>;
-    constexpr int RW = 8, SR = 4, NT = 4;
+    static_assert(NW == 4 || NW == 8, "waves");
+    using Slice = BSlice<2, NW>;
+    constexpr int RW = 8, SR = 4;
+    constexpr int WC = NW / 2;   // wave grid 2 x WC
+    constexpr int NT = 8 / WC;   // 32-column tiles per wave
     constexpr int A_BYTES = RW * kA_BYTES;
-    constexpr int AI = RW / 2;  // A load instructions per wave (two 512-byte segments each)
+    constexpr int AI = 4 * RW / NW / 2;  // A load instructions per wave (two 512-byte segments each)
     constexpr int PER = AI + Slice::BI;
     constexpr int B_RING = S * A_BYTES;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[S * (A_BYTES + Slice::BYTES)];
@@ -680,7 +702,7 @@ __global__ __launch_bounds__(256, 1) void spmm_group_wide_kernel(SpmmArgs p) {
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, q = lane >> 5;
-    const int wr = wave >> 1, wc = wave & 1;
+    const int wr = wave / WC, wc = wave % WC;
     const uint32_t lds0 = lds_address(smem);
     const Slice bsl(wave, lane, it.tile * Slice::TN, p.N, p.ldb);
     const BReads<Slice::TN, NT> brd(lane, wc * NT * 32, false);
@@ -692,7 +714,7 @@ __global__ __launch_bounds__(256, 1) void spmm_group_wide_kernel(SpmmArgs p) {
 #pragma unroll
     for (int j = 0; j < AI; ++j) {
         const int L = 2 * (wave * AI + j) + (lane >> 5);
-        a_voff[j] = 2 * ((L >> 2) * 32 * p.lda + (8 * (L & 3) + (lane & 7)) * p.lda + 8 * ((lane & 31) >> 3));
+        a_voff[j] = 2 * ((L >> 2) * 32 * p.lda + a_load_offset(L & 3, lane, p.lda));
     }
     const uint32_t a_lds = lds0 + wave * AI * 1024;
     const uint32_t b_lds = lds0 + B_RING + wave * Slice::BI * 1024;
@@ -706,7 +728,7 @@ __global__ __launch_bounds__(256, 1) void spmm_group_wide_kernel(SpmmArgs p) {
         bsl.issue(p.b, p.ldb, bw, b_lds + stage * Slice::BYTES);
     };
 
-    const int a_rd = (l32 >> 3) * 512 + (8 * q + (l32 & 7)) * 16;  // + s * 256 + sub-block * 2 KB
+    const int a_rd = a_read_offset(l32, q);  // + s * 256 + sub-block * 2 KB
     f32x16 acc[SR][NT];
 #pragma unroll
     for (int i = 0; i < SR; ++i)
@@ -719,21 +741,19 @@ __global__ __launch_bounds__(256, 1) void spmm_group_wide_kernel(SpmmArgs p) {
         u32x4 a[SR][2];
         u32x4 b[2][NT];
     };
-    run_ring_halves<S, PER, Operands>(
-        it.e_end - it.e_begin, issue,
-        [&](int stage, Operands& o, int h) {
-            const uint8_t* as = smem + stage * A_BYTES;
+    auto read_half = [&](int stage, Operands& o, int h) {
+        const uint8_t* as = smem + stage * A_BYTES;
 #pragma unroll
-            for (int i = 0; i < SR; ++i) o.a[i][h] = *(const u32x4*)(as + (wr * SR + i) * kA_BYTES + 256 * h + a_rd);
-            brd.read_half(smem + B_RING + stage * Slice::BYTES, o.b, h);
-        },
-        [&](const Operands& o, int h) {
+        for (int i = 0; i < SR; ++i) o.a[i][h] = *(const u32x4*)(as + (wr * SR + i) * kA_BYTES + 256 * h + a_rd);
+        brd.read_half(smem + B_RING + stage * Slice::BYTES, o.b, h);
+    };
+    auto mul_half = [&](const Operands& o, int h) {
 #pragma unroll
-            for (int i = 0; i < SR; ++i)
+        for (int i = 0; i < SR; ++i)
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt) acc[i][nt] = mfma32(o.a[i][h], o.b[h][nt], acc[i][nt]);
-        },
-        [] {});
+            for (int nt = 0; nt < NT; ++nt) acc[i][nt] = mfma32(o.a[i][h], o.b[h][nt], acc[i][nt]);
+    };
+    run_ring_halves<S, PER, Operands>(it.e_end - it.e_begin, issue, read_half, mul_half, [] {});
 
 #pragma unroll
     for (int i = 0; i < SR; ++i) {
@@ -834,7 +854,8 @@ __global__ __launch_bounds__(256) void attention_kernel(AttentionArgs pa) {
     };
 
     // Mask values of lane (query l32, half q): keys 8i + 4q .. +3 are 8 bytes
-    // of chunk i of the query's row in the A layout.
+    // of chunk i of the query's row.  The mask is loaded without the SpMM A
+    // layout's chunk XOR: segment g, chunk j of row r at (8j + r%8) * 16.
     const int m_rd = (l32 >> 3) * 512 + (l32 & 7) * 16 + 8 * q;  // + i * 128
     f32x16 acc[1];
 #pragma unroll
@@ -1373,14 +1394,14 @@ __global__ __launch_bounds__(256) void spgemm_kernel(SpgemmArgs p) {
     __asm__ volatile("" : "+v"(off_lo), "+v"(off_hi), "+v"(t_end));
 
     // Loads of one product (two 1 KB instructions each for A and B):
-    //   A: instruction h, lane L loads row 8*(2h + L/32) + L%8, 16-byte chunk
-    //      (L%32)/8 into byte 1024h + 16L: 512-byte segments of 8 rows, chunk
-    //      j of row i at (8j + i) * 16 inside its segment.
+    //   A: instruction h, lane L loads segment g = 2h + L/32: row 8g + L%8,
+    //      16-byte chunk ((L%32)/8) ^ (g%2) into byte 1024h + 16L (the SpMM
+    //      sub-block layout, a_load_offset / a_read_offset).
     //   B: instruction h, lane L loads row 16h + L/4, chunk L%4 into byte
     //      1024h + 16L: plain row-major rows of 64 bytes.
     int64_t a_goff0, a_goff1, b_goff0, b_goff1;
-    a_goff0 = (int64_t)(8 * (lane >> 5) + (lane & 7)) * p.lda + 8 * ((lane & 31) >> 3);
-    a_goff1 = a_goff0 + (int64_t)16 * p.lda;
+    a_goff0 = spmm_detail::a_load_offset(lane >> 5, lane, p.lda);
+    a_goff1 = spmm_detail::a_load_offset(2 + (lane >> 5), lane, p.lda);
     b_goff0 = (int64_t)(lane >> 2) * p.ldb + 8 * (lane & 3);
     b_goff1 = b_goff0 + (int64_t)16 * p.ldb;
     auto issue = [&](int e, int stage) {
@@ -1399,7 +1420,7 @@ __global__ __launch_bounds__(256) void spgemm_kernel(SpgemmArgs p) {
     // Operand reads: A row l32, chunk 2*s + q; B column l32 by transpose
     // reads of rows 16*s + 8*q + 4*h + (lane%16)/4, columns 16*(lane/16 % 2)
     // + 4*(lane%4) (the second k-step adds 16 rows = 1 KB).
-    const int a_rd = (l32 >> 3) * 512 + (8 * q + (l32 & 7)) * 16;  // + 256 * s
+    const int a_rd = spmm_detail::a_read_offset(l32, q);  // + 256 * s
     const int b_rd = 2048 + (8 * ((lane >> 4) >> 1) + ((lane & 15) >> 2)) * 64 +
                      2 * (16 * ((lane >> 4) & 1) + 4 * (lane & 3));  // + 256 * h + 1024 * s
 
@@ -1473,10 +1494,19 @@ static void launch_spmm_t(const SpmmArgs& a, bool out_bf16, int grid, int n_spli
         else
             hipLaunchKernelGGL((spmm_kernel<NTW, S, false>), dim3(grid), dim3(256), 0, stream, a);
     } else if constexpr (G == 8 && NTW == 2) {
-        if (out_bf16)
-            hipLaunchKernelGGL((spmm_group_wide_kernel<S, true>), dim3(grid), dim3(256), 0, stream, a);
-        else
-            hipLaunchKernelGGL((spmm_group_wide_kernel<S, false>), dim3(grid), dim3(256), 0, stream, a);
+        // Eight waves (two per SIMD, 128 x 64 outputs each) unless BSP_SPMM_WIDE_WAVES=4.
+        const char* ww = std::getenv("BSP_SPMM_WIDE_WAVES");
+        if (!(ww && std::atoi(ww) == 4)) {
+            if (out_bf16)
+                hipLaunchKernelGGL((spmm_group_wide_kernel<S, true, 8>), dim3(grid), dim3(512), 0, stream, a);
+            else
+                hipLaunchKernelGGL((spmm_group_wide_kernel<S, false, 8>), dim3(grid), dim3(512), 0, stream, a);
+        } else {
+            if (out_bf16)
+                hipLaunchKernelGGL((spmm_group_wide_kernel<S, true, 4>), dim3(grid), dim3(256), 0, stream, a);
+            else
+                hipLaunchKernelGGL((spmm_group_wide_kernel<S, false, 4>), dim3(grid), dim3(256), 0, stream, a);
+        }
     } else {
         if (out_bf16)
             hipLaunchKernelGGL((spmm_group_kernel<G, S, true>), dim3(grid), dim3(256), 0, stream, a);

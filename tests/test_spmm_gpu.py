@@ -310,9 +310,10 @@ def test_row_group_chosen_for_large_blocks():
     assert_parity(got[:rows], golden_spmm(sub, w["b"]), spmm_k_eff(sub), "8192^3 R=256 prefix")
 
 
+@pytest.mark.parametrize("waves", [4, 8])
 @pytest.mark.parametrize("split", [0, 3])
 @pytest.mark.parametrize("out_dtype", ["f32", "bf16"])
-def test_row_group_wide_tile(monkeypatch, split, out_dtype):
+def test_row_group_wide_tile(monkeypatch, waves, split, out_dtype):
     """256 x 256 blocks on the 256-column tile (the wide 8-stripe group
     kernel), forced on a small shape: with and without split rows (whose
     pieces the reduce kernel adds in the 256-column layout), both outputs,
@@ -320,6 +321,7 @@ def test_row_group_wide_tile(monkeypatch, split, out_dtype):
     monkeypatch.setenv("BSP_SPMM_GROUP", "8")
     monkeypatch.setenv("BSP_SPMM_WIDE_GROUP", "2")
     monkeypatch.setenv("BSP_SPMM_SPLIT", str(split or 100000))
+    monkeypatch.setenv("BSP_SPMM_WIDE_WAVES", str(waves))
     w = W.spmm_workload(2048, 2048, 512, 256, 256, 0.3, seed=90 + split)
     plan = capi.SpmmPlan(bsr_of(w["a"]), 512, out_dtype)
     info = plan.info()
@@ -328,5 +330,5 @@ def test_row_group_wide_tile(monkeypatch, split, out_dtype):
     got = run_spmm(w["a"], w["b"], out_dtype, plan=plan)
     again = run_spmm(w["a"], w["b"], out_dtype, plan=plan)
     plan.close()
-    assert_parity(got, golden_spmm(w["a"], w["b"]), spmm_k_eff(w["a"]), f"wide group split={split} {out_dtype}")
+    assert_parity(got, golden_spmm(w["a"], w["b"]), spmm_k_eff(w["a"]), f"wide group waves={waves} split={split} {out_dtype}")
     np.testing.assert_array_equal(got, again)
