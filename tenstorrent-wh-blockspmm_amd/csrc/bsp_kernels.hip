@@ -328,51 +328,77 @@ __device__ __forceinline__ void run_ring(int n, Issue&& issue, Read&& read, Mult
 }
 
 // The ring of run_ring (one operand set) with each entry's operands and
-// products in two halves (the two 16-deep k-steps): step k multiplies half 0
-// of entry k, syncs (entry k+1 landed, stage k % S free, entry k+S issued),
-// reads half 0 of entry k+1 into the registers half 0 has just released,
-// multiplies half 1 of entry k, then reads half 1 of entry k+1.  The LDS
-// reads of one entry thus run under the other's products without a second
-// operand set.
-template <int S, int PER, class Ops, class Issue, class Read, class Multiply, class Landed>
+// products in two halves (the two 16-deep k-steps).  Step k:
+//   1. half 0's products of entry k, interleaved one for one with the LDS
+//      reads of entry k's half 1 (into the registers half 1 released in the
+//      previous step);
+//   2. sync: the reads complete, entry k+1 landed, barrier (stage k % S is
+//      then free), entry k+S issued;
+//   3. half 1's products of entry k, interleaved with the reads of entry
+//      k+1's half 0.
+// Each wave thus issues an LDS read under every product, and no phase of a
+// step is reads alone: the two waves of a SIMD, in step with each other
+// through the barrier, would otherwise both read while the matrix core
+// idles, then both multiply.  PAIRS is the number of (product, read) pairs
+// per half.  An entry issues PER loads per wave, an even entry EXTRA more (a
+// load shared by an entry pair goes with its first entry).  read(k, stage,
+// o, h) reads half h of entry k (in stage `stage`).
+template <int S, int PER, int EXTRA, int PAIRS, class Ops, class Issue, class Read, class Multiply, class Landed>
 __device__ __forceinline__ void run_ring_halves(int n, Issue&& issue, Read&& read, Multiply&& multiply,
                                                 Landed&& landed) {
-    static_assert(PER * (S - 2) < 64, "vmcnt budget");
+    // Loads issued for entries j+1 .. last (the even ones carry EXTRA more).
+    auto after = [](int j, int last) { return (last - j) * PER + EXTRA * ((last >> 1) - (j >> 1)); };
+    constexpr int MAXW = PER * (S - 2) + EXTRA * ((S - 1) / 2);
+    static_assert(MAXW < 64, "vmcnt budget");
     if (n <= 0) return;
 #pragma unroll
     for (int e = 0; e < S - 1; ++e)
         if (e < n) issue(e, e);
     Ops o;
-    wait_stages<PER, S - 2>(n - 1);  // entry 0 landed
+    wait_stages<1, MAXW>(after(0, min(S - 2, n - 1)));  // entry 0 landed
     barrier_no_fence();
     landed();
     if (S - 1 < n) issue(S - 1, S - 1);
-    read(0, o, 0);
-    read(0, o, 1);
+    read(0, 0, o, 0);
     int stage = 0;
     auto fence_sched = [] { __builtin_amdgcn_sched_barrier(0); };
+    auto interleave = [] {
+#pragma unroll
+        for (int i = 0; i < PAIRS; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        }
+    };
     auto step = [&](int k, bool full) {
         multiply(o, 0);
+        read(k, stage, o, 1);
+        interleave();
         fence_sched();
         __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (full || k <= n - S)
-            wait_vmcnt<PER * (S - 2)>();
-        else
-            wait_stages<PER, S - 2>(n - 2 - k);
+        // Entry k+1 landed: at most the loads of the entries after it are outstanding.
+        if constexpr (EXTRA == 0 || S % 2 == 0) {
+            if (full || k <= n - S)
+                wait_vmcnt<PER * (S - 2) + EXTRA * ((S - 2) / 2)>();
+            else
+                wait_stages<1, MAXW>(after(k + 1, n - 1));
+        } else {
+            wait_stages<1, MAXW>(after(k + 1, min(k + S - 1, n - 1)));
+        }
         barrier_no_fence();
         if (full || k + S < n) issue(k + S, stage);
         stage = stage == S - 1 ? 0 : stage + 1;
-        read(stage, o, 0);
-        fence_sched();
         multiply(o, 1);
-        fence_sched();
-        read(stage, o, 1);
+        read(k + 1, stage, o, 0);
+        interleave();
         fence_sched();
     };
     int k = 0;
     for (; k + S < n; ++k) step(k, true);
     for (; k + 1 < n; ++k) step(k, false);
     multiply(o, 0);
+    read(k, stage, o, 1);
+    interleave();
+    fence_sched();
     multiply(o, 1);
 }
 
@@ -682,7 +708,7 @@ __global__ __launch_bounds__(256, 2) void spmm_group_kernel(SpmmArgs p) {
 // 256-column single-stripe layout (tile t's column l at the slot's
 // ((t % 2) * 16 + v) * 256 + (t / 2) * 64 + l), which spmm_reduce_kernel<2>
 // adds.
-template <int S, bool OUT_BF16, int NW>
+template <int S, bool OUT_BF16, int NW, bool PAIR>
 __global__ __launch_bounds__(64 * NW, 1) void spmm_group_wide_kernel(SpmmArgs p) {
     using namespace spmm_detail;
     static_assert(NW == 4 || NW == 8, "waves");
@@ -690,11 +716,15 @@ __global__ __launch_bounds__(64 * NW, 1) void spmm_group_wide_kernel(SpmmArgs p)
     constexpr int RW = 8, SR = 4;
     constexpr int WC = NW / 2;   // wave grid 2 x WC
     constexpr int NT = 8 / WC;   // 32-column tiles per wave
-    constexpr int A_BYTES = RW * kA_BYTES;
-    constexpr int AI = 4 * RW / NW / 2;  // A load instructions per wave (two 512-byte segments each)
-    constexpr int PER = AI + Slice::BI;
-    constexpr int B_RING = S * A_BYTES;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[S * (A_BYTES + Slice::BYTES)];
+    constexpr int A_BYTES = RW * kA_BYTES;  // A of one entry (16 KB)
+    constexpr int AI = 4 * RW / NW / 2;     // per entry and wave: A load instructions of 1 KB
+    constexpr int NP = S / 2 + 1;           // pair slots (the pairs of entries k .. k+S-1, and one being filled)
+    constexpr int A_RING = PAIR ? NP * 2 * A_BYTES : S * A_BYTES;
+    constexpr int AL = PAIR ? 2 * AI : AI;  // A loads per wave and issue (an even entry's, for a pair)
+    constexpr int PER = PAIR ? Slice::BI : AI + Slice::BI;
+    constexpr int EXTRA = PAIR ? AL : 0;
+    constexpr int B_RING = A_RING;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[A_RING + S * Slice::BYTES];
 
     const SpmmWg it = load_const(p.wgs + blockIdx.x);
     if (it.row < 0) return;
@@ -707,28 +737,62 @@ __global__ __launch_bounds__(64 * NW, 1) void spmm_group_wide_kernel(SpmmArgs p)
     const Slice bsl(wave, lane, it.tile * Slice::TN, p.N, p.ldb);
     const BReads<Slice::TN, NT> brd(lane, wc * NT * 32, false);
 
-    // A of one entry: 32 segments of 512 bytes (sub-block L/4, rows
-    // 8*(L%4) .. +7); segment L lands at L*512, and wave w's load j covers
-    // segments 2*(w*AI + j) and 2*(w*AI + j) + 1.
-    uint32_t a_voff[AI];
+    // A without pairs: of one entry, 32 segments of 512 bytes (sub-block
+    // L/4, rows 8*(L%4) .. +7); segment L lands at L*512, and wave w's load j
+    // covers segments 2*(w*AI + j) and 2*(w*AI + j) + 1.
+    // A with pairs (C a multiple of 64: entries 2m and 2m+1 of an item are the
+    // two 32-column halves of the same 64 columns of one block): an even
+    // entry fetches both, 256 rows of 128 bytes, so that every request is a
+    // whole 128-byte line (a 64-byte half-line request costs the L1 as much
+    // as a whole line, and the DMA-only loop measured 189 us against 138 us
+    // on 256x256 blocks).  Load I (0..31) holds rows 8I .. 8I+7 of the group,
+    // row r of them at I*1024 + (r%8)*128 with its 16-byte chunk c at
+    // position c ^ ((r%8)/2 + 4*(I%2)): each 16-lane quarter of a read then
+    // covers every bank.  Pair m sits in slot m % NP.
+    uint32_t a_voff[AL];
 #pragma unroll
-    for (int j = 0; j < AI; ++j) {
-        const int L = 2 * (wave * AI + j) + (lane >> 5);
-        a_voff[j] = 2 * ((L >> 2) * 32 * p.lda + a_load_offset(L & 3, lane, p.lda));
+    for (int j = 0; j < AL; ++j) {
+        if constexpr (PAIR) {
+            const int I = wave * AL + j, r = lane >> 3;
+            const int c = (lane & 7) ^ ((r >> 1) | ((I & 1) << 2));
+            a_voff[j] = 2 * ((8 * I + r) * p.lda + 8 * c);
+        } else {
+            const int L = 2 * (wave * AI + j) + (lane >> 5);
+            a_voff[j] = 2 * ((L >> 2) * 32 * p.lda + a_load_offset(L & 3, lane, p.lda));
+        }
     }
-    const uint32_t a_lds = lds0 + wave * AI * 1024;
+    const uint32_t a_lds = lds0 + wave * AL * 1024;
     const uint32_t b_lds = lds0 + B_RING + wave * Slice::BI * 1024;
     EntryWords words(p.ents + it.e_begin, it.e_end - it.e_begin, lane);
     auto issue = [&](int e, int stage) {
         uint32_t bw, aw;
         words.get(e, lane, bw, aw);
         const uint16_t* ablk = p.a + (int64_t)aw * 32;
+        if constexpr (PAIR) {
+            if ((e & 1) == 0) {
+                const uint32_t slot = a_lds + ((e >> 1) % NP) * (2 * A_BYTES);
 #pragma unroll
-        for (int j = 0; j < AI; ++j) gl_lds16_s(a_voff[j], ablk, a_lds + stage * A_BYTES + j * 1024);
+                for (int j = 0; j < AL; ++j) gl_lds16_s(a_voff[j], ablk, slot + j * 1024);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < AL; ++j) gl_lds16_s(a_voff[j], ablk, a_lds + stage * A_BYTES + j * 1024);
+        }
         bsl.issue(p.b, p.ldb, bw, b_lds + stage * Slice::BYTES);
     };
 
     const int a_rd = a_read_offset(l32, q);  // + s * 256 + sub-block * 2 KB
+    // With pairs, lane (l32, q)'s A operand of k-step s of the pair's half
+    // ph: row l32 of the stripe (load 4*stripe + l32/8, row r = l32%8),
+    // chunk 4*ph + 2*s + q, at position chunk ^ (r/2 + 4*((l32/8)%2)); half
+    // ph = 1 flips bit 2 of the position (byte offset bit 6).
+    int a_rdp[2];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+        const int r = l32 & 7;
+        const int c = (2 * s2 + q) ^ ((r >> 1) | (((l32 >> 3) & 1) << 2));
+        a_rdp[s2] = (l32 >> 3) * 1024 + r * 128 + c * 16;
+    }
     f32x16 acc[SR][NT];
 #pragma unroll
     for (int i = 0; i < SR; ++i)
@@ -741,10 +805,17 @@ __global__ __launch_bounds__(64 * NW, 1) void spmm_group_wide_kernel(SpmmArgs p)
         u32x4 a[SR][2];
         u32x4 b[2][NT];
     };
-    auto read_half = [&](int stage, Operands& o, int h) {
-        const uint8_t* as = smem + stage * A_BYTES;
+    auto read_half = [&](int k, int stage, Operands& o, int h) {
+        if constexpr (PAIR) {
+            const uint8_t* as = smem + ((k >> 1) % NP) * (2 * A_BYTES);
+            const int off = a_rdp[h] ^ ((k & 1) << 6);
 #pragma unroll
-        for (int i = 0; i < SR; ++i) o.a[i][h] = *(const u32x4*)(as + (wr * SR + i) * kA_BYTES + 256 * h + a_rd);
+            for (int i = 0; i < SR; ++i) o.a[i][h] = *(const u32x4*)(as + (wr * SR + i) * 4096 + off);
+        } else {
+            const uint8_t* as = smem + stage * A_BYTES;
+#pragma unroll
+            for (int i = 0; i < SR; ++i) o.a[i][h] = *(const u32x4*)(as + (wr * SR + i) * kA_BYTES + 256 * h + a_rd);
+        }
         brd.read_half(smem + B_RING + stage * Slice::BYTES, o.b, h);
     };
     auto mul_half = [&](const Operands& o, int h) {
@@ -753,7 +824,7 @@ __global__ __launch_bounds__(64 * NW, 1) void spmm_group_wide_kernel(SpmmArgs p)
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) acc[i][nt] = mfma32(o.a[i][h], o.b[h][nt], acc[i][nt]);
     };
-    run_ring_halves<S, PER, Operands>(it.e_end - it.e_begin, issue, read_half, mul_half, [] {});
+    run_ring_halves<S, PER, EXTRA, SR * NT, Operands>(it.e_end - it.e_begin, issue, read_half, mul_half, [] {});
 
 #pragma unroll
     for (int i = 0; i < SR; ++i) {
@@ -1494,19 +1565,29 @@ static void launch_spmm_t(const SpmmArgs& a, bool out_bf16, int grid, int n_spli
         else
             hipLaunchKernelGGL((spmm_kernel<NTW, S, false>), dim3(grid), dim3(256), 0, stream, a);
     } else if constexpr (G == 8 && NTW == 2) {
-        // Eight waves (two per SIMD, 128 x 64 outputs each) unless BSP_SPMM_WIDE_WAVES=4.
+        // Eight waves (two per SIMD, 128 x 64 outputs each) unless BSP_SPMM_WIDE_WAVES=4;
+        // A fetched in entry pairs when C is a multiple of 64 (the plan then
+        // starts every item at an even entry of its block).
         const char* ww = std::getenv("BSP_SPMM_WIDE_WAVES");
-        if (!(ww && std::atoi(ww) == 4)) {
-            if (out_bf16)
-                hipLaunchKernelGGL((spmm_group_wide_kernel<S, true, 8>), dim3(grid), dim3(512), 0, stream, a);
-            else
-                hipLaunchKernelGGL((spmm_group_wide_kernel<S, false, 8>), dim3(grid), dim3(512), 0, stream, a);
+        const bool four = ww && std::atoi(ww) == 4;
+        const bool pair = a.lda % 64 == 0;
+#define BSP_WIDE(NW_, PAIR_)                                                                                  \
+    do {                                                                                                      \
+        if (out_bf16)                                                                                         \
+            hipLaunchKernelGGL((spmm_group_wide_kernel<S, true, NW_, PAIR_>), dim3(grid), dim3(64 * NW_), 0,  \
+                               stream, a);                                                                    \
+        else                                                                                                  \
+            hipLaunchKernelGGL((spmm_group_wide_kernel<S, false, NW_, PAIR_>), dim3(grid), dim3(64 * NW_), 0, \
+                               stream, a);                                                                    \
+    } while (0)
+        if (four) {
+            if (pair) BSP_WIDE(4, true);
+            else BSP_WIDE(4, false);
         } else {
-            if (out_bf16)
-                hipLaunchKernelGGL((spmm_group_wide_kernel<S, true, 4>), dim3(grid), dim3(256), 0, stream, a);
-            else
-                hipLaunchKernelGGL((spmm_group_wide_kernel<S, false, 4>), dim3(grid), dim3(256), 0, stream, a);
+            if (pair) BSP_WIDE(8, true);
+            else BSP_WIDE(8, false);
         }
+#undef BSP_WIDE
     } else {
         if (out_bf16)
             hipLaunchKernelGGL((spmm_group_kernel<G, S, true>), dim3(grid), dim3(256), 0, stream, a);

@@ -274,6 +274,7 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
     int64_t L = std::max<int64_t>({32, 2 * mean, (fair + 1) / 2});
     L = env_int("BSP_SPMM_SPLIT", L);
     if (L < 1) L = 1;
+    if (a->C % 64 == 0 && L < 2) L = 2;  // pieces hold whole entry pairs (below)
     s.split_limit = (int32_t)L;
 
     s.items.clear();
@@ -304,13 +305,18 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
             cost.push_back((cnt + 2) * group);
             s.max_item_entries = std::max<int32_t>(s.max_item_entries, (int32_t)cnt);
         } else {
-            const int64_t np = (cnt + L - 1) / L;
+            // Pieces start at an even entry of the block when C is a multiple
+            // of 64 (a row's count is then even): the kernels may fetch A for
+            // the two 32-column halves of 64 columns together.
+            const int64_t unit = (a->C % 64 == 0) ? 2 : 1;
+            const int64_t cu = cnt / unit, lu = std::max<int64_t>(1, L / unit);
+            const int64_t np = (cu + lu - 1) / lu;
             const int32_t base = s.n_slots;
             s.n_slots += (int32_t)(np * group);
             s.n_split_rows += group;
             for (int64_t p = 0; p < np; ++p) {
-                const int32_t b0 = e0 + (int32_t)(cnt * p / np);
-                const int32_t b1 = e0 + (int32_t)(cnt * (p + 1) / np);
+                const int32_t b0 = e0 + (int32_t)(unit * (cu * p / np));
+                const int32_t b1 = e0 + (int32_t)(unit * (cu * (p + 1) / np));
                 s.items.push_back({(int32_t)sr, b0, b1, base + (int32_t)p, base, (int32_t)np});
                 cost.push_back(((b1 - b0) + 4) * group);
                 s.max_item_entries = std::max<int32_t>(s.max_item_entries, b1 - b0);
@@ -321,6 +327,15 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
         msg = "too many work items";
         return BSP_ERR_UNSUPPORTED;
     }
+    // With C a multiple of 64 every item must start at an even 32-column
+    // step of its block: a kernel then fetches A for entries 2m and 2m+1 as
+    // one 64-column span, which for an odd start would reach past the row.
+    if (a->C % 64 == 0)
+        for (const SpmmItem& it : s.items)
+            if (it.e_end > it.e_begin && (s.ent_off[it.e_begin] % a->C) / kSub % 2 != 0) {
+                msg = "internal: work item starts at an odd 32-column step";
+                return BSP_ERR_UNSUPPORTED;
+            }
     // Column groups of the XCD map: the fewest (1, 2, 4, 8) that bring one
     // XCD's slice of B to at most 2 MiB, limited by the tile count.
     int64_t cg = 1;

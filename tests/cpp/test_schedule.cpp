@@ -143,6 +143,8 @@ void check_spmm(const Bsr& a, int64_t N, int cus, const std::string& name) {
         int64_t at = stripe_begin[gi];
         for (size_t k = 0; k < its.size(); ++k) {
             expect(its[k]->e_begin == at, name + ": items contiguous");
+            if (a.C % 64 == 0)
+                expect((its[k]->e_begin - stripe_begin[gi]) % 2 == 0, name + ": items start at an even entry (A pairs)");
             at = its[k]->e_end;
             covered += its[k]->e_end - its[k]->e_begin;
             if (its.size() > 1) {
@@ -385,6 +387,12 @@ int main() {
     check_spmm(skewed(16384, 16384, 32, 32, 5243, 5), 1024, cus, "spmm skewed, duplicates");
     check_spmm(uniform(8192, 8192, 256, 256, 256, 6), 8192, cus, "spmm 256x256 blocks (row groups)");
     check_spmm(uniform(2048, 1024, 64, 128, 60, 7), 256, cus, "spmm 64x128 blocks");
+    for (const char* lim : {"1", "3", "6"}) {
+        setenv("BSP_SPMM_SPLIT", lim, 1);
+        check_spmm(uniform(2048, 2048, 256, 256, 40, 8), 512, cus, std::string("spmm 256x256 split ") + lim);
+        check_spmm(uniform(2048, 1024, 64, 128, 60, 7), 256, cus, std::string("spmm 64x128 split ") + lim);
+        unsetenv("BSP_SPMM_SPLIT");
+    }
     check_spmm(skewed(1024, 2048, 128, 64, 40, 8), 96, cus, "spmm 128x64 blocks, skewed");
     check_spmm(uniform(1024, 1024, 32, 32, 0, 9), 256, cus, "spmm empty");
     check_spmm(banded(8192, 32, 8, 655, 19), 128, cus, "spmm banded 8192^2 (row bands)");
