@@ -329,18 +329,19 @@ __device__ __forceinline__ void run_ring(int n, Issue&& issue, Read&& read, Mult
 
 // The ring of run_ring (one operand set) with each entry's operands and
 // products in two halves (the two 16-deep k-steps).  Step k:
-//   1. half 0's products of entry k, interleaved one for one with the LDS
-//      reads of entry k's half 1 (into the registers half 1 released in the
-//      previous step);
+//   1. half 0's products of entry k, interleaved with the LDS reads of entry
+//      k's half 1 (into the registers half 1 released in the previous step);
 //   2. sync: the reads complete, entry k+1 landed, barrier (stage k % S is
 //      then free), entry k+S issued;
 //   3. half 1's products of entry k, interleaved with the reads of entry
 //      k+1's half 0.
-// Each wave thus issues an LDS read under every product, and no phase of a
-// step is reads alone: the two waves of a SIMD, in step with each other
-// through the barrier, would otherwise both read while the matrix core
-// idles, then both multiply.  PAIRS is the number of (product, read) pairs
-// per half.  An entry issues PER loads per wave, an even entry EXTRA more (a
+// The reads go two after each of the first PAIRS/2 products (PAIRS products
+// per half), so that the last of them lands before the next part's first
+// product needs it, and no phase of a step is reads alone: the two waves of
+// a SIMD, in step with each other through the barrier, would otherwise both
+// read while the matrix core idles, then both multiply.  (256x256 blocks:
+// reads before the products 281-290 us, one read per product 270-277, two
+// per product over the first half 265-273.)  An entry issues PER loads per wave, an even entry EXTRA more (a
 // load shared by an entry pair goes with its first entry).  read(k, stage,
 // o, h) reads half h of entry k (in stage `stage`).
 template <int S, int PER, int EXTRA, int PAIRS, class Ops, class Issue, class Read, class Multiply, class Landed>
@@ -364,10 +365,11 @@ __device__ __forceinline__ void run_ring_halves(int n, Issue&& issue, Read&& rea
     auto fence_sched = [] { __builtin_amdgcn_sched_barrier(0); };
     auto interleave = [] {
 #pragma unroll
-        for (int i = 0; i < PAIRS; ++i) {
+        for (int i = 0; i < PAIRS / 2; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // two LDS reads
         }
+        __builtin_amdgcn_sched_group_barrier(0x008, PAIRS - PAIRS / 2, 0);
     };
     auto step = [&](int k, bool full) {
         multiply(o, 0);
