@@ -21,7 +21,9 @@ overhead excluded).  Each launch is also timed individually with an event pair
 
 The CPU baseline is the oracle (the C restatement of the reference's golden,
 oracle/bsp_oracle.c) on this host: all cores on the whole 25% workload, and
-one core on a 32-block-row sample.
+one core on a 32-block-row sample.  Every other section carries a "cpu"
+record too: the oracle on the same workload (or a named sample of its block
+rows), its TFLOP/s and the GPU's speedup over it.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -330,6 +332,83 @@ def cpu_baseline(W, orc):
     }
 
 
+def cpu_per_config(W, orc, out, cores):
+    """The oracle on this host beside each GPU figure: all `cores` threads
+    (the SpGEMM golden is single-threaded), each workload whole or, where
+    that would take more than a few seconds, a named sample of its block
+    rows.  Adds a "cpu" record (TFLOP/s, seconds, sample, GPU speedup) to
+    each section of `out`."""
+    def rate(fn, flops):
+        t0 = time.perf_counter()
+        fn()
+        t = time.perf_counter() - t0
+        return flops / t / 1e12, t
+
+    def record(tf, t, sample, gpu_tflops, threads=cores):
+        return {"tflops": round(tf, 6), "cores": threads, "kind": "port", "seconds": round(t, 3),
+                "sample": sample, "gpu_speedup": round(gpu_tflops / tf, 1) if gpu_tflops else None}
+
+    if "sweep" in out:
+        for d in W.SPMM_SWEEP_DENSITIES:
+            rows = [r for r in out["sweep"] if r["density"] == d and not r.get("warm_cache")]
+            if not rows:
+                continue
+            w = W.workload_spmm_sweep(d)
+            a = w["a"]
+            tf, t = rate(lambda: orc.spmm(a.indptr, a.indices, a.data, a.H, a.W, 32, 32, w["b"], threads=cores),
+                         W.spmm_flops(a.nblocks, 32, 32, w["b"].shape[1]))
+            for r in rows:
+                r["cpu"] = record(tf, t, "whole workload", r["tflops"])
+    if "sddmm" in out:
+        s = W.workload_sddmm()
+        m = s["mask"]
+        tf, t = rate(lambda: orc.sddmm(m.indptr, m.indices, m.data, m.H, m.W, 32, 32, s["x"], s["y"],
+                                       threads=cores),
+                     W.sddmm_flops(m.nblocks, 32, 32, s["x"].shape[1]))
+        out["sddmm"]["cpu"] = record(tf, t, "whole workload", out["sddmm"]["tflops"])
+    if "skewed" in out:
+        w = W.workload_spmm_skewed()
+        a = w["a"]
+        tf, t = rate(lambda: orc.spmm(a.indptr, a.indices, a.data, a.H, a.W, 32, 32, w["b"], threads=cores),
+                     W.spmm_flops(a.nblocks, 32, 32, w["b"].shape[1]))
+        out["skewed"]["cpu"] = record(tf, t, "whole workload", out["skewed"]["tflops"])
+    if "attention" in out:
+        w = W.workload_attention()
+        m = w["mask"]
+        d = w["d"]
+
+        def pair():
+            orc.sddmm(m.indptr, m.indices, m.data, m.H, m.W, 32, 32, w["q"], w["k"], y_colmajor=True, threads=cores)
+            orc.spmm(m.indptr, m.indices, m.data, m.H, m.W, 32, 32, w["v"], threads=cores)
+        tf, t = rate(pair, W.sddmm_flops(m.nblocks, 32, 32, d) + W.spmm_flops(m.nblocks, 32, 32, d))
+        out["attention"]["cpu"] = record(tf, t, "whole pair (SDDMM then SpMM)", out["attention"]["fused"]["tflops"])
+    if "spgemm" in out:
+        w = W.workload_spgemm()
+        a, b = w["a"], w["b"]
+        rows = 32
+        nb = int(a.indptr[rows])
+        bcount = np.diff(b.indptr).astype(np.int64)
+        pairs = int(bcount[a.indices[:nb]].sum())
+        tf, t = rate(lambda: orc.spgemm(a.indptr[:rows + 1], a.indices[:nb], a.data[:nb * a.R * a.C], rows * a.R,
+                                        a.R, a.C, b.indptr, b.indices, b.data, b.W, b.C),
+                     2.0 * pairs * a.R * a.C * b.C)
+        gpu = next(r["tflops"] for r in out["spgemm"]["runs"] if r["out"] == "f32")
+        out["spgemm"]["cpu"] = record(tf, t, f"block rows 0..{rows - 1} of A ({nb} blocks, {pairs} block products)",
+                                      gpu, threads=1)
+    if "large_blocks" in out:
+        w = W.workload_spmm_large_blocks(0.25)
+        a = w["a"]
+        rows, ncols = min(a.nbrows, cores), 64  # one block row per thread
+        nb = int(a.indptr[rows])
+        bs = np.ascontiguousarray(w["b"][:, :ncols])
+        tf, t = rate(lambda: orc.spmm(a.indptr[:rows + 1], a.indices[:nb], a.data[:nb * a.R * a.C], rows * a.R, a.W,
+                                      a.R, a.C, bs, threads=cores),
+                     W.spmm_flops(nb, a.R, a.C, ncols))
+        gpu = next(r["tflops"] for r in out["large_blocks"]["runs"] if r["out"] == "f32")
+        out["large_blocks"]["cpu"] = record(
+            tf, t, f"block rows 0..{rows - 1} ({nb} of {a.nblocks} blocks) times the first {ncols} columns of B", gpu)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -455,7 +534,9 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(W, entry._load_oracle())
+        orc = entry._load_oracle()
+        cpu = cpu_baseline(W, orc)
+        cpu_per_config(W, orc, out, cpu["cores"])
 
     if head is None:
         print(json.dumps(out))
