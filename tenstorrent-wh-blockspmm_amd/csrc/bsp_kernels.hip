@@ -24,6 +24,7 @@ namespace bsp {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -46,6 +47,13 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
 
 __device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f32x16& c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// v_mfma_f32_16x16x32_bf16: lane l holds A[l%16][8*(l/16) .. +7] and
+// B[8*(l/16) .. +7][l%16]; result element v of lane l is D[4*(l/16) + v][l%16].
+__device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
@@ -236,9 +244,12 @@ namespace spmm_detail {
 // entry k+1's reads follow it.  landed() runs once entry 0 (and every load
 // issued before it) has landed and is visible to all waves.  With MIX (and
 // OVERLAP), entry k+1's reads and entry k's products form one scheduling
-// region, which multiply() orders itself (sched_group_barrier).
-template <int S, int PER, bool OVERLAP, class Ops, bool MIX = false, class Issue, class Read, class Multiply,
-          class Landed>
+// region.  With XCHG (and OVERLAP), read() may leave LDS data that the other
+// waves' multiply() of the same entry reads: a barrier then also follows
+// landed() (whose LDS reads complete first) and precedes a multiply() that no
+// ring step separates from its entry's read().
+template <int S, int PER, bool OVERLAP, class Ops, bool MIX = false, bool XCHG = false, class Issue, class Read,
+          class Multiply, class Landed>
 __device__ __forceinline__ void run_ring(int n, Issue&& issue, Read&& read, Multiply&& multiply,
                                          Landed&& landed) {
     static_assert(PER * (S - 2) < 64, "vmcnt budget");
@@ -250,6 +261,13 @@ __device__ __forceinline__ void run_ring(int n, Issue&& issue, Read&& read, Mult
     wait_stages<PER, S - 2>(n - 1);  // entry 0 landed
     barrier_no_fence();
     landed();
+    auto xchg = [] {
+        if constexpr (XCHG) {
+            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            barrier_no_fence();
+        }
+    };
+    xchg();
     if (S - 1 < n) issue(S - 1, S - 1);
     read(0, o0);
     int stage = 0;  // stage of entry k
@@ -314,8 +332,10 @@ __device__ __forceinline__ void run_ring(int n, Issue&& issue, Read&& read, Mult
             read(stage, o1);
             fence_rm();
             multiply(o0);
+            xchg();
             multiply(o1);
         } else {
+            xchg();
             multiply(o0);
         }
     } else {
@@ -859,13 +879,14 @@ __global__ __launch_bounds__(64 * NW, 1) void spmm_group_wide_kernel(SpmmArgs p)
 // Block-sparse attention pair, fused: O = S * V with S = bf16(mask (.) (Q*K^T))
 // at the mask's blocks, S never leaving the compute unit.  Same schedule and
 // ring as the SpMM (the mask plays A, V plays B, one 128-column tile); each
-// ring stage also carries the entry's 32 x DK block of K.  Every wave
-// computes the whole 32x32 S^T = K_blk * Q^T of its entry from LDS (Q^T of the
-// stripe stays in registers), applies the mask and rounds to bf16, and uses
-// the result directly as the A operand of O += S * V: the result holds, per
-// lane, keys 8i + 4q + j of one query row, so the B operand reads V's rows in
-// that order.  Numerically the same as bsp_sddmm (column-major Y = K, bf16
-// output) followed by bsp_spmm with the same structure.
+// ring stage also carries the entry's 32 x DK block of K.  Each wave computes
+// one 16 x 16 quadrant of the entry's S^T = K_blk * Q^T from LDS (its 16
+// queries of Q^T stay in registers), applies the mask, rounds to bf16 and
+// writes the quadrant to an S buffer in LDS; after the next ring barrier
+// every wave reads the whole 32 x 32 S from there as the A operand of
+// O += S * V.  Numerically the same as bsp_sddmm (column-major Y = K, bf16
+// output) followed by bsp_spmm with the same structure, up to the fp32
+// summation order of Q K^T.
 template <int DK, int S, bool OUT_BF16>
 __global__ __launch_bounds__(256) void attention_kernel(AttentionArgs pa) {
     using namespace spmm_detail;
@@ -879,7 +900,8 @@ __global__ __launch_bounds__(256) void attention_kernel(AttentionArgs pa) {
     constexpr int B_RING = K_RING + S * K_BYTES;
     constexpr int Q_AREA = B_RING + S * Slice::BYTES;
     static_assert(KI >= 1 && DK % 32 == 0 && DK <= 128, "head dimension");
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[Q_AREA + K_BYTES];
+    // The Q area holds Q, then (Q in registers) the two 2 KB S buffers.
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[Q_AREA + (K_BYTES > 4096 ? K_BYTES : 4096)];
 
     const SpmmWg it = load_const(p.wgs + blockIdx.x);
     if (it.row < 0) return;
@@ -889,7 +911,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttentionArgs pa) {
     const int l32 = lane & 31, q = lane >> 5;
     const uint32_t lds0 = lds_address(smem);
     const Slice bsl(wave, lane, 0, p.N, p.ldb);
-    const BReads<Slice::TN, 1> brd(lane, wave * 32, true);
+    const BReads<Slice::TN, 1> brd(lane, wave * 32, false);
 
     // K blocks and the stripe's Q rows in LDS as 16-byte chunks (c, row r) at
     // (32c + r) * 16, so that the operand of step s of row l32 (chunk 2s + q)
@@ -913,9 +935,14 @@ __global__ __launch_bounds__(256) void attention_kernel(AttentionArgs pa) {
         for (int j = 0; j < KI; ++j)
             if (lane < K_LANES) gl_lds16(qrow + q_goff[j], lds0 + Q_AREA + wave * DK * 16 + j * K_LANES * 16);
     }
-    // Q^T operands of the stripe: lane (query l32, half q) holds
-    // Q[row][16s + 8q .. +7] for every 16-deep step s of the head dimension.
-    u32x4 qv[DK / 16];
+    // S = mask (.) Q K^T of an entry is computed in four 16 x 16 quadrants,
+    // one per wave: wave w takes keys ka = 16*(w%2) .. +15 and queries
+    // qb = 16*(w/2) .. +15, S^T quadrant = K[ka..][:] * Q[qb..][:]^T in DK/32
+    // 16x16x32 products.  Lane l holds Q[qb + l%16][32t + 8*(l/16) .. +7]
+    // for each 32-deep step t (the B operand).
+    const int ka = 16 * (wave & 1), qb = 16 * (wave >> 1);
+    const int l16 = lane & 15, g4 = lane >> 4;
+    u32x4 qv[DK / 32];
     const uint32_t a_voff = 2 * ((8 * wave + (lane & 7)) * p.lda + 8 * ((lane & 31) >> 3));
     const uint32_t a_lds = lds0 + wave * 512;
     const uint32_t k_lds = lds0 + K_RING + wave * DK * 16;
@@ -932,58 +959,54 @@ __global__ __launch_bounds__(256) void attention_kernel(AttentionArgs pa) {
         bsl.issue(p.b, p.ldb, bw, b_lds + stage * Slice::BYTES);
     };
 
-    // Mask values of lane (query l32, half q): keys 8i + 4q .. +3 are 8 bytes
-    // of chunk i of the query's row.  The mask is loaded without the SpMM A
+    // The quadrant's mask values of lane l: query qb + l%16, keys ka + 4*(l/16)
+    // .. +3, 8 bytes of the mask's row.  The mask is loaded without the SpMM A
     // layout's chunk XOR: segment g, chunk j of row r at (8j + r%8) * 16.
-    const int m_rd = (l32 >> 3) * 512 + (l32 & 7) * 16 + 8 * q;  // + i * 128
+    const int mq = qb + l16, mkey = ka + 4 * g4;
+    const int m_rd = (mq >> 3) * 512 + (8 * (mkey >> 3) + (mq & 7)) * 16 + 2 * (mkey & 7);
+    // S of an entry in LDS (two buffers in the Q area, free once Q is in
+    // registers), bf16 row-major by query, 64 bytes a row, 16-byte chunk c of
+    // row r at position c ^ (r/4 % 4): each 16-lane quarter of the O
+    // operand read, and each half-wave of the quadrant write, covers every bank.
+    auto s_pos = [](int r, int key) { return r * 64 + 16 * ((key >> 3) ^ ((r >> 2) & 3)) + 2 * (key & 7); };
+    const int s_wr = s_pos(mq, mkey);
+    const int s_rd0 = s_pos(l32, 8 * q), s_rd1 = s_pos(l32, 16 + 8 * q);
     f32x16 acc[1];
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[0][v] = 0.0f;
 
-    // Operands of one entry: its raw S^T (products over the head dimension),
-    // its mask values, V's rows.  The mask product and the rounding to bf16
-    // happen in multiply(), in one scheduling region with the next entry's
-    // reads and S^T products (run_ring's MIX), so the compiler can place that
-    // VALU work among products that do not depend on it; with one wave per
-    // SIMD nothing else would overlap it.  (12.1-12.9 -> 11.6-12.4 us on the
-    // attention workload; forcing reads, conversion, products in that order
-    // measured slower, 12.7-13.1.)
+    // Operands of one entry kept in registers: V's rows (its S is in LDS).
     struct Operands {
-        f32x16 st;
-        uint32_t mk[8];
         u32x4 b[2][1];
     };
-    run_ring<S, PER, true, Operands, true>(
+    int e_read = 0, e_mul = 0;  // entries read / multiplied so far (S buffer = entry % 2)
+    run_ring<S, PER, true, Operands, true, true>(
         n, issue,
         [&](int stage, Operands& o) {
             const uint8_t* ks = smem + K_RING + stage * K_BYTES;
+            f32x4 sq = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int v = 0; v < 16; ++v) o.st[v] = 0.0f;
-#pragma unroll
-            for (int s2 = 0; s2 < DK / 16; ++s2)
-                o.st = mfma32(*(const u32x4*)(ks + (32 * (2 * s2 + q) + l32) * 16), qv[s2], o.st);
-            const uint8_t* ms = smem + stage * kA_BYTES;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint64_t w = *(const uint64_t*)(ms + m_rd + i * 128);
-                o.mk[2 * i] = (uint32_t)w;
-                o.mk[2 * i + 1] = (uint32_t)(w >> 32);
-            }
+            for (int t = 0; t < DK / 32; ++t)
+                sq = mfma16(*(const u32x4*)(ks + (32 * (4 * t + g4) + ka + l16) * 16), qv[t], sq);
+            const uint64_t mw = *(const uint64_t*)(smem + stage * kA_BYTES + m_rd);
+            const uint32_t m0 = (uint32_t)mw, m1 = (uint32_t)(mw >> 32);
+            // sq[v] = S^T[ka + 4*(l/16) + v][qb + l%16]: keys mkey + v of query mq.
+            const uint32_t lo = pack_bf16x2(sq[0] * __uint_as_float(m0 << 16), sq[1] * __uint_as_float(m0 & 0xffff0000u));
+            const uint32_t hi = pack_bf16x2(sq[2] * __uint_as_float(m1 << 16), sq[3] * __uint_as_float(m1 & 0xffff0000u));
+            *(uint64_t*)(smem + Q_AREA + (e_read & 1) * 2048 + s_wr) = (uint64_t)lo | ((uint64_t)hi << 32);
+            ++e_read;
             brd.read(smem + B_RING + stage * Slice::BYTES, o.b);
         },
         [&](const Operands& o) {
-            uint32_t sb[8];
-#pragma unroll
-            for (int t = 0; t < 8; ++t)
-                sb[t] = pack_bf16x2(o.st[2 * t] * __uint_as_float(o.mk[t] << 16),
-                                    o.st[2 * t + 1] * __uint_as_float(o.mk[t] & 0xffff0000u));
-            acc[0] = mfma32(u32x4{sb[0], sb[1], sb[2], sb[3]}, o.b[0][0], acc[0]);
-            acc[0] = mfma32(u32x4{sb[4], sb[5], sb[6], sb[7]}, o.b[1][0], acc[0]);
+            const uint8_t* sx = smem + Q_AREA + (e_mul & 1) * 2048;
+            ++e_mul;
+            acc[0] = mfma32(*(const u32x4*)(sx + s_rd0), o.b[0][0], acc[0]);
+            acc[0] = mfma32(*(const u32x4*)(sx + s_rd1), o.b[1][0], acc[0]);
         },
         [&] {
 #pragma unroll
-            for (int s2 = 0; s2 < DK / 16; ++s2)
-                qv[s2] = *(const u32x4*)(smem + Q_AREA + (32 * (2 * s2 + q) + l32) * 16);
+            for (int t = 0; t < DK / 32; ++t)
+                qv[t] = *(const u32x4*)(smem + Q_AREA + (32 * (4 * t + g4) + qb + l16) * 16);
         });
     spmm_finish<1, OUT_BF16>(p, it, acc, tid);
 }
