@@ -722,29 +722,30 @@ __global__ __launch_bounds__(256, 2) void spmm_group_kernel(SpmmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// SpMM over 8-stripe row groups (R = 256) with a 256-column tile: a
-// workgroup owns a 256 x 256 output tile, one workgroup per compute unit,
-// with a deep ring (S stages of 16 KB of A and 16 KB of B).  NW = 8 waves
-// (two per SIMD) in a 2 x 4 grid each hold 4 stripes x 2 32-column tiles
-// (128 accumulators per lane); NW = 4 waves (one per SIMD) in a 2 x 2 grid
-// hold 4 x 4 (256 accumulators, the whole register file shared with the
-// AGPRs), which halves the LDS bytes read per product but leaves no second
-// wave to hide a wave's waits behind: eight waves measure 6% faster.  Either
-// way one operand set per wave, read in halves under the other half's
-// products (run_ring_halves).  Ring, B slice and entry words are the
-// single-stripe kernel's; split pieces leave their partials in the
-// 256-column single-stripe layout (tile t's column l at the slot's
-// ((t % 2) * 16 + v) * 256 + (t / 2) * 64 + l), which spmm_reduce_kernel<2>
-// adds.
-template <int S, bool OUT_BF16, int NW, bool PAIR>
+// SpMM over RW-stripe row groups (RW = 4 or 8: R = 128 or 256) with a
+// 256-column tile: a workgroup owns a 32*RW x 256 output tile, one workgroup
+// per compute unit, with a deep ring (S stages of RW x 2 KB of A and 16 KB of
+// B).  NW = 8 waves (two per SIMD) in a 2 x 4 grid each hold RW/2 stripes x 2
+// 32-column tiles (128 accumulators per lane at RW = 8); NW = 4 waves (one
+// per SIMD) in a 2 x 2 grid hold RW/2 x 4 (256 accumulators at RW = 8, the
+// whole register file shared with the AGPRs), which reads fewer LDS bytes
+// per product but leaves no second wave to hide a wave's waits behind:
+// eight waves measure 6% faster.  Either way one operand set per wave, read
+// in halves under the other half's products (run_ring_halves).  Ring, B
+// slice and entry words are the single-stripe kernel's; split pieces leave
+// their partials in the 256-column single-stripe layout (tile t's column l
+// at the slot's ((t % 2) * 16 + v) * 256 + (t / 2) * 64 + l), which
+// spmm_reduce_kernel<2> adds.
+template <int RW, int S, bool OUT_BF16, int NW, bool PAIR>
 __global__ __launch_bounds__(64 * NW, 1) void spmm_group_wide_kernel(SpmmArgs p) {
     using namespace spmm_detail;
     static_assert(NW == 4 || NW == 8, "waves");
+    static_assert(RW == 4 || RW == 8, "row group");
     using Slice = BSlice<2, NW>;
-    constexpr int RW = 8, SR = 4;
+    constexpr int SR = RW / 2;   // stripes per wave
     constexpr int WC = NW / 2;   // wave grid 2 x WC
     constexpr int NT = 8 / WC;   // 32-column tiles per wave
-    constexpr int A_BYTES = RW * kA_BYTES;  // A of one entry (16 KB)
+    constexpr int A_BYTES = RW * kA_BYTES;  // A of one entry (RW sub-blocks)
     constexpr int AI = 4 * RW / NW / 2;     // per entry and wave: A load instructions of 1 KB
     constexpr int NP = S / 2 + 1;           // pair slots (the pairs of entries k .. k+S-1, and one being filled)
     constexpr int A_RING = PAIR ? NP * 2 * A_BYTES : S * A_BYTES;
@@ -770,10 +771,10 @@ __global__ __launch_bounds__(64 * NW, 1) void spmm_group_wide_kernel(SpmmArgs p)
     // covers segments 2*(w*AI + j) and 2*(w*AI + j) + 1.
     // A with pairs (C a multiple of 64: entries 2m and 2m+1 of an item are the
     // two 32-column halves of the same 64 columns of one block): an even
-    // entry fetches both, 256 rows of 128 bytes, so that every request is a
+    // entry fetches both, 32*RW rows of 128 bytes, so that every request is a
     // whole 128-byte line (a 64-byte half-line request costs the L1 as much
     // as a whole line, and the DMA-only loop measured 189 us against 138 us
-    // on 256x256 blocks).  Load I (0..31) holds rows 8I .. 8I+7 of the group,
+    // on 256x256 blocks).  Load I (0 .. 4*RW-1) holds rows 8I .. 8I+7 of the group,
     // row r of them at I*1024 + (r%8)*128 with its 16-byte chunk c at
     // position c ^ ((r%8)/2 + 4*(I%2)): each 16-lane quarter of a read then
     // covers every bank.  Pair m sits in slot m % NP.
@@ -1600,8 +1601,8 @@ static void launch_spmm_t(const SpmmArgs& a, bool out_bf16, int grid, int n_spli
             hipLaunchKernelGGL((spmm_kernel<NTW, S, true>), dim3(grid), dim3(256), 0, stream, a);
         else
             hipLaunchKernelGGL((spmm_kernel<NTW, S, false>), dim3(grid), dim3(256), 0, stream, a);
-    } else if constexpr (G == 8 && NTW == 2) {
-        // Eight waves (two per SIMD, 128 x 64 outputs each) unless BSP_SPMM_WIDE_WAVES=4;
+    } else if constexpr ((G == 4 || G == 8) && NTW == 2) {
+        // Eight waves (two per SIMD, 32*RW/2 x 64 outputs each) unless BSP_SPMM_WIDE_WAVES=4;
         // A fetched in entry pairs when C is a multiple of 64 (the plan then
         // starts every item at an even entry of its block).
         const char* ww = std::getenv("BSP_SPMM_WIDE_WAVES");
@@ -1610,10 +1611,10 @@ static void launch_spmm_t(const SpmmArgs& a, bool out_bf16, int grid, int n_spli
 #define BSP_WIDE(NW_, PAIR_)                                                                                  \
     do {                                                                                                      \
         if (out_bf16)                                                                                         \
-            hipLaunchKernelGGL((spmm_group_wide_kernel<S, true, NW_, PAIR_>), dim3(grid), dim3(64 * NW_), 0,  \
+            hipLaunchKernelGGL((spmm_group_wide_kernel<G, S, true, NW_, PAIR_>), dim3(grid), dim3(64 * NW_), 0, \
                                stream, a);                                                                    \
         else                                                                                                  \
-            hipLaunchKernelGGL((spmm_group_wide_kernel<S, false, NW_, PAIR_>), dim3(grid), dim3(64 * NW_), 0, \
+            hipLaunchKernelGGL((spmm_group_wide_kernel<G, S, false, NW_, PAIR_>), dim3(grid), dim3(64 * NW_), 0, \
                                stream, a);                                                                    \
     } while (0)
         if (four) {

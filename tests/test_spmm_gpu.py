@@ -310,29 +310,29 @@ def test_row_group_chosen_for_large_blocks():
     assert_parity(got[:rows], golden_spmm(sub, w["b"]), spmm_k_eff(sub), "8192^3 R=256 prefix")
 
 
-@pytest.mark.parametrize("C", [256, 128, 64, 32])
+@pytest.mark.parametrize("R,C", [(256, 256), (256, 128), (256, 64), (256, 32), (128, 128), (128, 64), (128, 32)])
 @pytest.mark.parametrize("waves", [4, 8])
 @pytest.mark.parametrize("split", [0, 3])
 @pytest.mark.parametrize("out_dtype", ["f32", "bf16"])
-def test_row_group_wide_tile(monkeypatch, C, waves, split, out_dtype):
-    """256 x C blocks on the 256-column tile (the wide 8-stripe group
-    kernel), forced on a small shape: C a multiple of 64 fetches A in entry
-    pairs (C = 64: one pair per block), C = 32 one entry at a time; with and
-    without split rows (whose pieces the reduce kernel adds in the
-    256-column layout, and which start at even entries), both outputs, held
-    to the oracle, and the same bits on a second run."""
-    monkeypatch.setenv("BSP_SPMM_GROUP", "8")
+def test_row_group_wide_tile(monkeypatch, R, C, waves, split, out_dtype):
+    """R x C blocks on the 256-column tile (the wide group kernel over
+    R/32 = 8 or 4 stripes), forced on a small shape: C a multiple of 64
+    fetches A in entry pairs (C = 64: one pair per block), C = 32 one entry
+    at a time; with and without split rows (whose pieces the reduce kernel
+    adds in the 256-column layout, and which start at even entries), both
+    outputs, held to the oracle, and the same bits on a second run."""
+    monkeypatch.setenv("BSP_SPMM_GROUP", str(R // 32))
     monkeypatch.setenv("BSP_SPMM_WIDE_GROUP", "2")
     monkeypatch.setenv("BSP_SPMM_SPLIT", str(split or 100000))
     monkeypatch.setenv("BSP_SPMM_WIDE_WAVES", str(waves))
-    w = W.spmm_workload(2048, 2048, 512, 256, C, 0.3 if C > 32 else 0.1, seed=90 + split + C)
+    w = W.spmm_workload(2048, 2048, 512, R, C, 0.3 if C > 32 else 0.1, seed=90 + split + C + R)
     plan = capi.SpmmPlan(bsr_of(w["a"]), 512, out_dtype)
     info = plan.info()
-    assert info["group"] == 8 and info["tile_n"] == 256
+    assert info["group"] == R // 32 and info["tile_n"] == 256
     assert (info["n_split_rows"] > 0) == bool(split)
     got = run_spmm(w["a"], w["b"], out_dtype, plan=plan)
     again = run_spmm(w["a"], w["b"], out_dtype, plan=plan)
     plan.close()
     assert_parity(got, golden_spmm(w["a"], w["b"]), spmm_k_eff(w["a"]),
-                  f"wide group C={C} waves={waves} split={split} {out_dtype}")
+                  f"wide group R={R} C={C} waves={waves} split={split} {out_dtype}")
     np.testing.assert_array_equal(got, again)
