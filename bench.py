@@ -512,6 +512,17 @@ def main():
         out["large_blocks"] = {"workload": "SpMM 8192^3, 256x256 blocks, 25% (256 blocks)",
                                "nnzb": w["a"].nblocks, "runs": rows}
         del w
+        # The same shape with the reference's other block sizes (R = C = 128
+        # and 64), fp32 C.
+        rows = []
+        for R in (128, 64):
+            w = W.workload_spmm_large_blocks(0.25, R=R)
+            t, fl, nb, info, _ = bench_spmm(torch, capi, W, w["a"], w["b"], "f32", max(10, steps // 10),
+                                            max(2, warmup // 10))
+            rows.append({"R": R, "C": R, "nnzb": w["a"].nblocks, "out": "f32", **summarize(t, fl, nb, steps),
+                         "group": info["group"], "tile_n": info["tile_n"], "grid": info["grid"]})
+            del w
+        out["block_sizes"] = {"workload": "SpMM 8192^3, R x R blocks, 25%, fp32 C", "runs": rows}
 
     if not only or "host" in only:
         # The blocking host-buffer entry point (the reference operator's shape):
