@@ -506,7 +506,7 @@ def main():
         rows = []
         for od in ("bf16", "f32"):
             t, fl, nb, info, _ = bench_spmm(torch, capi, W, w["a"], w["b"], od, max(10, steps // 10),
-                                            max(2, warmup // 10))
+                                            max(10, warmup // 2))
             rows.append({"out": od, **summarize(t, fl, nb, steps), "tile_n": info["tile_n"],
                          "grid": info["grid"]})
         out["large_blocks"] = {"workload": "SpMM 8192^3, 256x256 blocks, 25% (256 blocks)",
@@ -518,7 +518,7 @@ def main():
         for R in (128, 64):
             w = W.workload_spmm_large_blocks(0.25, R=R)
             t, fl, nb, info, _ = bench_spmm(torch, capi, W, w["a"], w["b"], "f32", max(10, steps // 10),
-                                            max(2, warmup // 10))
+                                            max(10, warmup // 2))
             rows.append({"R": R, "C": R, "nnzb": w["a"].nblocks, "out": "f32", **summarize(t, fl, nb, steps),
                          "group": info["group"], "tile_n": info["tile_n"], "grid": info["grid"]})
             del w
