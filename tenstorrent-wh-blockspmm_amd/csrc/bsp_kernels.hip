@@ -722,7 +722,7 @@ __global__ __launch_bounds__(256, 2) void spmm_group_kernel(SpmmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// SpMM over RW-stripe row groups (RW = 4 or 8: R = 128 or 256) with a
+// SpMM over RW-stripe row groups (RW = 2, 4 or 8: R = 64, 128 or 256) with a
 // 256-column tile: a workgroup owns a 32*RW x 256 output tile, one workgroup
 // per compute unit, with a deep ring (S stages of RW x 2 KB of A and 16 KB of
 // B).  NW = 8 waves (two per SIMD) in a 2 x 4 grid each hold RW/2 stripes x 2
@@ -740,17 +740,22 @@ template <int RW, int S, bool OUT_BF16, int NW, bool PAIR>
 __global__ __launch_bounds__(64 * NW, 1) void spmm_group_wide_kernel(SpmmArgs p) {
     using namespace spmm_detail;
     static_assert(NW == 4 || NW == 8, "waves");
-    static_assert(RW == 4 || RW == 8, "row group");
+    static_assert(RW == 2 || RW == 4 || RW == 8, "row group");
     using Slice = BSlice<2, NW>;
     constexpr int SR = RW / 2;   // stripes per wave
     constexpr int WC = NW / 2;   // wave grid 2 x WC
     constexpr int NT = 8 / WC;   // 32-column tiles per wave
     constexpr int A_BYTES = RW * kA_BYTES;  // A of one entry (RW sub-blocks)
-    constexpr int AI = 4 * RW / NW / 2;     // per entry and wave: A load instructions of 1 KB
+    constexpr int A_KB = A_BYTES / 1024;    // its 1 KB loads
+    // Without pairs and with fewer loads than waves (RW = 2, eight waves),
+    // each wave loads one 512-byte segment with lanes 0-31.
+    constexpr bool HALF = !PAIR && A_KB < NW;
     constexpr int NP = S / 2 + 1;           // pair slots (the pairs of entries k .. k+S-1, and one being filled)
     constexpr int A_RING = PAIR ? NP * 2 * A_BYTES : S * A_BYTES;
-    constexpr int AL = PAIR ? 2 * AI : AI;  // A loads per wave and issue (an even entry's, for a pair)
-    constexpr int PER = PAIR ? Slice::BI : AI + Slice::BI;
+    // A loads per wave and issue (an even entry's, for a pair).
+    constexpr int AL = PAIR ? 2 * A_KB / NW : (HALF ? 1 : A_KB / NW);
+    static_assert(AL >= 1 && (PAIR ? AL * NW == 2 * A_KB : (HALF ? NW == 4 * RW : AL * NW == A_KB)), "A loads");
+    constexpr int PER = PAIR ? Slice::BI : AL + Slice::BI;
     constexpr int EXTRA = PAIR ? AL : 0;
     constexpr int B_RING = A_RING;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[A_RING + S * Slice::BYTES];
@@ -766,9 +771,9 @@ __global__ __launch_bounds__(64 * NW, 1) void spmm_group_wide_kernel(SpmmArgs p)
     const Slice bsl(wave, lane, it.tile * Slice::TN, p.N, p.ldb);
     const BReads<Slice::TN, NT> brd(lane, wc * NT * 32, false);
 
-    // A without pairs: of one entry, 32 segments of 512 bytes (sub-block
+    // A without pairs: of one entry, 4*RW segments of 512 bytes (sub-block
     // L/4, rows 8*(L%4) .. +7); segment L lands at L*512, and wave w's load j
-    // covers segments 2*(w*AI + j) and 2*(w*AI + j) + 1.
+    // covers segments 2*(w*AL + j) and 2*(w*AL + j) + 1 (HALF: segment w).
     // A with pairs (C a multiple of 64: entries 2m and 2m+1 of an item are the
     // two 32-column halves of the same 64 columns of one block): an even
     // entry fetches both, 32*RW rows of 128 bytes, so that every request is a
@@ -786,11 +791,11 @@ __global__ __launch_bounds__(64 * NW, 1) void spmm_group_wide_kernel(SpmmArgs p)
             const int c = (lane & 7) ^ ((r >> 1) | ((I & 1) << 2));
             a_voff[j] = 2 * ((8 * I + r) * p.lda + 8 * c);
         } else {
-            const int L = 2 * (wave * AI + j) + (lane >> 5);
+            const int L = HALF ? wave : 2 * (wave * AL + j) + (lane >> 5);
             a_voff[j] = 2 * ((L >> 2) * 32 * p.lda + a_load_offset(L & 3, lane, p.lda));
         }
     }
-    const uint32_t a_lds = lds0 + wave * AL * 1024;
+    const uint32_t a_lds = lds0 + wave * (HALF ? 512 : AL * 1024);
     const uint32_t b_lds = lds0 + B_RING + wave * Slice::BI * 1024;
     EntryWords words(p.ents + it.e_begin, it.e_end - it.e_begin, lane);
     auto issue = [&](int e, int stage) {
@@ -805,7 +810,8 @@ __global__ __launch_bounds__(64 * NW, 1) void spmm_group_wide_kernel(SpmmArgs p)
             }
         } else {
 #pragma unroll
-            for (int j = 0; j < AL; ++j) gl_lds16_s(a_voff[j], ablk, a_lds + stage * A_BYTES + j * 1024);
+            for (int j = 0; j < AL; ++j)
+                if (!HALF || lane < 32) gl_lds16_s(a_voff[j], ablk, a_lds + stage * A_BYTES + j * 1024);
         }
         bsl.issue(p.b, p.ldb, bw, b_lds + stage * Slice::BYTES);
     };
@@ -1601,7 +1607,7 @@ static void launch_spmm_t(const SpmmArgs& a, bool out_bf16, int grid, int n_spli
             hipLaunchKernelGGL((spmm_kernel<NTW, S, true>), dim3(grid), dim3(256), 0, stream, a);
         else
             hipLaunchKernelGGL((spmm_kernel<NTW, S, false>), dim3(grid), dim3(256), 0, stream, a);
-    } else if constexpr ((G == 4 || G == 8) && NTW == 2) {
+    } else if constexpr (NTW == 2) {
         // Eight waves (two per SIMD, 32*RW/2 x 64 outputs each) unless BSP_SPMM_WIDE_WAVES=4;
         // A fetched in entry pairs when C is a multiple of 64 (the plan then
         // starts every item at an even entry of its block).

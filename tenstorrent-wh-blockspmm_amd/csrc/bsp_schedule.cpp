@@ -233,14 +233,14 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
     if (group != 1 && group != 2 && group != 4 && group != 8) group = 1;
     if (RS % group != 0) group = 1;
     s.group = group;
-    // Row groups take 128-column tiles; 4- and 8-stripe groups take 256 (the
-    // wide group kernel, one workgroup per compute unit) when N is a multiple
-    // of 256 and the groups' tiles still fill every compute unit.
+    // Row groups take 256-column tiles (the wide group kernel, one workgroup
+    // per compute unit) when N is a multiple of 256 and the groups' tiles
+    // still fill every compute unit, else 128-column tiles.
     // (BSP_SPMM_WIDE_GROUP: 0 never, 2 whenever N allows it.)
     if (group > 1) {
         const int64_t wide_tiles = N % 256 == 0 ? (nsr / group) * (N / 256) : 0;
         const int64_t wide = env_int("BSP_SPMM_WIDE_GROUP", 1);
-        force_tile_n = (group >= 4 && wide_tiles > 0 && (wide == 2 || (wide == 1 && wide_tiles >= num_cus))) ? 256 : 128;
+        force_tile_n = (wide_tiles > 0 && (wide == 2 || (wide == 1 && wide_tiles >= num_cus))) ? 256 : 128;
     }
 
     // Workgroup width: 128 columns (four waves of 32); 256 (four waves of 64)

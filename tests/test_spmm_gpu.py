@@ -310,17 +310,19 @@ def test_row_group_chosen_for_large_blocks():
     assert_parity(got[:rows], golden_spmm(sub, w["b"]), spmm_k_eff(sub), "8192^3 R=256 prefix")
 
 
-@pytest.mark.parametrize("R,C", [(256, 256), (256, 128), (256, 64), (256, 32), (128, 128), (128, 64), (128, 32)])
+@pytest.mark.parametrize("R,C", [(256, 256), (256, 128), (256, 64), (256, 32), (128, 128), (128, 64), (128, 32),
+                                 (64, 64), (64, 32)])
 @pytest.mark.parametrize("waves", [4, 8])
 @pytest.mark.parametrize("split", [0, 3])
 @pytest.mark.parametrize("out_dtype", ["f32", "bf16"])
 def test_row_group_wide_tile(monkeypatch, R, C, waves, split, out_dtype):
     """R x C blocks on the 256-column tile (the wide group kernel over
-    R/32 = 8 or 4 stripes), forced on a small shape: C a multiple of 64
+    R/32 = 8, 4 or 2 stripes), forced on a small shape: C a multiple of 64
     fetches A in entry pairs (C = 64: one pair per block), C = 32 one entry
-    at a time; with and without split rows (whose pieces the reduce kernel
-    adds in the 256-column layout, and which start at even entries), both
-    outputs, held to the oracle, and the same bits on a second run."""
+    at a time (R = 64: 512 bytes per wave with eight waves); with and
+    without split rows (whose pieces the reduce kernel adds in the
+    256-column layout, and which start at even entries), both outputs, held
+    to the oracle, and the same bits on a second run."""
     monkeypatch.setenv("BSP_SPMM_GROUP", str(R // 32))
     monkeypatch.setenv("BSP_SPMM_WIDE_GROUP", "2")
     monkeypatch.setenv("BSP_SPMM_SPLIT", str(split or 100000))
