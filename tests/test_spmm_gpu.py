@@ -293,21 +293,24 @@ def test_row_group_split_rows(monkeypatch, group, split):
     plan.close()
 
 
-def test_row_group_chosen_for_large_blocks():
-    """The reference's published shape (8192^3, 256 x 256 blocks, 25%) runs
-    in groups of 8 stripes without any override; checked on its first 1024
-    rows (a block-row prefix) against the oracle."""
-    w = W.workload_spmm_large_blocks(0.25)
+@pytest.mark.parametrize("R", [256, 128, 64])
+def test_row_group_chosen_for_large_blocks(R):
+    """The reference's published shape (8192^3 at 25%) with R x R blocks runs
+    in groups of R/32 stripes on 256-column tiles without any override;
+    checked on a block-row prefix against the oracle (bf16 C for 256, fp32
+    for the others)."""
+    w = W.workload_spmm_large_blocks(0.25, R=R)
     a = w["a"]
-    plan = capi.SpmmPlan(bsr_of(a), 8192, "bf16")
-    assert plan.info()["group"] == 8
-    got = run_spmm(a, w["b"], "bf16", plan=plan)
+    od = "bf16" if R == 256 else "f32"
+    plan = capi.SpmmPlan(bsr_of(a), 8192, od)
+    assert plan.info()["group"] == R // 32 and plan.info()["tile_n"] == 256
+    got = run_spmm(a, w["b"], od, plan=plan)
     plan.close()
-    rows = 1024
-    nb = int(a.indptr[rows // 256])
-    sub = W.BsrArrays(rows, a.W, 256, 256, np.ascontiguousarray(a.indptr[:rows // 256 + 1]),
-                      a.indices[:nb], a.data[:nb * 65536])
-    assert_parity(got[:rows], golden_spmm(sub, w["b"]), spmm_k_eff(sub), "8192^3 R=256 prefix")
+    rows = 1024 if R == 256 else 512
+    nb = int(a.indptr[rows // R])
+    sub = W.BsrArrays(rows, a.W, R, R, np.ascontiguousarray(a.indptr[:rows // R + 1]),
+                      a.indices[:nb], a.data[:nb * R * R])
+    assert_parity(got[:rows], golden_spmm(sub, w["b"]), spmm_k_eff(sub), f"8192^3 R={R} prefix")
 
 
 @pytest.mark.parametrize("R,C", [(256, 256), (256, 128), (256, 64), (256, 32), (128, 128), (128, 64), (128, 32),
