@@ -778,11 +778,11 @@ __global__ __launch_bounds__(64 * NW, 1) void spmm_group_wide_kernel(SpmmArgs p)
     // two 32-column halves of the same 64 columns of one block): an even
     // entry fetches both, 32*RW rows of 128 bytes, so that every request is a
     // whole 128-byte line (a 64-byte half-line request costs the L1 as much
-    // as a whole line, and the DMA-only loop measured 189 us against 138 us
-    // on 256x256 blocks).  Load I (0 .. 4*RW-1) holds rows 8I .. 8I+7 of the group,
-    // row r of them at I*1024 + (r%8)*128 with its 16-byte chunk c at
-    // position c ^ ((r%8)/2 + 4*(I%2)): each 16-lane quarter of a read then
-    // covers every bank.  Pair m sits in slot m % NP.
+    // as a whole line: a DMA-only copy of the loop on 256x256 blocks took
+    // 189 us without pairs, 161 us with).  Load I (0 .. 4*RW-1) holds rows
+    // 8I .. 8I+7 of the group, row r of them at I*1024 + (r%8)*128 with its
+    // 16-byte chunk c at position c ^ ((r%8)/2 + 4*(I%2)): each 16-lane
+    // quarter of a read then covers every bank.  Pair m sits in slot m % NP.
     uint32_t a_voff[AL];
 #pragma unroll
     for (int j = 0; j < AL; ++j) {
