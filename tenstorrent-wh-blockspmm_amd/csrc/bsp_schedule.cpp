@@ -262,16 +262,21 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
     s.n_tiles = (int32_t)((N + tn - 1) / tn);
 
     // Split limit: a piece holds at most L entries.  L is the larger of twice
-    // the mean length of non-empty rows (uniform rows stay whole) and half of
-    // one compute unit's fair share of the total (skewed rows are cut so no
-    // workgroup dwarfs the rest), and at least 32.
+    // the mean length of non-empty rows (uniform rows stay whole) and one
+    // compute unit's fair share of the total (a longer row would alone
+    // outlast the rest), and at least 32.  A split row costs a partial round
+    // trip and a second launch, which a row shorter than the fair share does
+    // not repay: the skewed 16384^2 Zipf(1.2) workload (rows of at most 101
+    // entries, fair share 164) ran 8-11% faster with its rows whole than
+    // with its 12 longest halved at half the fair share (two boxes:
+    // 42.2-43.4 -> 37.7-38.2 us, 44.4-44.9 -> 40.8-41.4 us).
     // (In units of group entries: one entry of a group serves `group` stripes.)
     const int64_t gtotal = total / group;
     int64_t nonempty = 0;
     for (int64_t i = 0; i < nbr; ++i) nonempty += (a->indptr[i + 1] > a->indptr[i]) ? RS / group : 0;
     const int64_t mean = nonempty ? (gtotal + nonempty - 1) / nonempty : 0;
     const int64_t fair = (gtotal * s.n_tiles + num_cus - 1) / num_cus;
-    int64_t L = std::max<int64_t>({32, 2 * mean, (fair + 1) / 2});
+    int64_t L = std::max<int64_t>({32, 2 * mean, fair});
     L = env_int("BSP_SPMM_SPLIT", L);
     if (L < 1) L = 1;
     if (a->C % 64 == 0 && L < 2) L = 2;  // pieces hold whole entry pairs (below)

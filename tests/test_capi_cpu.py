@@ -214,8 +214,11 @@ def test_spmm_schedule_uniform(num_cus):
 
 
 def test_spmm_schedule_skewed_splits_long_rows():
+    """Rows longer than one compute unit's fair share are cut: the skewed
+    structure planned for 1024 compute units (fair share 41 entries, its
+    longest rows 101)."""
     s = W.workload_spmm_skewed()["a"]
-    sch = _check_spmm_schedule(s, 1024, 256)
+    sch = _check_spmm_schedule(s, 1024, 1024)
     info = sch["info"]
     counts = np.diff(s.indptr)
     assert info["n_split_rows"] > 0

@@ -126,16 +126,23 @@ def test_many_empty_rows_R256():
 
 
 # --- skewed rows: exercises split rows and the last-arriver fixup
-def test_skewed_workload_full_size():
+@pytest.mark.parametrize("split", [None, 40])
+def test_skewed_workload_full_size(monkeypatch, split):
+    """The skewed workload as planned (its rows fit one compute unit's share,
+    so they stay whole) and with the rows over 40 entries cut into pieces
+    (the reduce kernel adds them): held to the oracle, and the same bits on a
+    second run."""
+    if split:
+        monkeypatch.setenv("BSP_SPMM_SPLIT", str(split))
     w = W.workload_spmm_skewed()
     a = w["a"]
     plan = capi.SpmmPlan(capi.Bsr(a.H, a.W, 32, 32, a.indptr, a.indices), w["N"], "f32")
     info = plan.info()
-    assert info["n_split_rows"] > 0
+    assert (info["n_split_rows"] > 0) == bool(split)
     got1 = run_spmm(a, w["b"], "f32", plan=plan)
     got2 = run_spmm(a, w["b"], "f32", plan=plan)
     np.testing.assert_array_equal(got1, got2)  # counters reset, summation order fixed
-    assert_parity(got1, golden_spmm(a, w["b"]), spmm_k_eff(a), "skewed")
+    assert_parity(got1, golden_spmm(a, w["b"]), spmm_k_eff(a), f"skewed split={split}")
     plan.close()
 
 
