@@ -38,6 +38,10 @@ def test_fused_attention_full_size():
     gold, s_arr = golden_attention(mask, q, k, v)
     got = run_attention(mask, q, k, v, "f32")
     assert_parity(got, gold, spmm_k_eff(s_arr), "fused O = bf16(mask (.) QK^T) V")
+    # The S quadrants meet in LDS behind the ring's barriers: the same bits on
+    # every run.
+    for _ in range(3):
+        np.testing.assert_array_equal(run_attention(mask, q, k, v, "f32"), got)
     # Against the unfused GPU pipeline: the same S up to the bf16 rounding of
     # its fp32 sums, O up to fp32 summation order.
     s_vals = run_sddmm(mask, q, k, "bf16", y_layout=capi.COL_MAJOR)
