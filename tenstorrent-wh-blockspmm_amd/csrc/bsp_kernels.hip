@@ -724,8 +724,8 @@ __global__ __launch_bounds__(256, 2) void spmm_group_kernel(SpmmArgs p) {
 // ---------------------------------------------------------------------------
 // SpMM over RW-stripe row groups (RW = 2, 4 or 8: R = 64, 128 or 256) with a
 // 256-column tile: a workgroup owns a 32*RW x 256 output tile, one workgroup
-// per compute unit (two for RW = 2, on a 3-stage ring), with a deep ring (S
-// stages of RW x 2 KB of A and 16 KB of B).  NW = 8 waves (two per SIMD) in a 2 x 4 grid each hold RW/2 stripes x 2
+// per compute unit (two for RW = 2 and 4, on a 3-stage ring: 64 and 80 KB
+// of LDS), with a deep ring (S stages of RW x 2 KB of A and 16 KB of B).  NW = 8 waves (two per SIMD) in a 2 x 4 grid each hold RW/2 stripes x 2
 // 32-column tiles (128 accumulators per lane at RW = 8); NW = 4 waves (one
 // per SIMD) in a 2 x 2 grid hold RW/2 x 4 (256 accumulators at RW = 8, the
 // whole register file shared with the AGPRs), which reads fewer LDS bytes
@@ -737,7 +737,7 @@ __global__ __launch_bounds__(256, 2) void spmm_group_kernel(SpmmArgs p) {
 // at the slot's ((t % 2) * 16 + v) * 256 + (t / 2) * 64 + l), which
 // spmm_reduce_kernel<2> adds.
 template <int RW, int S, bool OUT_BF16, int NW, bool PAIR>
-__global__ __launch_bounds__(64 * NW, RW == 2 ? 2 : 1) void spmm_group_wide_kernel(SpmmArgs p) {
+__global__ __launch_bounds__(64 * NW, RW <= 4 && S == 3 ? 2 : 1) void spmm_group_wide_kernel(SpmmArgs p) {
     using namespace spmm_detail;
     static_assert(NW == 4 || NW == 8, "waves");
     static_assert(RW == 2 || RW == 4 || RW == 8, "row group");

@@ -88,7 +88,7 @@ inline int64_t spmm_partial_floats(int tile_n) { return (int64_t)tile_n * 32; }
     X(256, 3, 2)             \
     X(128, 4, 4)             \
     X(128, 5, 4)             \
-    X(256, 4, 4)             \
+    X(256, 3, 4)             \
     X(128, 3, 8)             \
     X(128, 4, 8)             \
     X(256, 3, 8)             \
@@ -112,7 +112,7 @@ inline bool spmm_variant_supported(const SpmmVariant& v) {
 inline SpmmVariant spmm_default_variant(int tile_n, int group) {
     switch (group) {
         case 2: return tile_n >= 256 ? SpmmVariant{256, 3, 2} : SpmmVariant{128, 6, 2};
-        case 4: return tile_n >= 256 ? SpmmVariant{256, 4, 4} : SpmmVariant{128, 4, 4};
+        case 4: return tile_n >= 256 ? SpmmVariant{256, 3, 4} : SpmmVariant{128, 4, 4};
         case 8: return tile_n >= 256 ? SpmmVariant{256, 4, 8} : SpmmVariant{128, 3, 8};
         default: return tile_n >= 256 ? SpmmVariant{256, 4, 1} : SpmmVariant{128, 6, 1};
     }
