@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define BSP_ABI_VERSION 3
+#define BSP_ABI_VERSION 4
 
 typedef enum bsp_status {
     BSP_OK = 0,
@@ -106,8 +106,12 @@ typedef struct bsp_plan_info {
                             flight + 1); SDDMM: 1 = one-shot kernel, 0 = looped */
     int32_t group;       /* SpMM: 32-row stripes of one block row per workgroup
                             (1; or 2, 4, 8 for blocks of R >= 64) */
-    int32_t reserved;
+    int32_t waves;       /* SpMM: waves per workgroup (fixed at plan creation) */
     int64_t workspace_bytes; /* device scratch owned by the plan */
+    int32_t persistent;  /* SpMM: 1 = persistent kernel (each workgroup streams
+                            a list of stripe x tile units; n_items counts the
+                            units, stages is the B ring depth) */
+    int32_t a_stages;    /* SpMM persistent: depth of the A ring */
 } bsp_plan_info;
 
 /* ---- library ------------------------------------------------------------- */

@@ -2,6 +2,7 @@
 // points.  See include/bsparse.h for the contract of each function.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -31,6 +32,11 @@ struct bsp_plan {
     bsp::SpgemmRun* d_runs = nullptr;  // wave runs
     int32_t wg_per_xcd = 0;
     int32_t sddmm_one_shot = 0;  // SDDMM: the one-shot kernel runs this plan
+    // SpMM persistent kernel: variant, unit records and A words (the B words
+    // go in d_ent_off, the workgroup records in d_wgs).
+    bsp::SpmmStreamVariant stream_variant{};
+    bsp::SpmmStreamUnit* d_units = nullptr;
+    uint32_t* d_aw = nullptr;
 };
 
 namespace {
@@ -77,6 +83,10 @@ void free_plan_buffers(bsp_plan* p) {
     if (p->d_ws) (void)hipFree(p->d_ws);
     if (p->d_terms) (void)hipFree(p->d_terms);
     if (p->d_runs) (void)hipFree(p->d_runs);
+    if (p->d_units) (void)hipFree(p->d_units);
+    if (p->d_aw) (void)hipFree(p->d_aw);
+    p->d_units = nullptr;
+    p->d_aw = nullptr;
     p->d_terms = nullptr;
     p->d_runs = nullptr;
     p->d_wgs = nullptr;
@@ -129,6 +139,14 @@ void fill_info_spmm(const bsp::SpmmSchedule& s, bsp_plan_info* info) {
     }
     info->stages = v.stages;
     info->group = s.group;
+    // Row groups on 256-column tiles run eight waves (two per SIMD) unless
+    // BSP_SPMM_WIDE_WAVES=4 asks for four; read here, once, so that a plan
+    // launches the same kernel every time (a captured graph included).
+    info->waves = 4;
+    if (s.group > 1 && s.tile_n == 256) {
+        const char* ww = std::getenv("BSP_SPMM_WIDE_WAVES");
+        info->waves = (ww && std::atoi(ww) == 4) ? 4 : 8;
+    }
     info->workspace_bytes =
         (int64_t)s.n_slots * s.n_tiles * bsp::spmm_partial_floats(s.tile_n) * (int64_t)sizeof(float);
 }
@@ -213,6 +231,94 @@ int bsp_sddmm_schedule(const bsp_bsr_desc* m, int64_t K, int num_cus, bsp_plan_i
 
 namespace {
 
+int64_t env_int(const char* name, int64_t dflt) {
+    const char* v = std::getenv(name);
+    if (!v || !*v) return dflt;
+    char* end = nullptr;
+    long long x = std::strtoll(v, &end, 10);
+    return (end && *end == 0) ? (int64_t)x : dflt;
+}
+
+// Whether an SpMM plan runs the persistent kernel, and which variant.  It
+// takes blocks whose stripes do not form row groups (row groups share each B
+// panel among the stripes of a block row, which the per-item group kernels
+// exploit) and N a multiple of 128.  BSP_SPMM_STREAM=0 turns it off;
+// BSP_SPMM_STREAM_VARIANT="tile,sb,sa,nbw" picks another compiled variant and
+// BSP_SPMM_STREAM_WPC the workgroups per compute unit (all read here, at plan
+// creation).
+bool choose_spmm_stream(const bsp_bsr_desc* a, int64_t N, int cus, bsp::SpmmStreamVariant* sv, int* wpc) {
+    if (env_int("BSP_SPMM_STREAM", 1) == 0) return false;
+    if (N % 128 != 0) return false;
+    const int64_t group = env_int("BSP_SPMM_GROUP", bsp::spmm_choose_group(a->R, a->H, N, cus));
+    if (group > 1 && (a->R / bsp::kSub) % group == 0) return false;
+    bsp::SpmmStreamVariant v{128, 6, 12, 2};
+    if (const char* e = std::getenv("BSP_SPMM_STREAM_VARIANT")) {
+        bsp::SpmmStreamVariant w{};
+        if (std::sscanf(e, "%d,%d,%d,%d", &w.tile_n, &w.sb, &w.sa, &w.nbw) == 4 &&
+            bsp::spmm_stream_variant_supported(w))
+            v = w;
+    }
+    if (N % v.tile_n != 0) v = bsp::SpmmStreamVariant{128, 6, 12, 2};
+    const int lds = bsp::spmm_stream_lds_bytes(v);
+    int w = std::max(1, std::min(2, bsp::kLdsBytesPerCu / lds));
+    w = (int)env_int("BSP_SPMM_STREAM_WPC", w);
+    if (w < 1 || w * lds > bsp::kLdsBytesPerCu) w = 1;
+    *sv = v;
+    *wpc = w;
+    return true;
+}
+
+// Plan of the persistent SpMM kernel: per-workgroup unit lists and entry
+// streams, uploaded once.
+int make_spmm_stream_plan(bsp_plan** out, const bsp_bsr_desc* a, int64_t N, int out_dtype, int device, int cus,
+                          const bsp::SpmmStreamVariant& sv, int wpc) {
+    std::string msg;
+    bsp::SpmmStream ss;
+    const int cg = (int)env_int("BSP_SPMM_XCD_COLS", 0);
+    int st = bsp::build_spmm_stream(a, N, cus, sv.tile_n, wpc, ss, msg, cg);
+    if (st != BSP_OK) return fail(st, msg);
+    DeviceGuard g(device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    bsp_plan* p = new bsp_plan();
+    p->kind = 1;
+    p->device = device;
+    p->out_dtype = out_dtype;
+    p->layout = BSP_ROW_MAJOR;
+    p->M = a->H;
+    p->K = a->W;
+    p->N = N;
+    p->R = a->R;
+    p->C = a->C;
+    p->nblocks = a->nblocks;
+    p->stream_variant = sv;
+    bsp_plan_info& in = p->info;
+    std::memset(&in, 0, sizeof(in));
+    in.kind = 1;
+    in.tile_n = ss.tile_n;
+    in.n_tiles = ss.n_tiles;
+    in.n_items = (int32_t)(ss.units.size() - bsp::kStreamPad);
+    in.n_entries = (int32_t)ss.n_entries;
+    in.grid = (int32_t)ss.wgs.size();
+    in.max_item_entries = ss.max_wg_entries;
+    in.stages = sv.sb;
+    in.group = 1;
+    in.waves = 5 + sv.nbw;
+    in.persistent = 1;
+    in.a_stages = sv.sa;
+    hipError_t e = upload((bsp::SpmmStreamWg**)&p->d_wgs, ss.wgs);
+    if (e == hipSuccess) e = upload(&p->d_units, ss.units);
+    if (e == hipSuccess) e = upload(&p->d_ent_off, ss.bw);
+    if (e == hipSuccess) e = upload(&p->d_aw, ss.aw);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        free_plan_buffers(p);
+        delete p;
+        return hip_fail(e, "SpMM plan upload");
+    }
+    *out = p;
+    return BSP_OK;
+}
+
 // Plan of an SpMM-shaped launch (SpMM, or the fused attention pair with the
 // mask as A and N = head dimension): schedule, upload, split-row scratch.
 int make_spmm_plan(bsp_plan** out, int kind, const bsp_bsr_desc* a, int64_t N, int out_dtype, int device,
@@ -225,6 +331,11 @@ int make_spmm_plan(bsp_plan** out, int kind, const bsp_bsr_desc* a, int64_t N, i
     int cus = 256;
     st = device_cus(device, &cus);
     if (st != BSP_OK) return st;
+    if (kind == 1) {
+        bsp::SpmmStreamVariant sv{};
+        int wpc = 1;
+        if (choose_spmm_stream(a, N, cus, &sv, &wpc)) return make_spmm_stream_plan(out, a, N, out_dtype, device, cus, sv, wpc);
+    }
     bsp::SpmmSchedule s;
     st = bsp::build_spmm_schedule(a, N, cus, s, msg, force_tile_n, kind == 3 ? 1 : 0);
     if (st != BSP_OK) return fail(st, msg);
@@ -315,9 +426,27 @@ int bsp_spmm(const bsp_plan* p, const uint16_t* a_vals, const uint16_t* b, int64
     DeviceGuard g(p->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     const bsp::SpmmArgs args = spmm_args(p, a_vals, b, ldb, c, ldc);
-    const bsp::SpmmVariant v{p->info.tile_n, p->info.stages, p->info.group};
-    hipError_t e = bsp::launch_spmm(args, v, p->out_dtype == BSP_DTYPE_BF16, p->info.grid, p->info.n_split_rows,
+    hipError_t e;
+    if (p->info.persistent) {
+        bsp::SpmmStreamArgs sa{};
+        sa.a = a_vals;
+        sa.b = b;
+        sa.c = c;
+        sa.wgs = (const bsp::SpmmStreamWg*)p->d_wgs;
+        sa.units = p->d_units;
+        sa.bw = p->d_ent_off;
+        sa.aw = p->d_aw;
+        sa.ldb = ldb;
+        sa.ldc = ldc;
+        sa.lda = (int32_t)p->C;
+        sa.N = (int32_t)p->N;
+        e = bsp::launch_spmm_stream(sa, p->stream_variant, p->out_dtype == BSP_DTYPE_BF16, p->info.grid,
                                     (hipStream_t)stream);
+    } else {
+        const bsp::SpmmVariant v{p->info.tile_n, p->info.stages, p->info.group, p->info.waves};
+        e = bsp::launch_spmm(args, v, p->out_dtype == BSP_DTYPE_BF16, p->info.grid, p->info.n_split_rows,
+                             (hipStream_t)stream);
+    }
     if (e != hipSuccess) return hip_fail(e, "SpMM launch");
     return BSP_OK;
 }

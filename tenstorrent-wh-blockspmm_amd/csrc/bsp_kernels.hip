@@ -192,12 +192,24 @@ __device__ __forceinline__ u32x4 ld_tr_b16(const uint8_t* lds) {
 
 }  // namespace spmm_detail
 
-// Output stores are non-temporal: the output is written once and not read by
-// the kernel, so it should not displace the operands from the caches
-// (measured on the 1% SpMM sweep case: 5.5 -> 4.3 us per launch).
+// Output stores write through the L2 (agent scope: a relaxed atomic store at
+// agent scope is a global store with sc1 on gfx950).  The output is written
+// once and never read by the kernel; written through, it streams out while
+// the kernel runs instead of being written back from every XCD's L2 at the
+// kernel's end.  8 MB of fp32 tiles from 512 workgroups, per launch in a
+// graph: plain or non-temporal stores 2.98 us, write-through 2.40 us (32 MB:
+// 7.0-7.2 -> 5.7 us).
 template <typename T>
 __device__ __forceinline__ void store_out(T* p, T v) {
-    __builtin_nontemporal_store(v, p);
+    if constexpr (sizeof(T) <= 8) {
+        __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        static_assert(sizeof(T) == 16, "16-byte or scalar stores");
+        const uint64_t* w = (const uint64_t*)&v;
+        uint64_t* d = (uint64_t*)p;
+        __hip_atomic_store(d, w[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(d + 1, w[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // Stores one 32x32 MFMA result at rows row0.., column col (this lane's
@@ -879,6 +891,256 @@ __global__ __launch_bounds__(64 * NW, RW <= 4 && S == 3 ? 2 : 1) void spmm_group
                 store_tile32<OUT_BF16>(p, acc[i][nt], (int64_t)(it.row + st) * 32,
                                        (int64_t)it.tile * Slice::TN + (wc * NT + nt) * 32 + l32, q);
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Persistent SpMM with specialised waves.  A workgroup owns a list of units
+// (one 32-row stripe x one tile of TN = 128*NTW columns) and streams the
+// entries of all of them, back to back, through two LDS rings: an A ring of SA
+// stages (2 KB each) and a B ring of SB stages (the 32 x TN slice of B).
+//   - waves 0-3 (MFMA waves) read the operands from LDS, multiply, and store
+//     each unit's tile when its last entry is done; they issue no loads, so
+//     their stores never sit in front of a load in a wave's queue;
+//   - waves 4 .. 4+NBW-1 (B loaders) issue the B slice of each entry;
+//   - wave 4+NBW (A loader) issues the entry's A sub-block.
+// A sub-blocks mostly miss to HBM while B slices mostly hit in L2.  A wave's
+// loads return in order, so an A miss at the head of a wave's queue holds back
+// the B hits behind it: with the two in separate waves, a 2 MB L2-resident
+// stream mixed with 1/5 (1/9) of its bytes from HBM measured 19.2 (21.3) TB/s
+// against 15.8 (15.6) with every wave loading both (same byte counts).
+// The ring never drains between units, so a unit's store and the next unit's
+// first loads overlap, and only the first entry of the whole stream waits
+// for a cold fetch.
+// Step k (one barrier X_k): loaders wait until entry k has landed, barrier,
+// then refill the stage of entry k-1 with entry k+S-1; the MFMA waves read
+// entry k's operands (into the set not in use) and multiply entry k-1, then
+// wait for their LDS reads (the stage of entry k is refilled after X_{k+1}).
+// Every wave executes the same n barriers.
+namespace spmm_detail {
+
+// The B slice pieces (1 KB each) of B loader wave wb: piece p = wb*BI + j of
+// the 32 x TN slice in the layout of BSlice; the byte offsets are relative to
+// (first row, first column) of the slice, which the entry word supplies.
+template <int TN, int NBW>
+struct BSliceLoader {
+    static constexpr int ROW_BYTES = 2 * TN;
+    static constexpr int BYTES = 32 * ROW_BYTES;
+    static constexpr int BI = BYTES / 1024 / NBW;
+    static_assert(BI * NBW * 1024 == BYTES, "B pieces per loader wave");
+    uint32_t voff[BI];
+    __device__ __forceinline__ BSliceLoader(int wb, int lane, int64_t ldb) {
+#pragma unroll
+        for (int j = 0; j < BI; ++j) {
+            const int byte = (wb * BI + j) * 1024 + lane * 16;
+            const int r = byte / ROW_BYTES;
+            const int slot = (byte % ROW_BYTES) / 16;
+            voff[j] = (uint32_t)(2 * ((int64_t)r * ldb + 8 * (slot ^ (4 * (r & 3)))));
+        }
+    }
+};
+
+// One loader wave's side of the ring: issue(e, word) issues entry e's loads
+// (P per wave) into stage e % S; the wave takes part in the n barriers.  The
+// entry words come from plan memory through scalar loads, eight at a time and
+// two chunks ahead of use (a scalar-cache miss on the step that needs the
+// word would otherwise stall the issue on every eighth entry).  The word
+// arrays are padded past every stream's end, so the chunks ahead need no
+// bounds test.
+template <int S, int P, typename WT, class Issue>
+__device__ __forceinline__ void stream_loader(int n, const WT* words, Issue&& issue) {
+    static_assert(P * (S - 2) < 64, "vmcnt budget");
+    static_assert(S - 1 <= 16, "the prologue takes its words from the first two chunks");
+    struct W8 {
+        WT w[8];
+    };
+    const W8* ch = (const W8*)words;
+    {
+        const W8 c0 = load_const(ch), c1 = load_const(ch + 1);
+#pragma unroll
+        for (int e = 0; e < S - 1; ++e)
+            if (e < n) issue(e, e < 8 ? c0.w[e] : c1.w[e - 8]);
+    }
+    // Steps 8m .. 8m+7 issue entries 8m+S-1 .. 8m+S+6: chunks m+OFF and m+OFF+1.
+    constexpr int OFF = (S - 1) / 8, R0 = (S - 1) % 8;
+    W8 ca = load_const(ch + OFF), cb = load_const(ch + OFF + 1);
+    for (int k0 = 0; k0 < n; k0 += 8) {
+        const W8 cc = load_const(ch + k0 / 8 + OFF + 2);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int k = k0 + j;
+            if (k >= n) break;
+            if (k + S - 1 < n) {
+                wait_vmcnt<P * (S - 2)>();  // entry k landed (entries k+1 .. k+S-2 may be in flight)
+                barrier_no_fence();
+                issue(k + S - 1, R0 + j < 8 ? ca.w[R0 + j] : cb.w[R0 + j - 8]);
+            } else {
+                wait_stages<P, S - 2>(n - 1 - k);
+                barrier_no_fence();
+            }
+        }
+        ca = cb;
+        cb = cc;
+    }
+}
+
+}  // namespace spmm_detail
+
+template <int NTW, int SB, int SA, int NBW, bool OUT_BF16>
+__global__ __launch_bounds__(64 * (5 + NBW)) void spmm_stream_kernel(SpmmStreamArgs p) {
+    using namespace spmm_detail;
+    constexpr int TN = 128 * NTW;
+    using Loader = BSliceLoader<TN, NBW>;
+    constexpr int A_RING = SA * kA_BYTES;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[A_RING + SB * Loader::BYTES];
+
+    const SpmmStreamWg wg = load_const(p.wgs + blockIdx.x);
+    const int n = wg.n;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t lds0 = lds_address(smem);
+
+    if (wave == 4 + NBW) {
+        // A loader: load j (1 KB) covers segments 2j and 2j+1 of the 32x32
+        // sub-block (lanes 0-31 and 32-63), in the layout of a_load_offset.
+        uint32_t a_voff[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) a_voff[j] = 2 * a_load_offset(2 * j + (lane >> 5), lane, p.lda);
+        stream_loader<SA, 2>(n, p.aw + wg.w_begin, [&](int e, uint32_t w) {
+            const uint16_t* ablk = p.a + (int64_t)w * 32;
+            const uint32_t dst = lds0 + (uint32_t)(e % SA) * kA_BYTES;
+            gl_lds16_s(a_voff[0], ablk, dst);
+            gl_lds16_s(a_voff[1], ablk, dst + 1024);
+        });
+        return;
+    }
+    if (wave >= 4) {
+        const int wb = wave - 4;
+        const Loader ld(wb, lane, p.ldb);
+        const uint32_t b_lds = lds0 + A_RING + wb * Loader::BI * 1024;
+        stream_loader<SB, Loader::BI>(n, p.bw + wg.w_begin, [&](int e, int64_t w) {
+            const uint16_t* bpan = p.b + (int64_t)(uint32_t)w * p.ldb + (int32_t)(w >> 32);
+            const uint32_t dst = b_lds + (uint32_t)(e % SB) * Loader::BYTES;
+#pragma unroll
+            for (int j = 0; j < Loader::BI; ++j) gl_lds16_s(ld.voff[j], bpan, dst + j * 1024);
+        });
+        return;
+    }
+
+    // MFMA waves: wave w owns columns w*NTW*32 .. of each unit's tile.
+    const int l32 = lane & 31, q = lane >> 5;
+    const BReads<TN, NTW> brd(lane, wave * NTW * 32, false);
+    const int a_rd = a_read_offset(l32, q);
+    f32x16 acc[NTW];
+#pragma unroll
+    for (int i = 0; i < NTW; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
+
+    // Unit walk: `cur` is the unit being accumulated, `left` its entries not
+    // yet multiplied, `nxt` the record after it, loaded ahead.  Units with no
+    // entries are stored as zeros on the way.  (The unit array is padded: the
+    // records ahead are valid reads even past the last unit.)
+    const SpmmStreamUnit* units = p.units + wg.u_begin;
+    int u = 0;
+    SpmmStreamUnit cur = load_const(units);
+    SpmmStreamUnit nxt = load_const(units + 1);
+    auto store_cur = [&] {
+        const int64_t row0 = (int64_t)cur.row * 32;
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt) {
+            const int64_t col = cur.n0 + wave * (NTW * 32) + nt * 32 + l32;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int64_t row = row0 + 8 * (v >> 2) + 4 * q + (v & 3);
+                if (OUT_BF16)
+                    store_out(&((uint16_t*)p.c)[row * p.ldc + col], f32_to_bf16_rne(acc[nt][v]));
+                else
+                    store_out(&((float*)p.c)[row * p.ldc + col], acc[nt][v]);
+            }
+        }
+    };
+    // Moves to the next unit with entries, storing (zero) tiles of empty ones.
+    auto next_unit = [&] {
+        ++u;
+        while (u < wg.n_units) {
+            cur = nxt;
+            nxt = load_const(units + u + 1);
+            if (cur.count > 0) return cur.count;
+            store_cur();
+            ++u;
+        }
+        return 0;
+    };
+    int left = 0;
+    if (wg.n_units > 0) {
+        if (cur.count > 0) {
+            left = cur.count;
+        } else {
+            store_cur();
+            left = next_unit();
+        }
+    }
+
+    struct Operands {
+        u32x4 a[2];
+        u32x4 b[2][NTW];
+    };
+    auto read = [&](int k, Operands& o) {
+        const uint8_t* as = smem + (k % SA) * kA_BYTES;
+        o.a[0] = *(const u32x4*)(as + a_rd);
+        o.a[1] = *(const u32x4*)(as + 256 + a_rd);
+        brd.read(smem + A_RING + (k % SB) * Loader::BYTES, o.b);
+    };
+    auto multiply = [&](const Operands& o) {
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int nt = 0; nt < NTW; ++nt) acc[nt] = mfma32(o.a[s2], o.b[s2][nt], acc[nt]);
+        if (--left == 0) {
+            store_cur();
+#pragma unroll
+            for (int i = 0; i < NTW; ++i)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
+            left = next_unit();
+        }
+    };
+    auto fence_sched = [] { __builtin_amdgcn_sched_barrier(0); };
+    auto lds_done = [] { __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); };
+    Operands o0, o1;
+    int k = 0;
+    if (n > 0) {
+        barrier_no_fence();  // X_0
+        read(0, o0);
+        lds_done();
+        k = 1;
+    }
+    // Steps k (odd) and k+1: reads into o1 then o0.
+    for (; k + 1 < n; k += 2) {
+        barrier_no_fence();
+        read(k, o1);
+        fence_sched();
+        multiply(o0);
+        fence_sched();
+        lds_done();
+        barrier_no_fence();
+        read(k + 1, o0);
+        fence_sched();
+        multiply(o1);
+        fence_sched();
+        lds_done();
+    }
+    if (k < n) {
+        barrier_no_fence();
+        read(k, o1);
+        fence_sched();
+        multiply(o0);
+        lds_done();
+        multiply(o1);
+    } else if (n > 0) {
+        multiply(o0);
     }
 }
 
@@ -1601,18 +1863,17 @@ __global__ __launch_bounds__(256) void spgemm_kernel(SpgemmArgs p) {
 
 // ---------------------------------------------------------------------------
 template <int NTW, int S, int G>
-static void launch_spmm_t(const SpmmArgs& a, bool out_bf16, int grid, int n_split, hipStream_t stream) {
+static void launch_spmm_t(const SpmmArgs& a, bool out_bf16, int grid, int n_split, int waves, hipStream_t stream) {
     if constexpr (G == 1) {
         if (out_bf16)
             hipLaunchKernelGGL((spmm_kernel<NTW, S, true>), dim3(grid), dim3(256), 0, stream, a);
         else
             hipLaunchKernelGGL((spmm_kernel<NTW, S, false>), dim3(grid), dim3(256), 0, stream, a);
     } else if constexpr (NTW == 2) {
-        // Eight waves (two per SIMD, 32*RW/2 x 64 outputs each) unless BSP_SPMM_WIDE_WAVES=4;
-        // A fetched in entry pairs when C is a multiple of 64 (the plan then
-        // starts every item at an even entry of its block).
-        const char* ww = std::getenv("BSP_SPMM_WIDE_WAVES");
-        const bool four = ww && std::atoi(ww) == 4;
+        // Eight waves (two per SIMD, 32*RW/2 x 64 outputs each), or four as the
+        // plan fixed; A fetched in entry pairs when C is a multiple of 64 (the
+        // plan then starts every item at an even entry of its block).
+        const bool four = waves == 4;
         const bool pair = a.lda % 64 == 0;
 #define BSP_WIDE(NW_, PAIR_)                                                                                  \
     do {                                                                                                      \
@@ -1652,11 +1913,29 @@ hipError_t launch_spmm(const SpmmArgs& a, const SpmmVariant& v, bool out_bf16, i
     if (!spmm_variant_supported(v)) return hipErrorInvalidValue;
 #define BSP_SPMM_CASE(TN, S, G)                                                   \
     if (v.tile_n == TN && v.stages == S && v.group == G) {                       \
-        launch_spmm_t<TN / 128, S, G>(a, out_bf16, grid, n_split, stream);      \
+        launch_spmm_t<TN / 128, S, G>(a, out_bf16, grid, n_split, v.waves, stream); \
         return hipGetLastError();                                                \
     }
     BSP_SPMM_VARIANTS(BSP_SPMM_CASE)
 #undef BSP_SPMM_CASE
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_spmm_stream(const SpmmStreamArgs& a, const SpmmStreamVariant& v, bool out_bf16, int grid,
+                              hipStream_t stream) {
+    if (grid <= 0) return hipSuccess;
+#define BSP_STREAM_CASE(TN, SB, SA, NB)                                                                         \
+    if (v.tile_n == TN && v.sb == SB && v.sa == SA && v.nbw == NB) {                                           \
+        if (out_bf16)                                                                                          \
+            hipLaunchKernelGGL((spmm_stream_kernel<TN / 128, SB, SA, NB, true>), dim3(grid), dim3(64 * (5 + NB)), 0, \
+                               stream, a);                                                                     \
+        else                                                                                                   \
+            hipLaunchKernelGGL((spmm_stream_kernel<TN / 128, SB, SA, NB, false>), dim3(grid), dim3(64 * (5 + NB)), \
+                               0, stream, a);                                                                  \
+        return hipGetLastError();                                                                              \
+    }
+    BSP_SPMM_STREAM_VARIANTS(BSP_STREAM_CASE)
+#undef BSP_STREAM_CASE
     return hipErrorInvalidValue;
 }
 

@@ -25,6 +25,53 @@ struct SpmmArgs {
     int32_t pad;
 };
 
+// Persistent SpMM (spmm_stream_kernel): each workgroup streams the entries of
+// its units (stripe x tile) through one ring.
+struct SpmmStreamArgs {
+    const uint16_t* a;             // A block values (bf16)
+    const uint16_t* b;             // B (bf16), row-major K x N, leading dim ldb
+    void* c;                       // C (fp32 or bf16), row-major M x N, leading dim ldc
+    const SpmmStreamWg* wgs;       // one per workgroup
+    const SpmmStreamUnit* units;   // unit records (padded)
+    const int64_t* bw;             // per stream entry: first row of B | first column << 32 (padded)
+    const uint32_t* aw;            // per stream entry: A sub-block offset / 32 (padded)
+    int64_t ldb;
+    int64_t ldc;
+    int32_t lda;                   // row stride inside an A block (= C)
+    int32_t N;
+};
+
+// Compiled persistent SpMM variants: tile width, B ring depth, A ring depth,
+// B loader waves.  A workgroup has 4 MFMA waves (each 32*tile/128 columns),
+// the B loader waves and one A loader wave; LDS = 64*tile*SB + 2 KB*SA.
+#define BSP_SPMM_STREAM_VARIANTS(X) \
+    X(128, 6, 12, 2)                \
+    X(128, 6, 12, 4)                \
+    X(128, 4, 16, 4)                \
+    X(256, 4, 16, 4)                \
+    X(256, 5, 16, 8)                \
+    X(256, 6, 8, 8)
+
+struct SpmmStreamVariant {
+    int tile_n;
+    int sb;
+    int sa;
+    int nbw;
+};
+
+inline bool spmm_stream_variant_supported(const SpmmStreamVariant& v) {
+#define BSP_SPMM_STREAM_MATCH(TN, SB, SA, NB) \
+    if (v.tile_n == TN && v.sb == SB && v.sa == SA && v.nbw == NB) return true;
+    BSP_SPMM_STREAM_VARIANTS(BSP_SPMM_STREAM_MATCH)
+#undef BSP_SPMM_STREAM_MATCH
+    return false;
+}
+
+inline int spmm_stream_lds_bytes(const SpmmStreamVariant& v) { return 64 * v.tile_n * v.sb + 2048 * v.sa; }
+
+hipError_t launch_spmm_stream(const SpmmStreamArgs& a, const SpmmStreamVariant& v, bool out_bf16, int grid,
+                              hipStream_t stream);
+
 // Fused attention pair: the SpMM arguments with the mask as A (a = mask
 // values), V as B (b, ldb) and O as C (c, ldc), N = head dimension; plus Q and K.
 struct AttentionArgs {
@@ -98,6 +145,7 @@ struct SpmmVariant {
     int tile_n;
     int stages;
     int group;
+    int waves = 4;  // 256-column row groups: 8 (default) or 4 waves per workgroup
 };
 
 inline bool spmm_variant_supported(const SpmmVariant& v) {
@@ -111,9 +159,9 @@ inline bool spmm_variant_supported(const SpmmVariant& v) {
 // Default ring depth for a tile width and row group.
 inline SpmmVariant spmm_default_variant(int tile_n, int group) {
     switch (group) {
-        case 2: return tile_n >= 256 ? SpmmVariant{256, 3, 2} : SpmmVariant{128, 6, 2};
-        case 4: return tile_n >= 256 ? SpmmVariant{256, 3, 4} : SpmmVariant{128, 4, 4};
-        case 8: return tile_n >= 256 ? SpmmVariant{256, 4, 8} : SpmmVariant{128, 3, 8};
+        case 2: return tile_n >= 256 ? SpmmVariant{256, 3, 2, 8} : SpmmVariant{128, 6, 2};
+        case 4: return tile_n >= 256 ? SpmmVariant{256, 3, 4, 8} : SpmmVariant{128, 4, 4};
+        case 8: return tile_n >= 256 ? SpmmVariant{256, 4, 8, 8} : SpmmVariant{128, 3, 8};
         default: return tile_n >= 256 ? SpmmVariant{256, 4, 1} : SpmmVariant{128, 6, 1};
     }
 }

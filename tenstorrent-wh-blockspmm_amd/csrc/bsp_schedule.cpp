@@ -397,6 +397,134 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
     return BSP_OK;
 }
 
+int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n, int wg_per_cu, SpmmStream& s,
+                      std::string& msg, int col_groups) {
+    int st = validate_bsr(a, msg);
+    if (st != BSP_OK) return st;
+    if (tile_n != 128 && tile_n != 256) {
+        msg = "stream tile must be 128 or 256 columns";
+        return BSP_ERR_UNSUPPORTED;
+    }
+    if (N <= 0 || N % tile_n != 0 || N > INT32_MAX / 2) {
+        msg = "N must be a positive multiple of the stream tile";
+        return BSP_ERR_UNSUPPORTED;
+    }
+    if (a->R % kSub || a->C % kSub) {
+        msg = "R and C must be multiples of 32";
+        return BSP_ERR_UNSUPPORTED;
+    }
+    if (num_cus <= 0) num_cus = 256;
+    if (wg_per_cu < 1) wg_per_cu = 1;
+    const int64_t RS = a->R / kSub, CS = a->C / kSub;
+    const int64_t nsr = a->H / kSub;
+    const int64_t n_tiles = N / tile_n;
+    const int64_t per_stripe_total = a->nblocks * CS;  // entries summed over one stripe of every block row
+    if (per_stripe_total * RS * n_tiles > INT32_MAX - kStreamPad || nsr > INT32_MAX || a->W > INT32_MAX ||
+        a->nblocks * a->R * a->C / kSub > UINT32_MAX) {
+        msg = "problem too large for the stream schedule";
+        return BSP_ERR_UNSUPPORTED;
+    }
+    s = SpmmStream{};
+    s.tile_n = tile_n;
+    s.n_tiles = (int32_t)n_tiles;
+    s.wg_per_cu = wg_per_cu;
+
+    // Column groups: the fewest (1, 2, 4, 8) that bring one XCD's slice of B
+    // to at most 2 MiB, limited by the tile count (or as asked).
+    int64_t cg = 1;
+    const int64_t b_bytes = a->W * N * 2;
+    while (cg < kNumXcd && b_bytes / cg > (2 << 20) && n_tiles % (cg * 2) == 0) cg *= 2;
+    if (col_groups > 0) cg = col_groups;
+    if (cg < 1 || kNumXcd % cg != 0 || n_tiles % cg != 0) cg = 1;
+    s.col_groups = (int32_t)cg;
+    const int64_t rg_count = kNumXcd / cg, tpg = n_tiles / cg;
+
+    // Stripe entry counts; a unit costs its entries plus the store.
+    constexpr int64_t kStoreCost = 2;
+    std::vector<int64_t> cnt(nsr);
+    for (int64_t sr = 0; sr < nsr; ++sr) {
+        const int64_t i = sr / RS;
+        cnt[sr] = (int64_t)(a->indptr[i + 1] - a->indptr[i]) * CS;
+    }
+    // Stripes onto row groups, longest first onto the least-loaded group.
+    std::vector<int32_t> order(nsr);
+    std::iota(order.begin(), order.end(), 0);
+    std::stable_sort(order.begin(), order.end(), [&](int32_t x, int32_t y) { return cnt[x] > cnt[y]; });
+    std::vector<std::vector<int32_t>> rows(rg_count);
+    using Load = std::pair<int64_t, int>;
+    {
+        std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
+        for (int g = 0; g < rg_count; ++g) heap.push({0, g});
+        for (int32_t sr : order) {
+            Load l = heap.top();
+            heap.pop();
+            rows[l.second].push_back(sr);
+            heap.push({l.first + cnt[sr] + kStoreCost, l.second});
+        }
+    }
+    // Inside each XCD: units longest first onto the least-loaded compute
+    // unit, then each compute unit's units longest first onto the
+    // least-loaded of its workgroups.  The two workgroups of a compute unit
+    // share its load path, so the balance that matters first is per compute
+    // unit.  An XCD's dispatcher gives its j-th workgroup to compute unit
+    // j % C (C = compute units per XCD): workgroup c of compute unit u is the
+    // XCD's workgroup u + c*C.
+    const int cus_per_xcd = std::max(1, num_cus / kNumXcd);
+    const int bins = cus_per_xcd * wg_per_cu;
+    std::vector<std::vector<SpmmStreamUnit>> wg_units((size_t)bins * kNumXcd);
+    auto lpt = [](const std::vector<SpmmStreamUnit>& us, int nb, std::vector<std::vector<SpmmStreamUnit>>& out) {
+        out.assign(nb, {});
+        std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
+        for (int b = 0; b < nb; ++b) heap.push({0, b});
+        for (const SpmmStreamUnit& u : us) {  // longest first
+            Load l = heap.top();
+            heap.pop();
+            out[l.second].push_back(u);
+            heap.push({l.first + u.count + kStoreCost, l.second});
+        }
+    };
+    for (int64_t rg = 0; rg < rg_count; ++rg)
+        for (int64_t c = 0; c < cg; ++c) {
+            const int x = (int)(rg * cg + c);
+            std::vector<SpmmStreamUnit> us;
+            for (int32_t sr : rows[rg])  // rows[rg] is longest first
+                for (int64_t t = c * tpg; t < (c + 1) * tpg; ++t)
+                    us.push_back({sr, (int32_t)(t * tile_n), (int32_t)cnt[sr], 0});
+            std::vector<std::vector<SpmmStreamUnit>> per_cu, per_wg;
+            lpt(us, cus_per_xcd, per_cu);
+            for (int cu = 0; cu < cus_per_xcd; ++cu) {
+                lpt(per_cu[cu], wg_per_cu, per_wg);
+                for (int w = 0; w < wg_per_cu; ++w)
+                    wg_units[(size_t)(cu + w * cus_per_xcd) * kNumXcd + x] = std::move(per_wg[w]);
+            }
+        }
+    // Streams, workgroup by workgroup (workgroup g = bin * kNumXcd + xcd).
+    s.wgs.resize(wg_units.size());
+    for (size_t g = 0; g < wg_units.size(); ++g) {
+        SpmmStreamWg& w = s.wgs[g];
+        w.w_begin = (int32_t)s.bw.size();
+        w.u_begin = (int32_t)s.units.size();
+        w.n_units = (int32_t)wg_units[g].size();
+        for (const SpmmStreamUnit& u : wg_units[g]) {
+            s.units.push_back(u);
+            const int64_t i = u.row / RS, sub = u.row % RS;
+            for (int64_t blk = a->indptr[i]; blk < a->indptr[i + 1]; ++blk)
+                for (int64_t t = 0; t < CS; ++t) {
+                    const int64_t brow = (int64_t)a->indices[blk] * a->C + kSub * t;
+                    s.bw.push_back(brow | ((int64_t)u.n0 << 32));
+                    s.aw.push_back((uint32_t)((blk * a->R * a->C + kSub * sub * a->C + kSub * t) / kSub));
+                }
+        }
+        w.n = (int32_t)(s.bw.size() - w.w_begin);
+        s.max_wg_entries = std::max(s.max_wg_entries, w.n);
+    }
+    s.n_entries = (int64_t)s.bw.size();
+    s.bw.resize(s.bw.size() + kStreamPad, 0);
+    s.aw.resize(s.aw.size() + kStreamPad, 0);
+    s.units.resize(s.units.size() + kStreamPad, SpmmStreamUnit{0, 0, 0, 0});
+    return BSP_OK;
+}
+
 int build_sddmm_schedule(const bsp_bsr_desc* m, int64_t K, int num_cus, SddmmSchedule& s,
                          std::string& msg) {
     int st = validate_bsr(m, msg);

@@ -69,6 +69,54 @@ struct SpmmSchedule {
 
 // Per-workgroup records in launch order (items expanded through wgmap).
 std::vector<SpmmWg> spmm_wg_records(const SpmmSchedule& s);
+
+// ---- persistent SpMM (spmm_stream_kernel) -----------------------------------
+// A unit is one 32-row stripe times one tile of tile_n output columns.  Each
+// workgroup of the persistent grid owns a list of units and streams their
+// entries (32x32 sub-block products) back to back through one LDS ring, so
+// the ring never drains between units and a unit's store overlaps the next
+// unit's loads.
+struct SpmmStreamWg {
+    int32_t w_begin;  // first word of this workgroup's entry stream
+    int32_t n;        // entries in the stream (sum of its units' counts)
+    int32_t u_begin;  // first unit record
+    int32_t n_units;
+};
+static_assert(sizeof(SpmmStreamWg) == 16, "SpmmStreamWg layout is shared with the kernels");
+
+struct SpmmStreamUnit {
+    int32_t row;    // stripe (32 output rows)
+    int32_t n0;     // first output column
+    int32_t count;  // entries (0: the stripe has no nonzeros; its tile is stored as zeros)
+    int32_t pad;
+};
+static_assert(sizeof(SpmmStreamUnit) == 16, "SpmmStreamUnit layout is shared with the kernels");
+
+// Trailing words and units past the last workgroup's stream: the kernels
+// prefetch a few records ahead without a bounds test.
+constexpr int kStreamPad = 64;
+
+struct SpmmStream {
+    int32_t tile_n = 0;
+    int32_t n_tiles = 0;
+    int32_t wg_per_cu = 1;
+    int32_t col_groups = 1;        // column groups of the XCD map
+    int32_t max_wg_entries = 0;    // longest workgroup stream
+    int64_t n_entries = 0;         // sum over units (entries x tiles)
+    std::vector<SpmmStreamWg> wgs;        // one per workgroup; workgroup g runs on XCD g % kNumXcd
+    std::vector<SpmmStreamUnit> units;    // + kStreamPad zero records
+    std::vector<int64_t> bw;              // per stream entry: first row of B | first column << 32 (+ pad)
+    std::vector<uint32_t> aw;             // per stream entry: A sub-block element offset / 32 (+ pad)
+};
+
+// Persistent schedule for 32-row stripes (any R, C multiples of 32) and
+// tiles of tile_n (128 or 256) columns, N a multiple of tile_n, wg_per_cu
+// workgroups per compute unit.  Units are spread over the XCDs in a 2-D split
+// (column groups of tiles, row groups of stripes, as xcd_tile_map) and, inside
+// an XCD, longest first onto the least-loaded workgroup.  Cost of a unit:
+// entries + store_cost.
+int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n, int wg_per_cu,
+                      SpmmStream& s, std::string& msg, int col_groups = 0);
 // Entries packed for the kernel: first row of B | (A offset / 32) << 32.
 std::vector<int64_t> spmm_packed_entries(const SpmmSchedule& s);
 // The split stripes in slot order (a split group contributes each of its

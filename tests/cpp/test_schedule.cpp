@@ -375,6 +375,57 @@ void check_spgemm(const Bsr& a, const Bsr& b, int cus, const std::string& name) 
                 s.tasks.size(), s.terms.size(), s.grid);
 }
 
+// Persistent SpMM schedule: every (stripe, tile) unit appears once, on the
+// XCD whose column group holds its tile; each unit's stream entries are the
+// stripe's products in the reference's order (blocks in CSR order, then the
+// 32-column steps of a block) with the right B row, column and A offset; the
+// workgroup streams are contiguous and their lengths add up.
+void check_spmm_stream(const Bsr& a, int64_t N, int cus, int tile_n, int wpc, const std::string& name) {
+    SpmmStream s;
+    std::string msg;
+    const bsp_bsr_desc d = a.desc();
+    const int st = build_spmm_stream(&d, N, cus, tile_n, wpc, s, msg);
+    expect(st == BSP_OK, name + ": build (" + msg + ")");
+    if (st != BSP_OK) return;
+    const int64_t RS = a.R / kSub, CS = a.C / kSub, nsr = a.H / kSub, n_tiles = N / tile_n;
+    expect((int64_t)s.wgs.size() == (int64_t)(cus / kNumXcd) * wpc * kNumXcd, name + ": grid");
+    std::vector<int> seen(nsr * n_tiles, 0);
+    int64_t w = 0, u = 0;
+    const int64_t tpg = n_tiles / s.col_groups;
+    for (size_t g = 0; g < s.wgs.size(); ++g) {
+        const SpmmStreamWg& wg = s.wgs[g];
+        expect(wg.w_begin == w && wg.u_begin == u, name + ": contiguous streams");
+        int64_t e = wg.w_begin, total = 0;
+        for (int32_t j = 0; j < wg.n_units; ++j) {
+            const SpmmStreamUnit& un = s.units[wg.u_begin + j];
+            const int64_t tile = un.n0 / tile_n;
+            expect(un.n0 % tile_n == 0 && tile < n_tiles && un.row < nsr, name + ": unit fields");
+            ++seen[un.row * n_tiles + tile];
+            // XCD g % 8 is column group (g % 8) % col_groups.
+            expect(tile / tpg == (int64_t)((g % kNumXcd) % s.col_groups), name + ": unit on its column group's XCD");
+            const int64_t i = un.row / RS, sub = un.row % RS;
+            expect(un.count == (a.indptr[i + 1] - a.indptr[i]) * CS, name + ": unit count");
+            for (int64_t blk = a.indptr[i]; blk < a.indptr[i + 1]; ++blk)
+                for (int64_t t = 0; t < CS; ++t, ++e) {
+                    const int64_t brow = (int64_t)a.indices[blk] * a.C + kSub * t;
+                    const int64_t aoff = blk * a.R * a.C + kSub * sub * a.C + kSub * t;
+                    expect((s.bw[e] & 0xffffffffLL) == brow && (s.bw[e] >> 32) == un.n0, name + ": B word");
+                    expect((int64_t)s.aw[e] * kSub == aoff, name + ": A word");
+                }
+            total += un.count;
+        }
+        expect(total == wg.n && e == wg.w_begin + wg.n, name + ": stream length");
+        w += wg.n;
+        u += wg.n_units;
+    }
+    expect(std::all_of(seen.begin(), seen.end(), [](int v) { return v == 1; }), name + ": every unit once");
+    expect(w == s.n_entries && (int64_t)s.bw.size() == w + kStreamPad && (int64_t)s.aw.size() == w + kStreamPad &&
+               (int64_t)s.units.size() == u + kStreamPad,
+           name + ": padding");
+    std::printf("%-34s units %6lld entries %8lld grid %zu cg %d max wg %d\n", name.c_str(), (long long)u,
+                (long long)s.n_entries, s.wgs.size(), s.col_groups, s.max_wg_entries);
+}
+
 }  // namespace
 
 int main() {
@@ -396,6 +447,13 @@ int main() {
     check_spmm(skewed(1024, 2048, 128, 64, 40, 8), 96, cus, "spmm 128x64 blocks, skewed");
     check_spmm(uniform(1024, 1024, 32, 32, 0, 9), 256, cus, "spmm empty");
     check_spmm(banded(8192, 32, 8, 655, 19), 128, cus, "spmm banded 8192^2 (row bands)");
+    check_spmm_stream(uniform(4096, 4096, 32, 32, 4096, 1), 512, cus, 128, 2, "stream 4096^2 25% tile 128");
+    check_spmm_stream(uniform(4096, 4096, 32, 32, 4096, 1), 512, cus, 256, 1, "stream 4096^2 25% tile 256");
+    check_spmm_stream(uniform(4096, 4096, 32, 32, 164, 3), 512, cus, 128, 2, "stream 4096^2 1%");
+    check_spmm_stream(skewed(16384, 16384, 32, 32, 5243, 5), 1024, cus, 128, 2, "stream skewed, duplicates");
+    check_spmm_stream(uniform(2048, 1024, 64, 128, 60, 7), 256, cus, 256, 1, "stream 64x128 blocks");
+    check_spmm_stream(uniform(1024, 1024, 32, 32, 0, 9), 256, cus, 128, 1, "stream empty");
+    check_spmm_stream(uniform(1024, 1024, 32, 32, 30, 9), 128, 8, 128, 2, "stream 8 CUs");
     check_sddmm(uniform(4096, 4096, 32, 32, 1638, 10), 256, cus, "sddmm 4096^2 10% K=256");
     check_sddmm(skewed(2048, 2048, 64, 32, 300, 11), 128, cus, "sddmm 64x32 blocks, skewed");
     check_sddmm(uniform(1024, 1024, 128, 128, 20, 12), 64, cus, "sddmm 128x128 blocks");

@@ -125,19 +125,22 @@ def test_many_empty_rows_R256():
     assert np.all(got[256:] == 0.0)
 
 
-# --- skewed rows: exercises split rows and the last-arriver fixup
-@pytest.mark.parametrize("split", [None, 40])
-def test_skewed_workload_full_size(monkeypatch, split):
-    """The skewed workload as planned (its rows fit one compute unit's share,
-    so they stay whole) and with the rows over 40 entries cut into pieces
-    (the reduce kernel adds them): held to the oracle, and the same bits on a
-    second run."""
+# --- skewed rows: the persistent kernel, and the per-item kernels with split
+# rows (the reduce kernel adds the pieces)
+@pytest.mark.parametrize("kernel,split", [("persistent", None), ("items", None), ("items", 40)])
+def test_skewed_workload_full_size(monkeypatch, kernel, split):
+    """The skewed workload as planned (the persistent kernel), on the per-item
+    kernels with every row whole, and with the rows over 40 entries cut into
+    pieces: held to the oracle, and the same bits on a second run."""
+    if kernel == "items":
+        monkeypatch.setenv("BSP_SPMM_STREAM", "0")
     if split:
         monkeypatch.setenv("BSP_SPMM_SPLIT", str(split))
     w = W.workload_spmm_skewed()
     a = w["a"]
     plan = capi.SpmmPlan(capi.Bsr(a.H, a.W, 32, 32, a.indptr, a.indices), w["N"], "f32")
     info = plan.info()
+    assert info["persistent"] == (kernel == "persistent")
     assert (info["n_split_rows"] > 0) == bool(split)
     got1 = run_spmm(a, w["b"], "f32", plan=plan)
     got2 = run_spmm(a, w["b"], "f32", plan=plan)
@@ -148,7 +151,8 @@ def test_skewed_workload_full_size(monkeypatch, split):
 
 @pytest.mark.parametrize("split", [1, 3, 7])
 def test_forced_splits(monkeypatch, split):
-    """Every row cut into pieces of at most `split` entries."""
+    """Every row cut into pieces of at most `split` entries (per-item kernels)."""
+    monkeypatch.setenv("BSP_SPMM_STREAM", "0")
     monkeypatch.setenv("BSP_SPMM_SPLIT", str(split))
     w = W.spmm_workload(1024, 2048, 512, 32, 32, 0.2, seed=11)
     _case(w["a"], w["b"], "f32", f"split={split}")
@@ -163,6 +167,7 @@ SPMM_VARIANTS = [(128, 4), (128, 6), (128, 8), (256, 3), (256, 4)]
 @pytest.mark.parametrize("density", [0.1, 0.5])
 @pytest.mark.parametrize("tile_n,stages", SPMM_VARIANTS)
 def test_kernel_variants(monkeypatch, tile_n, stages, density):
+    monkeypatch.setenv("BSP_SPMM_STREAM", "0")
     monkeypatch.setenv("BSP_SPMM_TILE_N", str(tile_n))
     monkeypatch.setenv("BSP_SPMM_STAGES", str(stages))
     w = W.spmm_workload(2048, 2048, 512, 32, 32, density, seed=12)

@@ -1,0 +1,111 @@
+"""The persistent SpMM kernel (spmm_stream_kernel) on the GPU against the
+oracle (omp_spmm_bf16, block_spmm/inc/bsr_matrix.hpp:954-1000): every compiled
+variant and workgroups-per-compute-unit setting, streams that cross many
+units (empty stripes among them), streams longer than the word prefetch, and
+grids with more workgroups than units.  Outputs are poisoned with NaN before
+each launch, so an unwritten element fails."""
+import numpy as np
+import pytest
+
+from helpers import W, assert_parity, bsr_of, capi, golden_spmm, run_spmm, spmm_k_eff
+
+pytestmark = pytest.mark.gpu
+
+# (tile, B ring, A ring, B loader waves) of BSP_SPMM_STREAM_VARIANTS in csrc/bsp_kernels.hpp
+STREAM_VARIANTS = [(128, 6, 12, 2), (128, 6, 12, 4), (128, 4, 16, 4), (256, 4, 16, 4), (256, 5, 16, 8),
+                   (256, 6, 8, 8)]
+
+
+def _lds(v):
+    return 64 * v[0] * v[1] + 2048 * v[2]
+
+
+def _stream_env(monkeypatch, v, wpc=None):
+    monkeypatch.setenv("BSP_SPMM_STREAM", "1")
+    monkeypatch.setenv("BSP_SPMM_STREAM_VARIANT", ",".join(map(str, v)))
+    if wpc:
+        monkeypatch.setenv("BSP_SPMM_STREAM_WPC", str(wpc))
+
+
+def _check(a, b, out_dtype, what, v=None, wpc=None):
+    plan = capi.SpmmPlan(bsr_of(a), b.shape[1], out_dtype)
+    info = plan.info()
+    assert info["persistent"] == 1, f"{what}: plan is not persistent ({info})"
+    if v is not None:
+        assert (info["tile_n"], info["stages"], info["a_stages"], info["waves"]) == (v[0], v[1], v[2], 5 + v[3])
+    if wpc is not None:
+        assert info["grid"] == 256 * wpc
+    got = run_spmm(a, b, out_dtype, plan=plan)
+    got2 = run_spmm(a, b, out_dtype, plan=plan)
+    plan.close()
+    np.testing.assert_array_equal(got, got2, err_msg=f"{what}: two runs differ")
+    return assert_parity(got, golden_spmm(a, b), spmm_k_eff(a), what)
+
+
+@pytest.mark.parametrize("density", [0.1, 0.5])
+@pytest.mark.parametrize("v", STREAM_VARIANTS)
+def test_stream_variants(monkeypatch, v, density):
+    """Every variant, with as many workgroups per compute unit as its LDS
+    allows (one or two), both output types."""
+    for wpc in (1, 2):
+        if wpc * _lds(v) > 160 * 1024:
+            continue
+        _stream_env(monkeypatch, v, wpc)
+        w = W.spmm_workload(2048, 2048, 512, 32, 32, density, seed=80 + wpc)
+        for od in ("f32", "bf16"):
+            _check(w["a"], w["b"], od, f"variant={v} wpc={wpc} d={density} {od}", v, wpc)
+
+
+@pytest.mark.parametrize("v", [(128, 6, 12, 2), (256, 4, 16, 4)])
+def test_stream_many_units_per_workgroup(monkeypatch, v):
+    """32768 rows x 1024 columns at 0.2%: 8192 or 4096 units on 256-512
+    workgroups (16 per workgroup), many of them empty stripes, stored as zeros."""
+    _stream_env(monkeypatch, v)
+    w = W.spmm_workload(32768, 4096, 1024, 32, 32, 0.002, seed=91)
+    a = w["a"]
+    assert (np.diff(a.indptr) == 0).sum() > 100  # empty stripes among the units
+    _check(a, w["b"], "f32", f"many units {v}")
+
+
+@pytest.mark.parametrize("v", [(128, 6, 12, 2), (256, 5, 16, 8)])
+def test_stream_long_rows(monkeypatch, v):
+    """A few rows of 200-400 entries (streams far longer than the ring and the
+    word prefetch) among short ones."""
+    _stream_env(monkeypatch, v)
+    rng = np.random.default_rng(92)
+    nbr, nbc = 64, 512
+    counts = rng.integers(0, 6, nbr)
+    counts[[3, 17, 40]] = [400, 250, 200]
+    indices = np.concatenate([np.sort(rng.choice(nbc, c, replace=False)) for c in counts]).astype(np.int32)
+    indptr = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    a = W.BsrArrays(nbr * 32, nbc * 32, 32, 32, indptr, indices)
+    a.data = W.block_content(a.nblocks, 32, 32, "RAND", rng)
+    b = W.dense_content(nbc * 32, 256, "RAND", rng)
+    _check(a, b, "f32", f"long rows {v}")
+    _check(a, b, "bf16", f"long rows {v} bf16")
+
+
+def test_stream_fewer_units_than_workgroups(monkeypatch):
+    """A 64x128 problem: 2 units for 512 workgroups; the rest stream nothing."""
+    _stream_env(monkeypatch, (128, 6, 12, 2), 2)
+    w = W.spmm_workload(64, 256, 128, 32, 32, 0.5, seed=93)
+    _check(w["a"], w["b"], "f32", "2 units")
+
+
+def test_stream_empty_matrix(monkeypatch):
+    """No stored blocks: every unit is an empty stripe, every tile stored as zeros."""
+    _stream_env(monkeypatch, (128, 6, 12, 2))
+    a = W.BsrArrays(1024, 1024, 32, 32, np.zeros(33, np.int32), np.zeros(0, np.int32))
+    a.data = np.zeros(0, np.uint16)
+    b = W.dense_content(1024, 256, "RAND", np.random.default_rng(94))
+    got = run_spmm(a, b, "f32")
+    assert np.all(got == 0.0)
+
+
+@pytest.mark.parametrize("R,C", [(64, 64), (32, 96), (96, 32)])
+def test_stream_other_block_shapes(monkeypatch, R, C):
+    """Blocks other than 32x32 cut into 32-row stripes (no row groups)."""
+    monkeypatch.setenv("BSP_SPMM_GROUP", "1")
+    _stream_env(monkeypatch, (128, 6, 12, 2))
+    w = W.spmm_workload(1536, 1536, 256, R, C, 0.2, seed=95 + R + C)
+    _check(w["a"], w["b"], "f32", f"R={R} C={C}")
