@@ -1,37 +1,49 @@
 """Benchmark: effective TFLOP/s of block-sparse SpMM on one MI355X.
 
-Workload (the headline): C = A*B with A 4096x4096 in 32x32 bf16 blocks at 25%
-uniform-random block density, B 4096x512 bf16, fp32 accumulation and fp32
-output.  The same run reports the whole density sweep {1, 5, 25, 50}% (fp32
-and bf16 outputs), and one line each for the SDDMM, skewed-SpMM and
-attention-pair workloads.
+Workload of the headline line: C = A*B with A 4096x4096 in 32x32 bf16 blocks
+at 25% uniform-random block density, B 4096x512 bf16, fp32 accumulation and
+fp32 output.  The same run reports every benchmark configuration as a section:
+  c1         A 1024x1024, 10%, N=256 (the reference's CPU-golden case)
+  sweep      A 4096x4096, densities 1/5/25/50%, N=512, fp32 and bf16 C
+  sddmm      mask 4096x4096 10%, X 4096x256, Y 256x4096
+  skewed     A 16384x16384, Zipf(1.2) rows, 2% mean, N=1024
+  attention  seq 8192, d 128: SDDMM then SpMM, and the fused pair
+  spgemm     8192x8192 x 8192x8192, 32x32 blocks, 5% x 5%
+  large      the reference's 8192^3 configuration (256x256 blocks, 25%) and
+             the same shape with 128x128 and 64x64 blocks
+  patterns   the reference's pattern families (Row, Col, Multi-diag, Random,
+             tril, triu) at 8192^3 with 256x256 blocks
+  host       the blocking host-buffer entry point (PCIe included; never `value`)
 
-A step is one SpMM launch over the whole workload.  Inputs are resident in
-HBM: the timed loop cycles through enough copies of A, B and C (> 512 MB) that
-no launch finds its operands in the 256 MB Infinity Cache.  Effective
-TFLOP/s counts only nonzero-block FLOPs, 2*nnzb*R*C*N (the reference's formula,
-GEMM_profiling/read_spmm_profiler.py:73).
+A step is one launch over the whole workload.  Inputs are resident in HBM:
+the timed launches cycle through enough copies of the operands and outputs
+(> 512 MB) that no launch finds them in the 256 MB Infinity Cache.
+Effective TFLOP/s counts only nonzero-block FLOPs, 2*nnzb*R*C*N (the
+reference's formula, GEMM_profiling/read_spmm_profiler.py:73).
 
-Timing: the K timed launches are captured once into a HIP graph and replayed
-between two HIP events on the launch stream, bracketed by device
-synchronisations; `value` = FLOPs per launch / (replay time / K), the
-steady-state per-launch throughput of the device (launch gaps included, host
-overhead excluded).  Each launch is also timed individually with an event pair
-(`eager_event_us`), which adds the dispatch overhead of a lone launch.
-
+Timing, per section, all on the stream the kernels run on:
+  - us_per_launch: the K timed launches captured once into a HIP graph and
+    replayed between two HIP events; replay time / K is the steady-state time
+    per launch (the fixed cost of a launch included).  `value` and the
+    headline roofline use it.
+  - kernel_us: the same launches issued one by one and traced (torch's
+    profiler, the HIP runtime's activity records): the median kernel duration,
+    as rocprofv3 --kernel-trace reports it.
 The CPU baseline is the oracle (the C restatement of the reference's golden,
-oracle/bsp_oracle.c) on this host: all cores on the whole 25% workload, and
-one core on a 32-block-row sample.  Every other section carries a "cpu"
-record too: the oracle on the same workload (or a named sample of its block
-rows), its TFLOP/s and the GPU's speedup over it.
+oracle/bsp_oracle.c) on this host, per section: one thread (how the
+reference's golden runs: its OpenMP pragma does not compile) on a named
+sample of block rows, and all cores (OpenMP over block rows) on the whole
+workload; median of 3 runs after one warm-up.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only a,b]
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -44,6 +56,7 @@ sys.path.insert(0, str(REPO))
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (AMD Instinct MI355X datasheet)
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 ROTATE_BYTES = 600 << 20   # > 2 x the 256 MB Infinity Cache
+SECTIONS = ("c1", "sweep", "sddmm", "skewed", "attention", "spgemm", "large", "patterns", "host")
 
 
 def parse_args():
@@ -52,44 +65,46 @@ def parse_args():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-kernel-time", action="store_true", help="skip the traced kernel durations")
     p.add_argument("--copy-calibration", action="store_true",
                    help="first run a 256 MiB device copy and a 256 MiB elementwise multiply (kernels of known traffic, "
                         "for scaling FETCH_SIZE / WRITE_SIZE counters)")
-    p.add_argument("--only", default="", help="comma list of sections to run: head (25%% fp32 only), sweep, sddmm, skewed, attention, spgemm, "
-                   "large, host")
+    p.add_argument("--only", default="", help="comma list of sections (head = the 25%% fp32 sweep point only): "
+                   + ", ".join(("head",) + SECTIONS))
     return p.parse_args()
 
 
+# ---------------------------------------------------------------------------
+# Timing
 class Timer:
-    """Two measurements of the same launches, both with HIP events on the
-    stream the kernels run on:
-      - graph: the K timed launches are captured once into a HIP graph and
-        replayed back to back (no host work between launches); the events
-        bracket the replay, so wall/K is the per-launch time the device
-        delivers in steady state, launch gaps included;
-      - eager: one event pair around each individually launched kernel."""
+    """Graph replay of K launches between two HIP events (us_per_launch), and
+    the same launches one by one under the tracer (kernel durations)."""
 
-    def __init__(self, torch, steps):
+    def __init__(self, torch, steps, trace=True):
         self.torch = torch
         self.steps = steps
-        self.ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                   for _ in range(steps)]
+        self.trace = trace
 
-    def run(self, launch, steps, warmup):
+    def run(self, launch, warmup, kernel_filter=("bsp::",)):
         torch = self.torch
+        steps = self.steps
         cur = torch.cuda.current_stream()
         for i in range(warmup):
             launch(i, cur.cuda_stream)
         torch.cuda.synchronize()
-        # eager, per-launch events
-        for i in range(steps):
-            s, e = self.ev[i]
-            s.record()
-            launch(warmup + i, cur.cuda_stream)
-            e.record()
-        torch.cuda.synchronize()
-        per = [s.elapsed_time(e) for s, e in self.ev[:steps]]  # ms
-        # graph of the K launches, replayed between two events
+        kernels = {}
+        if self.trace:
+            from torch.profiler import ProfilerActivity, profile
+            with profile(activities=[ProfilerActivity.CUDA]) as prof:
+                for i in range(steps):
+                    launch(warmup + i, cur.cuda_stream)
+                    cur.synchronize()  # one launch at a time: each kernel starts on an idle GPU
+            per = {}
+            for e in prof.events():
+                if e.device_time > 0 and any(k in e.name for k in kernel_filter):
+                    per.setdefault(e.name, []).append(e.device_time)
+            kernels = {name: {"median_us": round(float(np.median(v)), 3), "mean_us": round(float(np.mean(v)), 3),
+                              "launches": len(v)} for name, v in per.items()}
         graph = torch.cuda.CUDAGraph()
         cap = torch.cuda.Stream()
         cap.wait_stream(cur)
@@ -100,27 +115,84 @@ class Timer:
         graph.replay()  # one untimed replay
         torch.cuda.synchronize()
         g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0 = time.perf_counter()
         g0.record()
         graph.replay()
         g1.record()
         torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
         graph_ms = g0.elapsed_time(g1)
         del graph
-        return {"wall_s": wall, "graph_ms": graph_ms, "launch_ms": graph_ms / steps,
-                "kernel_ms_mean": float(np.mean(per)), "kernel_ms_median": float(np.median(per)),
-                "kernel_ms_min": float(np.min(per))}
+        # kernel time per launch: the sum over the launch's kernels (a split
+        # plan adds its reduce kernel) of their median traced durations
+        k_us = sum(v["median_us"] * v["launches"] / steps for v in kernels.values()) if kernels else None
+        return {"graph_ms": graph_ms, "launch_ms": graph_ms / steps, "kernel_us": k_us, "kernels": kernels}
 
 
 def dev_u16(torch, arr):
     arr = np.ascontiguousarray(arr, dtype=np.uint16)
+    if arr.size == 0:
+        return torch.zeros(8, dtype=torch.int16, device="cuda")
     return torch.from_numpy(arr.view(np.int16)).to("cuda")
 
 
-def bench_spmm(torch, capi, W, a, b, out_dtype, steps, warmup, rotate=True):
-    """Times SpMM on (a, b); returns timings, FLOPs and algorithmic bytes."""
-    M, K, N = a.H, a.W, b.shape[1]
+def summarize(t, flops, nbytes):
+    """Per-launch figures from the graph replay and from the traced kernel
+    durations: us, TFLOP/s, GB/s (algorithmic bytes) and fractions of peak."""
+    k_s = t["launch_ms"] * 1e-3
+    out = {
+        "us_per_launch": round(t["launch_ms"] * 1e3, 3),
+        "tflops": round(flops / k_s / 1e12, 3),
+        "frac_mfma_peak": round(flops / k_s / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "gbs": round(nbytes / k_s / 1e9, 1),
+        "frac_hbm_peak": round(nbytes / k_s / 1e9 / PEAK_HBM_GBS, 4),
+        "flops": flops,
+        "bytes": nbytes,
+    }
+    if t.get("kernel_us"):
+        ks = t["kernel_us"] * 1e-6
+        out.update({"kernel_us": round(t["kernel_us"], 3),
+                    "kernel_tflops": round(flops / ks / 1e12, 3),
+                    "kernel_gbs": round(nbytes / ks / 1e9, 1),
+                    "kernel_frac_hbm_peak": round(nbytes / ks / 1e9 / PEAK_HBM_GBS, 4),
+                    "kernel_frac_mfma_peak": round(flops / ks / 1e12 / PEAK_BF16_TFLOPS, 4),
+                    "kernels": t["kernels"]})
+    return out
+
+
+def plan_summary(info):
+    keys = ("tile_n", "stages", "group", "grid", "waves", "persistent", "a_stages", "n_split_rows")
+    return {k: info[k] for k in keys if k in info}
+
+
+# ---------------------------------------------------------------------------
+# Measured HBM-side traffic from the committed counter summaries
+# (profiles/*_traffic.md: FETCH_SIZE and WRITE_SIZE per dispatch, scaled by
+# kernels of known traffic).
+def committed_traffic() -> dict:
+    out = {}
+    for f in sorted((REPO / "profiles").glob("*_traffic.md")):
+        kv = dict(line.split(": ", 1) for line in f.read_text().splitlines() if line.startswith("traffic_"))
+        if "traffic_workload" in kv and "traffic_bytes_per_launch" in kv:
+            out[kv["traffic_workload"]] = {"file": f.name, "kernel": kv.get("traffic_kernel"),
+                                           "bytes": int(kv["traffic_bytes_per_launch"])}
+    return out
+
+
+TRAFFIC = committed_traffic()
+
+
+def attach_traffic(rec, key):
+    tr = TRAFFIC.get(key)
+    if tr:
+        rec["traffic"] = {"bytes_per_launch": tr["bytes"], "ratio_to_algorithmic": round(tr["bytes"] / rec["bytes"], 3),
+                          "source": "profiles/" + tr["file"], "kernel": tr["kernel"]}
+    rec["traffic_key"] = key
+
+
+# ---------------------------------------------------------------------------
+# Sections
+def bench_spmm(torch, capi, W, a, b, out_dtype, timer, warmup, rotate=True):
+    """Times SpMM on (a, b); returns (timings, flops, bytes, plan info, copies)."""
+    M, N = a.H, b.shape[1]
     plan = capi.SpmmPlan(capi.Bsr(a.H, a.W, a.R, a.C, a.indptr, a.indices), N, out_dtype)
     out_bytes = 4 if out_dtype == "f32" else 2
     per_copy = a.data.nbytes + b.nbytes + M * N * out_bytes
@@ -130,20 +202,19 @@ def bench_spmm(torch, capi, W, a, b, out_dtype, steps, warmup, rotate=True):
     for _ in range(ncopy):
         dc = torch.empty((M, N), dtype=torch.float32 if out_dtype == "f32" else torch.int16, device="cuda")
         copies.append((da0.clone(), db0.clone(), dc))
+
     def launch(i, stream):
         da, db, dc = copies[i % ncopy]
         plan.run(da, db, dc, stream=stream)
 
-    t = Timer(torch, steps).run(launch, steps, warmup)
+    t = timer.run(launch, warmup)
     info = plan.info()
     plan.close()
     del copies
-    flops = W.spmm_flops(a.nblocks, a.R, a.C, N)
-    nbytes = W.spmm_bytes(a, N, out_bytes)
-    return t, flops, nbytes, info, ncopy
+    return t, W.spmm_flops(a.nblocks, a.R, a.C, N), W.spmm_bytes(a, N, out_bytes), info, ncopy
 
 
-def bench_sddmm(torch, capi, W, mask, x, y, y_layout, out_dtype, steps, warmup):
+def bench_sddmm(torch, capi, W, mask, x, y, y_layout, out_dtype, timer, warmup):
     K = x.shape[1]
     plan = capi.SddmmPlan(capi.Bsr(mask.H, mask.W, mask.R, mask.C, mask.indptr, mask.indices), K,
                           y_layout, out_dtype)
@@ -162,18 +233,16 @@ def bench_sddmm(torch, capi, W, mask, x, y, y_layout, out_dtype, steps, warmup):
         dm, dx, dy, do = copies[i % ncopy]
         plan.run(dm, dx, dy, do, ldy=ldy, stream=stream)
 
-    t = Timer(torch, steps).run(launch, steps, warmup)
+    t = timer.run(launch, warmup)
+    info = plan.info()
     plan.close()
     del copies
-    flops = W.sddmm_flops(mask.nblocks, mask.R, mask.C, K)
-    nbytes = W.sddmm_bytes(mask, K, out_bytes)
-    return t, flops, nbytes
+    return t, W.sddmm_flops(mask.nblocks, mask.R, mask.C, K), W.sddmm_bytes(mask, K, out_bytes), info
 
 
-def bench_attention(torch, capi, W, w, out_dtype, steps, warmup):
-    """Times the fused pair (bsp_attention) on the attention workload; bytes
-    are Q, K, V, the mask values, the index arrays and O (S never leaves the
-    chip)."""
+def bench_attention(torch, capi, W, w, out_dtype, timer, warmup):
+    """The fused pair (bsp_attention); bytes are Q, K, V, the mask values, the
+    index arrays and O (S never leaves the chip)."""
     m, q, k, v, d = w["mask"], w["q"], w["k"], w["v"], w["d"]
     plan = capi.AttentionPlan(capi.Bsr(m.H, m.W, m.R, m.C, m.indptr, m.indices), d, out_dtype)
     out_bytes = 4 if out_dtype == "f32" else 2
@@ -189,19 +258,19 @@ def bench_attention(torch, capi, W, w, out_dtype, steps, warmup):
         dm, dq, dk, dv, do = copies[i % ncopy]
         plan.run(dm, dq, dk, dv, do, stream=stream)
 
-    t = Timer(torch, steps).run(launch, steps, warmup)
+    t = timer.run(launch, warmup)
+    info = plan.info()
     plan.close()
     del copies
     flops = W.sddmm_flops(m.nblocks, m.R, m.C, d) + W.spmm_flops(m.nblocks, m.R, m.C, d)
     nbytes = (float(m.data.nbytes + q.nbytes + k.nbytes + v.nbytes) + 4.0 * (m.nblocks + m.nbrows + 1)
               + float(m.H) * d * out_bytes)
-    return t, flops, nbytes
+    return t, flops, nbytes, info
 
 
-def bench_spgemm(torch, capi, W, a, b, out_dtype, steps, warmup):
-    """Times the SpGEMM numeric phase on (a, b); FLOPs are 2*R*C*BC per
-    (A block, B block) pair, bytes are A's and B's values and index arrays
-    plus C's values."""
+def bench_spgemm(torch, capi, W, a, b, out_dtype, timer, warmup):
+    """The SpGEMM numeric phase on (a, b); FLOPs are 2*R*C*BC per (A block,
+    B block) pair, bytes are A's and B's values and index arrays plus C's."""
     plan = capi.SpgemmPlan(capi.Bsr(a.H, a.W, a.R, a.C, a.indptr, a.indices),
                            capi.Bsr(b.H, b.W, b.R, b.C, b.indptr, b.indices), out_dtype)
     out_bytes = 4 if out_dtype == "f32" else 2
@@ -218,7 +287,7 @@ def bench_spgemm(torch, capi, W, a, b, out_dtype, steps, warmup):
         da, db, do = copies[i % ncopy]
         plan.run(da, db, do, stream=stream)
 
-    t = Timer(torch, steps).run(launch, steps, warmup)
+    t = timer.run(launch, warmup)
     info = plan.info()
     nblocks = plan.structure.nblocks
     plan.close()
@@ -234,56 +303,210 @@ def bench_spgemm(torch, capi, W, a, b, out_dtype, steps, warmup):
     return t, flops, nbytes, info, {"pairs": pairs, "out_blocks": nblocks}
 
 
-def summarize(t, flops, nbytes, steps):
-    """Per-launch figures from the graph replay (us, TFLOP/s, GB/s and the
-    fractions of peak) plus the eager per-launch event figure."""
-    k_s = t["launch_ms"] * 1e-3
-    return {
-        "us_per_launch": round(t["launch_ms"] * 1e3, 3),
-        "eager_event_us": round(t["kernel_ms_mean"] * 1e3, 3),
-        "tflops": round(flops / k_s / 1e12, 3),
-        "frac_mfma_peak": round(flops / k_s / 1e12 / PEAK_BF16_TFLOPS, 4),
-        "gbs": round(nbytes / k_s / 1e9, 1),
-        "frac_hbm_peak": round(nbytes / k_s / 1e9 / PEAK_HBM_GBS, 4),
-        "flops": flops,
-        "bytes": nbytes,
-    }
+def traffic_key_spmm(a, N, out_dtype):
+    return f"spmm {a.H}x{a.W} r{a.R}c{a.C} nnzb{a.nblocks} N{N} {out_dtype}"
 
 
-def kernel_name(tile_n, stages):
-    return f"bsp::spmm_kernel<{tile_n // 128}, {stages}, false>"
+# ---------------------------------------------------------------------------
+# CPU baseline (the oracle on this host)
+def host_cores():
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    return max(1, min(cores, int(os.environ.get("OMP_NUM_THREADS", cores))))
 
 
-TRAFFIC_FILE = REPO / "profiles" / "spmm_kernel_d25_4096x4096_N512_traffic.md"
+def _median_time(fn, reps=3):
+    fn()  # warm-up
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
 
 
-def measured_traffic(kernel):
-    """HBM-side bytes per launch of the headline kernel: FETCH_SIZE x 2.0 +
-    WRITE_SIZE x 1.0 (factors from kernels of known traffic), from the
-    committed counter summary, or None when that summary is for another
-    kernel."""
-    try:
-        text = TRAFFIC_FILE.read_text()
-    except OSError:
-        return None
-    kv = dict(line.split(": ", 1) for line in text.splitlines() if line.startswith("traffic_"))
-    if kv.get("traffic_kernel") != kernel:
-        return None
-    return int(kv["traffic_bytes_per_launch"])
+def _row_prefix(indptr, flops_per_block, budget):
+    """Block rows 0..r-1 whose blocks cost at most `budget` FLOPs (at least one row)."""
+    cum = np.cumsum(np.diff(indptr).astype(np.float64) * flops_per_block)
+    return max(1, int(np.searchsorted(cum, budget, side="right")))
 
 
-def roofline(flops, nbytes, k_s, row):
+SINGLE_BUDGET = 4e8   # FLOPs of the one-thread sample (about half a second)
+ALL_BUDGET = 1.6e10   # the all-core leg times the whole workload up to this
+
+
+def cpu_spmm(orc, W, a, b, cores, gpu_tflops, single_budget=SINGLE_BUDGET):
+    N = b.shape[1]
+    fpb = 2.0 * a.R * a.C * N
+    rec = {}
+    for leg, threads, budget in (("single", 1, single_budget), ("all", cores, ALL_BUDGET)):
+        r = _row_prefix(a.indptr, fpb, budget)
+        r = min(r, a.nbrows)
+        nb = int(a.indptr[r])
+        ip = np.ascontiguousarray(a.indptr[: r + 1])
+        t = _median_time(lambda: orc.spmm(ip, a.indices[:nb], a.data[: nb * a.R * a.C], r * a.R, a.W, a.R, a.C, b,
+                                          threads=threads))
+        tf = W.spmm_flops(nb, a.R, a.C, N) / t / 1e12
+        rec[leg] = {"tflops": round(tf, 6), "cores": threads, "seconds": round(t, 4),
+                    "sample": "whole workload" if r == a.nbrows else
+                    f"block rows 0..{r - 1} ({nb} of {a.nblocks} blocks)",
+                    "gpu_speedup": round(gpu_tflops / tf, 1) if gpu_tflops and tf > 0 else None}
+    rec["kind"] = "port"
+    return rec
+
+
+def cpu_sddmm(orc, W, m, x, y, cores, gpu_tflops, y_colmajor=False):
+    K = x.shape[1]
+    fpb = 2.0 * m.R * m.C * K + m.R * m.C
+    rec = {}
+    for leg, threads, budget in (("single", 1, SINGLE_BUDGET), ("all", cores, ALL_BUDGET)):
+        r = min(_row_prefix(m.indptr, fpb, budget), m.nbrows)
+        nb = int(m.indptr[r])
+        ip = np.ascontiguousarray(m.indptr[: r + 1])
+        xs = np.ascontiguousarray(x[: r * m.R])
+        t = _median_time(lambda: orc.sddmm(ip, m.indices[:nb], m.data[: nb * m.R * m.C], r * m.R, m.W, m.R, m.C, xs,
+                                           y, y_colmajor=y_colmajor, threads=threads))
+        tf = W.sddmm_flops(nb, m.R, m.C, K) / t / 1e12
+        rec[leg] = {"tflops": round(tf, 6), "cores": threads, "seconds": round(t, 4),
+                    "sample": "whole workload" if r == m.nbrows else
+                    f"block rows 0..{r - 1} ({nb} of {m.nblocks} blocks)",
+                    "gpu_speedup": round(gpu_tflops / tf, 1) if gpu_tflops and tf > 0 else None}
+    rec["kind"] = "port"
+    return rec
+
+
+def cpu_pair(orc, W, w, cores, gpu_tflops):
+    """The attention pair on the oracle: SDDMM (K as column-major Y) then SpMM."""
+    m, d = w["mask"], w["d"]
+    fpb = 2.0 * m.R * m.C * d * 2 + m.R * m.C
+    rec = {}
+    for leg, threads, budget in (("single", 1, SINGLE_BUDGET), ("all", cores, ALL_BUDGET)):
+        r = min(_row_prefix(m.indptr, fpb, budget), m.nbrows)
+        nb = int(m.indptr[r])
+        ip = np.ascontiguousarray(m.indptr[: r + 1])
+        qs = np.ascontiguousarray(w["q"][: r * m.R])
+
+        def pair():
+            orc.sddmm(ip, m.indices[:nb], m.data[: nb * 1024], r * m.R, m.W, m.R, m.C, qs, w["k"], y_colmajor=True,
+                      threads=threads)
+            orc.spmm(ip, m.indices[:nb], m.data[: nb * 1024], r * m.R, m.W, m.R, m.C, w["v"], threads=threads)
+        t = _median_time(pair)
+        tf = (W.sddmm_flops(nb, m.R, m.C, d) + W.spmm_flops(nb, m.R, m.C, d)) / t / 1e12
+        rec[leg] = {"tflops": round(tf, 6), "cores": threads, "seconds": round(t, 4),
+                    "sample": "whole pair (SDDMM then SpMM)" if r == m.nbrows else
+                    f"block rows 0..{r - 1} ({nb} of {m.nblocks} blocks), SDDMM then SpMM",
+                    "gpu_speedup": round(gpu_tflops / tf, 1) if gpu_tflops and tf > 0 else None}
+    rec["kind"] = "port"
+    return rec
+
+
+def cpu_spgemm(orc, W, a, b, gpu_tflops):
+    """The SpGEMM golden (single-threaded, as the reference's bsr_matrix::spgemm)."""
+    rows = 32
+    nb = int(a.indptr[rows])
+    bcount = np.diff(b.indptr).astype(np.int64)
+    pairs = int(bcount[a.indices[:nb]].sum())
+    t = _median_time(lambda: orc.spgemm(a.indptr[: rows + 1], a.indices[:nb], a.data[: nb * a.R * a.C], rows * a.R,
+                                        a.R, a.C, b.indptr, b.indices, b.data, b.W, b.C))
+    tf = 2.0 * pairs * a.R * a.C * b.C / t / 1e12
+    single = {"tflops": round(tf, 6), "cores": 1, "seconds": round(t, 4),
+              "sample": f"block rows 0..{rows - 1} of A ({nb} blocks, {pairs} block products)",
+              "gpu_speedup": round(gpu_tflops / tf, 1) if gpu_tflops else None}
+    return {"single": single, "all": dict(single, note="the SpGEMM golden has no threaded form"), "kind": "port"}
+
+
+def cpu_large(orc, W, a, b, cores, gpu_tflops):
+    """256x256 blocks: per-block work is large; the sample is the first
+    block rows (one per thread) against the first 64 columns of B."""
+    ncols = 64
+    bs = np.ascontiguousarray(b[:, :ncols])
+    rec = {}
+    for leg, threads in (("single", 1), ("all", cores)):
+        rows = min(a.nbrows, threads)
+        nb = int(a.indptr[rows])
+        t = _median_time(lambda: orc.spmm(a.indptr[: rows + 1], a.indices[:nb], a.data[: nb * a.R * a.C], rows * a.R,
+                                          a.W, a.R, a.C, bs, threads=threads))
+        tf = W.spmm_flops(nb, a.R, a.C, ncols) / t / 1e12
+        rec[leg] = {"tflops": round(tf, 6), "cores": threads, "seconds": round(t, 4),
+                    "sample": f"block rows 0..{rows - 1} ({nb} of {a.nblocks} blocks) times the first {ncols} "
+                              "columns of B",
+                    "gpu_speedup": round(gpu_tflops / tf, 1) if gpu_tflops and tf > 0 else None}
+    rec["kind"] = "port"
+    return rec
+
+
+# ---------------------------------------------------------------------------
+# On-chip roof of the 32x32 SpMM: the kernel's L2 -> LDS volume at the
+# measured rate of an L2-resident DMA stream, plus the fixed cost of a launch.
+def probe_lib():
+    lib = ctypes.CDLL(str(REPO / "tenstorrent-wh-blockspmm_amd" / "libbsp_probe.so"))
+    lib.bsp_probe_dma_stream.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_void_p]
+    lib.bsp_probe_empty.argtypes = [ctypes.c_int, ctypes.c_void_p]
+    return lib
+
+
+def measure_roofs(torch, steps=50):
+    """TB/s of an L2-resident DMA stream (2 MB region, 256 workgroups x 8
+    waves, 16 loads of 1 KB in flight per wave) and an HBM one (1 GB), and the
+    graph-replay time of an empty 512-workgroup kernel."""
+    lib = probe_lib()
+    buf = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    buf.fill_(1)
+    st = torch.cuda.current_stream()
+    iters = 256
+
+    def graph_us(fn):
+        for _ in range(3):
+            fn(st.cuda_stream)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream()
+        cap.wait_stream(st)
+        with torch.cuda.graph(g, stream=cap):
+            for _ in range(steps):
+                fn(torch.cuda.current_stream().cuda_stream)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / steps
+
+    out = {}
+    for name, region in (("l2_stream_tbs", 2 << 20), ("hbm_stream_tbs", 1 << 30)):
+        us = graph_us(lambda s: lib.bsp_probe_dma_stream(buf.data_ptr(), region, 256, 8, iters, s))
+        out[name] = round(256 * 8 * iters * 1024 / (us * 1e-6) / 1e12, 2)
+    out["empty_launch_us"] = round(graph_us(lambda s: lib.bsp_probe_empty(512, s)), 3)
+    del buf
+    return out
+
+
+def on_chip_roof(info, us, roofs):
+    """L2 -> LDS bytes of a 32x32 SpMM launch (every entry brings its 2 KB A
+    sub-block and the 32 x tile slice of B into LDS) against the measured
+    L2-resident stream rate, plus the launch's fixed cost."""
+    vol = float(info["n_entries"]) * (2048 + 64 * info["tile_n"])
+    stream_us = vol / (roofs["l2_stream_tbs"] * 1e12) * 1e6
+    floor = stream_us + roofs["empty_launch_us"]
+    return {"l2_to_lds_bytes": vol, "l2_stream_tbs": roofs["l2_stream_tbs"],
+            "empty_launch_us": roofs["empty_launch_us"], "floor_us": round(floor, 3),
+            "frac": round(floor / us, 4),
+            "note": "floor = L2->LDS volume at the L2-resident DMA rate + an empty launch; frac = floor / us_per_launch"}
+
+
+# ---------------------------------------------------------------------------
+def roofline(flops, nbytes, us, traffic_bytes, kernel):
     """The bound is the lower roof for the kernel's algorithmic intensity:
     MFMA when FLOP/byte >= peak FLOP/s / peak bytes/s (312.5), else HBM."""
+    k_s = us * 1e-6
     ai = flops / nbytes
     ridge = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
     tflops = flops / k_s / 1e12
     gbs = nbytes / k_s / 1e9
-    kernel = kernel_name(row["tile_n"], row["stages"])
-    r = {"kernel": kernel, "us_per_launch": row["us_per_launch"],
-         "algorithmic_flop_per_launch": flops, "algorithmic_bytes_per_launch": nbytes,
-         "intensity_flop_per_byte": round(ai, 1), "traffic": measured_traffic(kernel),
-         "traffic_source": TRAFFIC_FILE.name,
+    r = {"kernel": kernel, "us_per_launch": round(us, 3), "algorithmic_flop_per_launch": flops,
+         "algorithmic_bytes_per_launch": nbytes, "intensity_flop_per_byte": round(ai, 1), "traffic": traffic_bytes,
          "mfma_tflops": round(tflops, 3), "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 4),
          "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)}
     if ai >= ridge:
@@ -295,118 +518,32 @@ def roofline(flops, nbytes, k_s, row):
     return r
 
 
-def cpu_baseline(W, orc):
-    """The oracle on this host: all cores on the whole 25% workload (median of
-    3 after one warm-up), one core on a 32-block-row sample."""
-    w = W.workload_spmm_sweep(0.25)
-    a, b = w["a"], w["b"]
-    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
-    cores = max(1, min(cores, int(os.environ.get("OMP_NUM_THREADS", cores))))
-
-    def timed(fn, reps=3):
-        fn()
-        ts = []
-        for _ in range(reps):
-            t0 = time.perf_counter()
-            fn()
-            ts.append(time.perf_counter() - t0)
-        return float(np.median(ts))
-
-    flops = W.spmm_flops(a.nblocks, 32, 32, 512)
-    t_all = timed(lambda: orc.spmm(a.indptr, a.indices, a.data, a.H, a.W, 32, 32, b, threads=cores))
-    rows = 32
-    nb = int(a.indptr[rows])
-    ip = np.ascontiguousarray(a.indptr[:rows + 1])
-    t_one = timed(lambda: orc.spmm(ip, a.indices[:nb], a.data[:nb * 1024], rows * 32, a.W, 32, 32, b,
-                                   threads=1), reps=1)
-    flops_one = W.spmm_flops(nb, 32, 32, 512)
-    return {
-        "value": round(flops / t_all / 1e12, 6),
-        "unit": "TFLOP/s",
-        "cores": cores,
-        "kind": "port",
-        "sample": f"whole 25% workload ({a.nblocks} blocks, N=512), fp32 out, OpenMP over block rows; "
-                  f"median of 3 runs after 1 warm-up: {t_all:.3f} s",
-        "single_core": {"value": round(flops_one / t_one / 1e12, 6), "cores": 1,
-                        "sample": f"block rows 0..{rows - 1} ({nb} blocks), N=512: {t_one:.3f} s"},
-    }
+PATTERNS = ("row", "col", "multi_diag", "random")
 
 
-def cpu_per_config(W, orc, out, cores):
-    """The oracle on this host beside each GPU figure: all `cores` threads
-    (the SpGEMM golden is single-threaded), each workload whole or, where
-    that would take more than a few seconds, a named sample of its block
-    rows.  Adds a "cpu" record (TFLOP/s, seconds, sample, GPU speedup) to
-    each section of `out`."""
-    def rate(fn, flops):
-        t0 = time.perf_counter()
-        fn()
-        t = time.perf_counter() - t0
-        return flops / t / 1e12, t
+def pattern_workload(W, pattern, density):
+    """A of 8192^2 in 256x256 blocks in one of the reference's pattern
+    families (block_spmm/inc/profiling_suite.hpp:3513-3574): the first
+    round(density * 1024) positions of FILL_ROW / FILL_COL / FILL_MULTI_DIAG,
+    or uniform-random ones; tril and triu are the full triangles.  Values
+    U[-1, 1] bf16."""
+    n, R = 8192, 256
+    nbr = n // R
+    rng = W.Rng(W.SEED_BASE + 7)
+    if pattern in ("tril", "triu"):
+        a = (W.fill_tril if pattern == "tril" else W.fill_triu)(n, n, R, R)
+    elif pattern == "random":
+        a = W.random_positions(n, n, R, R, int(round(density * nbr * nbr)), rng)
+    else:
+        fill = {"row": W.fill_row, "col": W.fill_col, "multi_diag": W.fill_multi_diag}[pattern]
+        a = fill(n, n, R, R, int(round(density * nbr * nbr)))
+    a.data = W.bf16_from_f32(W.uniform_f32(rng, a.nblocks * R * R))
+    return a
 
-    def record(tf, t, sample, gpu_tflops, threads=cores):
-        return {"tflops": round(tf, 6), "cores": threads, "kind": "port", "seconds": round(t, 3),
-                "sample": sample, "gpu_speedup": round(gpu_tflops / tf, 1) if gpu_tflops else None}
 
-    if "sweep" in out:
-        for d in W.SPMM_SWEEP_DENSITIES:
-            rows = [r for r in out["sweep"] if r["density"] == d and not r.get("warm_cache")]
-            if not rows:
-                continue
-            w = W.workload_spmm_sweep(d)
-            a = w["a"]
-            tf, t = rate(lambda: orc.spmm(a.indptr, a.indices, a.data, a.H, a.W, 32, 32, w["b"], threads=cores),
-                         W.spmm_flops(a.nblocks, 32, 32, w["b"].shape[1]))
-            for r in rows:
-                r["cpu"] = record(tf, t, "whole workload", r["tflops"])
-    if "sddmm" in out:
-        s = W.workload_sddmm()
-        m = s["mask"]
-        tf, t = rate(lambda: orc.sddmm(m.indptr, m.indices, m.data, m.H, m.W, 32, 32, s["x"], s["y"],
-                                       threads=cores),
-                     W.sddmm_flops(m.nblocks, 32, 32, s["x"].shape[1]))
-        out["sddmm"]["cpu"] = record(tf, t, "whole workload", out["sddmm"]["tflops"])
-    if "skewed" in out:
-        w = W.workload_spmm_skewed()
-        a = w["a"]
-        tf, t = rate(lambda: orc.spmm(a.indptr, a.indices, a.data, a.H, a.W, 32, 32, w["b"], threads=cores),
-                     W.spmm_flops(a.nblocks, 32, 32, w["b"].shape[1]))
-        out["skewed"]["cpu"] = record(tf, t, "whole workload", out["skewed"]["tflops"])
-    if "attention" in out:
-        w = W.workload_attention()
-        m = w["mask"]
-        d = w["d"]
-
-        def pair():
-            orc.sddmm(m.indptr, m.indices, m.data, m.H, m.W, 32, 32, w["q"], w["k"], y_colmajor=True, threads=cores)
-            orc.spmm(m.indptr, m.indices, m.data, m.H, m.W, 32, 32, w["v"], threads=cores)
-        tf, t = rate(pair, W.sddmm_flops(m.nblocks, 32, 32, d) + W.spmm_flops(m.nblocks, 32, 32, d))
-        out["attention"]["cpu"] = record(tf, t, "whole pair (SDDMM then SpMM)", out["attention"]["fused"]["tflops"])
-    if "spgemm" in out:
-        w = W.workload_spgemm()
-        a, b = w["a"], w["b"]
-        rows = 32
-        nb = int(a.indptr[rows])
-        bcount = np.diff(b.indptr).astype(np.int64)
-        pairs = int(bcount[a.indices[:nb]].sum())
-        tf, t = rate(lambda: orc.spgemm(a.indptr[:rows + 1], a.indices[:nb], a.data[:nb * a.R * a.C], rows * a.R,
-                                        a.R, a.C, b.indptr, b.indices, b.data, b.W, b.C),
-                     2.0 * pairs * a.R * a.C * b.C)
-        gpu = next(r["tflops"] for r in out["spgemm"]["runs"] if r["out"] == "f32")
-        out["spgemm"]["cpu"] = record(tf, t, f"block rows 0..{rows - 1} of A ({nb} blocks, {pairs} block products)",
-                                      gpu, threads=1)
-    if "large_blocks" in out:
-        w = W.workload_spmm_large_blocks(0.25)
-        a = w["a"]
-        rows, ncols = min(a.nbrows, cores), 64  # one block row per thread
-        nb = int(a.indptr[rows])
-        bs = np.ascontiguousarray(w["b"][:, :ncols])
-        tf, t = rate(lambda: orc.spmm(a.indptr[:rows + 1], a.indices[:nb], a.data[:nb * a.R * a.C], rows * a.R, a.W,
-                                      a.R, a.C, bs, threads=cores),
-                     W.spmm_flops(nb, a.R, a.C, ncols))
-        gpu = next(r["tflops"] for r in out["large_blocks"]["runs"] if r["out"] == "f32")
-        out["large_blocks"]["cpu"] = record(
-            tf, t, f"block rows 0..{rows - 1} ({nb} of {a.nblocks} blocks) times the first {ncols} columns of B", gpu)
+def pattern_b(W):
+    """B of the pattern sweep: 8192 x 8192 bf16 U[-1, 1]."""
+    return W.bf16_from_f32(W.uniform_f32(W.Rng(W.SEED_BASE + 8), (8192, 8192)))
 
 
 def main():
@@ -425,7 +562,16 @@ def main():
     capi, W = pkg.capi, pkg.workloads
     capi.load()
     only = set(filter(None, args.only.split(",")))
+
+    def run(section):
+        if only and section not in only:
+            return False
+        print(f"[bench] {section}", file=sys.stderr, flush=True)  # progress, one line per section
+        return True
     steps, warmup = args.steps, args.warmup
+    timer = Timer(torch, steps, trace=not args.no_kernel_time)
+    orc = None if args.no_cpu else entry._load_oracle()
+    cores = host_cores()
     if args.copy_calibration:
         # Two kernels that each read 256 MiB and write 256 MiB: the runtime's
         # device-to-device copy and an elementwise multiply.
@@ -437,94 +583,158 @@ def main():
         del src, dst
 
     out = {}
-    sweep = []
     head = None
-    if not only or "sweep" in only or "head" in only:
+
+    def spmm_section(w, od, label, rotate=True, cpu=True):
+        t, fl, nb, info, ncopy = bench_spmm(torch, capi, W, w["a"], w["b"], od, timer, warmup, rotate=rotate)
+        rec = {"workload": label, "out": od, "nnzb": w["a"].nblocks, **summarize(t, fl, nb),
+               "plan": plan_summary(info), "copies": ncopy}
+        attach_traffic(rec, traffic_key_spmm(w["a"], w["b"].shape[1], od))
+        if cpu and orc is not None:
+            rec["cpu"] = cpu_spmm(orc, W, w["a"], w["b"], cores, rec["tflops"])
+        return rec, t, fl, nb, info
+
+    if run("c1"):
+        w = W.workload_spmm_small()
+        rec, *_ = spmm_section(w, "f32", "SpMM A 1024x1024, 32x32 blocks, 10% (102 blocks), B 1024x256, fp32 C")
+        rec["input_sha256"] = W.workload_digest(w)
+        out["c1"] = rec
+
+    if run("sweep") or run("head"):
         head_only = "head" in only and "sweep" not in only
+        sweep = []
         for d in W.SPMM_SWEEP_DENSITIES:
             if head_only and d != 0.25:
                 continue
             w = W.workload_spmm_sweep(d)
+            digest = W.workload_digest(w)
+            cpu_rec = None
             for od in ("f32", "bf16"):
                 if head_only and od != "f32":
                     continue
-                t, fl, nbytes, info, ncopy = bench_spmm(torch, capi, W, w["a"], w["b"], od, steps, warmup)
-                row = {"density": d, "out": od, "nnzb": w["a"].nblocks, **summarize(t, fl, nbytes, steps),
-                       "tile_n": info["tile_n"], "stages": info["stages"], "grid": info["grid"],
-                       "copies": ncopy}
-                sweep.append(row)
+                rec, t, fl, nb, info = spmm_section(
+                    w, od, f"SpMM A 4096x4096, 32x32 blocks, {int(d * 100)}%, B 4096x512, {od} C",
+                    cpu=cpu_rec is None)
+                if cpu_rec is None:
+                    cpu_rec = rec.get("cpu")
+                elif cpu_rec is not None:
+                    # the oracle's rate does not depend on the GPU's output type
+                    rec["cpu"] = {k: (dict(v, gpu_speedup=round(rec["tflops"] / v["tflops"], 1))
+                                      if isinstance(v, dict) else v) for k, v in cpu_rec.items()}
+                rec.update({"density": d, "input_sha256": digest})
+                sweep.append(rec)
                 if d == 0.25 and od == "f32":
-                    head = (t, fl, nbytes, row)
+                    head = (t, fl, nb, rec, info)
             if head_only:
                 continue
             # warm (cache-resident) figure for the same launch, for reference
-            t, fl, nbytes, info, _ = bench_spmm(torch, capi, W, w["a"], w["b"], "f32", steps, warmup,
-                                                rotate=False)
-            sweep.append({"density": d, "out": "f32", "warm_cache": True, **summarize(t, fl, nbytes, steps)})
+            t, fl, nb, info, _ = bench_spmm(torch, capi, W, w["a"], w["b"], "f32", timer, warmup, rotate=False)
+            sweep.append({"density": d, "out": "f32", "warm_cache": True, **summarize(t, fl, nb)})
         out["sweep"] = sweep
-    if not only or "sddmm" in only:
+
+    if run("sddmm"):
         s = W.workload_sddmm()
-        t, fl, nb = bench_sddmm(torch, capi, W, s["mask"], s["x"], s["y"], capi.ROW_MAJOR, "f32", steps, warmup)
-        out["sddmm"] = {"workload": "SDDMM mask 4096x4096 32x32 blocks d=10%, X 4096x256, Y 256x4096, fp32 out",
-                        "nnzb": s["mask"].nblocks, **summarize(t, fl, nb, steps)}
-    if not only or "skewed" in only:
+        m = s["mask"]
+        t, fl, nb, info = bench_sddmm(torch, capi, W, m, s["x"], s["y"], capi.ROW_MAJOR, "f32", timer, warmup)
+        rec = {"workload": "SDDMM mask 4096x4096 32x32 blocks d=10%, X 4096x256, Y 256x4096, fp32 out",
+               "nnzb": m.nblocks, **summarize(t, fl, nb), "plan": {"grid": info["grid"], "one_shot": info["stages"]},
+               "input_sha256": W.workload_digest(s)}
+        attach_traffic(rec, f"sddmm {m.H}x{m.W} r{m.R}c{m.C} nnzb{m.nblocks} K{s['K']} f32")
+        if orc is not None:
+            rec["cpu"] = cpu_sddmm(orc, W, m, s["x"], s["y"], cores, rec["tflops"])
+        out["sddmm"] = rec
+
+    if run("skewed"):
         w = W.workload_spmm_skewed()
-        t, fl, nb, info, _ = bench_spmm(torch, capi, W, w["a"], w["b"], "f32", steps, warmup)
-        out["skewed"] = {"workload": "SpMM A 16384x16384 Zipf(1.2) rows, 2% mean density, B 16384x1024, fp32 out",
-                         "nnzb": w["a"].nblocks, "split_rows": info["n_split_rows"],
-                         **summarize(t, fl, nb, steps)}
-    if not only or "attention" in only:
+        rec, *_ = spmm_section(w, "f32", "SpMM A 16384x16384 Zipf(1.2) rows, 2% mean density, B 16384x1024, fp32 C")
+        rec["input_sha256"] = W.workload_digest(w)
+        rec["max_row_blocks"] = int(np.diff(w["a"].indptr).max())
+        out["skewed"] = rec
+
+    if run("attention"):
         w = W.workload_attention()
         m = w["mask"]
-        t1, f1, b1 = bench_sddmm(torch, capi, W, m, w["q"], w["k"], capi.COL_MAJOR, "bf16", steps, warmup)
+        t1, f1, b1, _ = bench_sddmm(torch, capi, W, m, w["q"], w["k"], capi.COL_MAJOR, "bf16", timer, warmup)
         a = W.BsrArrays(m.H, m.W, 32, 32, m.indptr, m.indices, m.data)
-        t2, f2, b2, _, _ = bench_spmm(torch, capi, W, a, w["v"], "f32", steps, warmup)
-        t3, f3, b3 = bench_attention(torch, capi, W, w, "f32", steps, warmup)
-        out["attention"] = {"workload": "seq 8192, d 128, 8 causal block bands + 1% global; S=mask(.)QK^T "
-                                        "(bf16) then O=S*V (fp32)",
-                            "nnzb": m.nblocks, "sddmm": summarize(t1, f1, b1, steps),
-                            "spmm": summarize(t2, f2, b2, steps),
-                            "pair_tflops": round((f1 + f2) / ((t1["launch_ms"] + t2["launch_ms"]) * 1e-3)
-                                                 / 1e12, 3),
-                            "fused": summarize(t3, f3, b3, steps)}
+        t2, f2, b2, info2, _ = bench_spmm(torch, capi, W, a, w["v"], "f32", timer, warmup)
+        t3, f3, b3, _ = bench_attention(torch, capi, W, w, "f32", timer, warmup)
+        fused = summarize(t3, f3, b3)
+        attach_traffic(fused, f"attention seq{m.H} d{w['d']} nnzb{m.nblocks} f32")
+        rec = {"workload": "seq 8192, d 128, 8 causal block bands + 1% global; S=mask(.)QK^T (bf16) then "
+                           "O=S*V (fp32)",
+               "nnzb": m.nblocks, "input_sha256": W.workload_digest(w), "sddmm": summarize(t1, f1, b1),
+               "spmm": {**summarize(t2, f2, b2), "plan": plan_summary(info2)},
+               "pair_tflops": round((f1 + f2) / ((t1["launch_ms"] + t2["launch_ms"]) * 1e-3) / 1e12, 3),
+               "fused": fused}
+        if orc is not None:
+            rec["cpu"] = cpu_pair(orc, W, w, cores, fused["tflops"])
+        out["attention"] = rec
 
-    if not only or "spgemm" in only:
+    if run("spgemm"):
         w = W.workload_spgemm()
         rows = []
         for od in ("f32", "bf16"):
-            t, fl, nb, info, extra = bench_spgemm(torch, capi, W, w["a"], w["b"], od, steps, warmup)
-            rows.append({"out": od, **summarize(t, fl, nb, steps), "grid": info["grid"],
-                         "sub_blocks": info["n_items"], "products": info["n_entries"], **extra})
-        out["spgemm"] = {"workload": "SpGEMM C=A*B, A and B 8192x8192, 32x32 blocks, 5% each (3277 blocks)",
-                         "nnzb": w["a"].nblocks, "runs": rows}
+            t, fl, nb, info, extra = bench_spgemm(torch, capi, W, w["a"], w["b"], od, timer, warmup)
+            rows.append({"out": od, **summarize(t, fl, nb), "grid": info["grid"], "sub_blocks": info["n_items"],
+                         "products": info["n_entries"], **extra})
+        rec = {"workload": "SpGEMM C=A*B, A and B 8192x8192, 32x32 blocks, 5% each (3277 blocks)",
+               "nnzb": w["a"].nblocks, "input_sha256": W.workload_digest(w), "runs": rows}
+        if orc is not None:
+            rec["cpu"] = cpu_spgemm(orc, W, w["a"], w["b"], rows[0]["tflops"])
+        out["spgemm"] = rec
         del w
 
-    if not only or "large" in only:
+    if run("large"):
         # The reference's own published configuration: M = N = K = 8192 with
-        # 256 x 256 blocks at 25% (its best: 50.6 TFLOP/s on a Wormhole N150).
+        # 256 x 256 blocks at 25% (its best: 50.6 TFLOP/s on a Wormhole N150,
+        # block_spmm/scripts/experiments_dram_reads_table.tex:27-30).
         w = W.workload_spmm_large_blocks(0.25)
+        lt = Timer(torch, max(10, steps // 10), trace=timer.trace)
         rows = []
         for od in ("bf16", "f32"):
-            t, fl, nb, info, _ = bench_spmm(torch, capi, W, w["a"], w["b"], od, max(10, steps // 10),
-                                            max(10, warmup // 2))
-            rows.append({"out": od, **summarize(t, fl, nb, steps), "tile_n": info["tile_n"],
-                         "grid": info["grid"]})
-        out["large_blocks"] = {"workload": "SpMM 8192^3, 256x256 blocks, 25% (256 blocks)",
-                               "nnzb": w["a"].nblocks, "runs": rows}
+            t, fl, nb, info, _ = bench_spmm(torch, capi, W, w["a"], w["b"], od, lt, max(5, warmup // 2))
+            r = {"out": od, **summarize(t, fl, nb), "plan": plan_summary(info)}
+            attach_traffic(r, traffic_key_spmm(w["a"], 8192, od))
+            rows.append(r)
+        rec = {"workload": "SpMM 8192^3, 256x256 blocks, 25% (256 blocks)", "nnzb": w["a"].nblocks,
+               "input_sha256": W.workload_digest(w), "runs": rows}
+        if orc is not None:
+            rec["cpu"] = cpu_large(orc, W, w["a"], w["b"], cores, rows[-1]["tflops"])
+        out["large_blocks"] = rec
         del w
-        # The same shape with the reference's other block sizes (R = C = 128
-        # and 64), fp32 C.
         rows = []
         for R in (128, 64):
             w = W.workload_spmm_large_blocks(0.25, R=R)
-            t, fl, nb, info, _ = bench_spmm(torch, capi, W, w["a"], w["b"], "f32", max(10, steps // 10),
-                                            max(10, warmup // 2))
-            rows.append({"R": R, "C": R, "nnzb": w["a"].nblocks, "out": "f32", **summarize(t, fl, nb, steps),
-                         "group": info["group"], "tile_n": info["tile_n"], "grid": info["grid"]})
+            t, fl, nb, info, _ = bench_spmm(torch, capi, W, w["a"], w["b"], "f32", lt, max(5, warmup // 2))
+            rows.append({"R": R, "C": R, "nnzb": w["a"].nblocks, "out": "f32", **summarize(t, fl, nb),
+                         "plan": plan_summary(info)})
             del w
         out["block_sizes"] = {"workload": "SpMM 8192^3, R x R blocks, 25%, fp32 C", "runs": rows}
 
-    if not only or "host" in only:
+    if run("patterns"):
+        # The reference's pattern sweep (Row, Col, Multi-diag, Random at 5% and
+        # 50%; full tril and triu) at 8192^3 with 256x256 blocks, bf16 C (its
+        # output type); its published DDA figures are in the records.
+        published = {("row", 0.05): 11.5, ("random", 0.05): 28.0, ("multi_diag", 0.05): 25.0, ("col", 0.05): 25.7,
+                     ("row", 0.5): 49.2, ("random", 0.5): 48.0, ("multi_diag", 0.5): 47.6, ("col", 0.5): 47.0,
+                     ("tril", 1.0): 43.3, ("triu", 1.0): 29.6}
+        lt = Timer(torch, max(10, steps // 10), trace=timer.trace)
+        rows = []
+        b = pattern_b(W)
+        for pat, d in [(p, d) for d in (0.05, 0.5) for p in PATTERNS] + [("tril", 1.0), ("triu", 1.0)]:
+            a = pattern_workload(W, pat, d)
+            t, fl, nb, info, _ = bench_spmm(torch, capi, W, a, b, "bf16", lt, max(5, warmup // 2))
+            r = {"pattern": pat, "density": d if pat not in ("tril", "triu") else round(a.nblocks / 1024, 4),
+                 "nnzb": a.nblocks, "out": "bf16", **summarize(t, fl, nb), "plan": plan_summary(info),
+                 "reference_dda_tflops_n150": published.get((pat, d))}
+            attach_traffic(r, traffic_key_spmm(a, 8192, "bf16") + f" {pat}")
+            rows.append(r)
+            del a
+        del b
+        out["patterns"] = {"workload": "SpMM 8192^3, 256x256 blocks, the reference's pattern families, bf16 C",
+                           "runs": rows}
+
+    if run("host"):
         # The blocking host-buffer entry point (the reference operator's shape):
         # plan, device allocation, PCIe upload of A and B, launch, download of
         # C, synchronise, free.  Reported beside `value`, never as it.
@@ -540,23 +750,31 @@ def main():
         t_host = float(np.median(ts))
         fl = W.spmm_flops(a.nblocks, 32, 32, 512)
         out["host_entry"] = {"workload": "25% SpMM through bsp_host_spmm (host buffers, blocking)",
-                             "ms_per_call": round(t_host * 1e3, 3),
-                             "tflops": round(fl / t_host / 1e12, 4)}
-
-    cpu = None
-    if not args.no_cpu:
-        orc = entry._load_oracle()
-        cpu = cpu_baseline(W, orc)
-        cpu_per_config(W, orc, out, cpu["cores"])
+                             "ms_per_call": round(t_host * 1e3, 3), "tflops": round(fl / t_host / 1e12, 4)}
 
     if head is None:
         print(json.dumps(out))
         return
-    t, fl, nbytes, row = head
-    k_s = t["launch_ms"] * 1e-3
+    t, fl, nbytes, row, info = head
+    us = t["launch_ms"] * 1e3
+    roofs = measure_roofs(torch)
+    tr = row.get("traffic", {}).get("bytes_per_launch")
+    rl = roofline(fl, nbytes, us, tr, next(iter(row.get("kernels", {})), None) if row.get("kernels") else None)
+    rl["on_chip"] = on_chip_roof(info, us, roofs)
+    rl["hbm_stream_tbs"] = roofs["hbm_stream_tbs"]
+    if row.get("kernel_us"):
+        rl["kernel_us"] = row["kernel_us"]
+    cpu = None
+    if "cpu" in row:
+        c = row["cpu"]
+        cpu = {"value": c["all"]["tflops"], "unit": "TFLOP/s", "cores": c["all"]["cores"], "kind": "port",
+               "sample": f"{c['all']['sample']} of the 25% workload, OpenMP over block rows; median of 3 runs "
+                         f"after 1 warm-up: {c['all']['seconds']} s",
+               "single_core": {"value": c["single"]["tflops"], "cores": 1,
+                               "sample": f"{c['single']['sample']}: {c['single']['seconds']} s"}}
     result = {
         "metric": "effective TFLOP/s on nonzero blocks (SpMM, SDDMM); % bf16 MFMA peak / % HBM BW",
-        "value": round(fl / k_s / 1e12, 3),
+        "value": round(fl / (us * 1e-6) / 1e12, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": steps,
@@ -566,13 +784,14 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded uniform-random block positions, U[-1,1] bf16 values)",
+        "data": "synthetic (seeded xoshiro256** uniform-random block positions, U[-1,1] bf16 values)",
         "config": {"workload": "BSR SpMM C=A*B: A 4096x4096, 32x32 blocks, 25% block density (4096 blocks), "
                                "B 4096x512 bf16, fp32 accumulate, fp32 C",
                    "M": 4096, "K": 4096, "N": 512, "block": [32, 32], "density": 0.25,
+                   "input_sha256": row.get("input_sha256"),
                    "peaks": {"bf16_mfma_tflops": PEAK_BF16_TFLOPS, "hbm_gbs": PEAK_HBM_GBS,
                              "source": "AMD Instinct MI355X published dense figures"}},
-        "roofline": roofline(fl, nbytes, k_s, row),
+        "roofline": rl,
         "cpu_baseline": cpu,
     }
     result.update(out)

@@ -16,6 +16,7 @@ REPO = PKG_DIR.parent
 CSRC = PKG_DIR / "csrc"
 INCLUDE = REPO / "include"
 LIB_PATH = PKG_DIR / "libbsparse.so"
+PROBE_PATH = PKG_DIR / "libbsp_probe.so"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -61,6 +62,13 @@ def build_library(verbose: bool = False) -> Path:
         print(" ".join(cmd))
     _run(cmd)
     os.replace(tmp, LIB_PATH)
+    # The memory-system probe bench.py uses for the on-chip roof (a library of
+    # its own: it is not part of the boundary).
+    obj = build_dir / "bsp_probe.hip.o"
+    _run([HIPCC, *HIP_FLAGS, "-x", "hip", "-c", str(CSRC / "bsp_probe.hip"), "-o", str(obj)])
+    tmp = PROBE_PATH.with_suffix(".so.tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", str(obj), "-o", str(tmp)])
+    os.replace(tmp, PROBE_PATH)
     return LIB_PATH
 
 

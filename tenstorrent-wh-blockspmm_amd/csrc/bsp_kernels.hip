@@ -199,6 +199,10 @@ __device__ __forceinline__ u32x4 ld_tr_b16(const uint8_t* lds) {
 // kernel's end.  8 MB of fp32 tiles from 512 workgroups, per launch in a
 // graph: plain or non-temporal stores 2.98 us, write-through 2.40 us (32 MB:
 // 7.0-7.2 -> 5.7 us).
+// A write-through store completes only when it has left the L2, so a wave
+// that waits on vmcnt for loads issued after its stores (the SpGEMM ring)
+// waits for that too: such a kernel stores with store_out_nt instead
+// (non-temporal, completing at the L2; SpGEMM 8192^2 fp32: 108 -> 28 us).
 template <typename T>
 __device__ __forceinline__ void store_out(T* p, T v) {
     if constexpr (sizeof(T) <= 8) {
@@ -210,6 +214,11 @@ __device__ __forceinline__ void store_out(T* p, T v) {
         __hip_atomic_store(d, w[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(d + 1, w[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+}
+
+template <typename T>
+__device__ __forceinline__ void store_out_nt(T* p, T v) {
+    __builtin_nontemporal_store(v, p);
 }
 
 // Stores one 32x32 MFMA result at rows row0.., column col (this lane's
@@ -1517,9 +1526,9 @@ __global__ __launch_bounds__(256) void sddmm_kernel(SddmmArgs p) {
                 const float val = sum * bf16_to_f32((uint16_t)mcur[j]);
                 const int64_t idx = off + (int64_t)(8 * wave + 4 * q + j) * p.ldo + l32;
                 if (OUT_BF16)
-                    store_out(&((uint16_t*)p.out)[idx], f32_to_bf16_rne(val));
+                    store_out_nt(&((uint16_t*)p.out)[idx], f32_to_bf16_rne(val));
                 else
-                    store_out(&((float*)p.out)[idx], val);
+                    store_out_nt(&((float*)p.out)[idx], val);
             }
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
@@ -1856,7 +1865,7 @@ __global__ __launch_bounds__(256) void spgemm_kernel(SpgemmArgs p) {
             const u32x4 val = *(const u32x4*)(tile + 16 * c);
             const int r = c / (ROW / 16), col = (c % (ROW / 16)) * (16 / ESZ);
             const int64_t idx = off + (int64_t)r * p.ldo + col;
-            store_out((u32x4*)((uint8_t*)p.out + idx * ESZ), val);
+            store_out_nt((u32x4*)((uint8_t*)p.out + idx * ESZ), val);
         }
     }
 }

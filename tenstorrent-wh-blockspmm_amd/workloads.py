@@ -5,13 +5,19 @@ Structure generators restate the fill modes of bsr_matrix<T>'s constructors
 (sparse_common/bsr_matrix.hpp:244-408, block_spmm/inc/bsr_matrix.hpp:376-405
 for FILL_TRIU) and its random-position constructor (:619-679).  The reference
 seeds positions from the clock and values from unseeded rand()
-(sparse_common/bsr_matrix.hpp:646-647, :55); here everything comes from a
-numpy PCG64 generator with an explicit seed, so inputs are identical on every
-machine.  Values are drawn in float32 and rounded to bf16 (round to nearest
-even), returned as uint16 bit patterns.
+(sparse_common/bsr_matrix.hpp:646-647, :55).  Here every benchmark workload
+comes from this module's own seeded generator (Rng: xoshiro256**, seeded
+through splitmix64), written in plain uint64 arithmetic, so its output does
+not depend on numpy's own generators (whose streams numpy does not promise to
+keep across versions) and is identical on every machine; workload_digest()
+pins each workload's bytes.  Values are drawn in float32 and rounded to bf16
+(round to nearest even), returned as uint16 bit patterns.  The generator
+functions also accept a numpy Generator (tests use them for inputs that are
+checked against the oracle in the same run and need no pinning).
 """
 from __future__ import annotations
 
+import hashlib
 from dataclasses import dataclass
 from typing import Optional
 
@@ -19,6 +25,104 @@ import numpy as np
 
 SEED_BASE = 0x5EED0000  # workload i uses SEED_BASE + i
 TILE = 32
+
+_M64 = (1 << 64) - 1
+
+
+class Rng:
+    """xoshiro256** (D. Blackman and S. Vigna, "Scrambled linear pseudorandom
+    number generators", 2018), run as `lanes` independent streams stepped
+    together: the state of lane l is four outputs of splitmix64 started at
+    seed * lanes + l.  Output k of a draw is step k // lanes of lane
+    k % lanes; a draw consumes whole steps.  uint64 arithmetic wraps, as the
+    algorithm requires; nothing else (no float library call) enters the
+    integer streams."""
+
+    def __init__(self, seed: int, lanes: int = 65536):
+        self.lanes = lanes
+        x = (np.uint64(seed & _M64) * np.uint64(lanes) + np.arange(lanes, dtype=np.uint64))
+        st = []
+        with np.errstate(over="ignore"):
+            for _ in range(4):
+                x = x + np.uint64(0x9E3779B97F4A7C15)
+                z = x.copy()
+                z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+                z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+                st.append(z ^ (z >> np.uint64(31)))
+        self.s = st
+
+    @staticmethod
+    def _rotl(x, k):
+        return (x << np.uint64(k)) | (x >> np.uint64(64 - k))
+
+    def u64(self, n: int) -> np.ndarray:
+        """n uint64 outputs."""
+        steps = -(-n // self.lanes)
+        out = np.empty((max(steps, 0), self.lanes), np.uint64)
+        s0, s1, s2, s3 = self.s
+        with np.errstate(over="ignore"):
+            for i in range(steps):
+                out[i] = self._rotl(s1 * np.uint64(5), 7) * np.uint64(9)
+                t = s1 << np.uint64(17)
+                s2 = s2 ^ s0
+                s3 = s3 ^ s1
+                s1 = s1 ^ s2
+                s0 = s0 ^ s3
+                s2 = s2 ^ t
+                s3 = self._rotl(s3, 45)
+        self.s = [s0, s1, s2, s3]
+        return out.reshape(-1)[:n]
+
+    def random(self, shape, dtype=np.float64) -> np.ndarray:
+        """U[0, 1): float64 from the top 53 bits, float32 from the top 24
+        (both exact)."""
+        n = int(np.prod(shape))
+        x = self.u64(n)
+        if np.dtype(dtype) == np.float32:
+            r = (x >> np.uint64(40)).astype(np.float32) * np.float32(2.0 ** -24)
+        else:
+            r = (x >> np.uint64(11)).astype(np.float64) * (2.0 ** -53)
+        return r.reshape(shape)
+
+    def standard_normal(self, shape, dtype=np.float32) -> np.ndarray:
+        """N(0, 1) by the Box-Muller transform of two float64 uniforms."""
+        n = int(np.prod(shape))
+        u1 = 1.0 - self.random(n)  # (0, 1]
+        u2 = self.random(n)
+        z = np.sqrt(-2.0 * np.log(u1)) * np.cos(2.0 * np.pi * u2)
+        return z.astype(dtype).reshape(shape)
+
+    def sample(self, n: int, k: int) -> np.ndarray:
+        """k distinct integers of [0, n), ascending: the k smallest of n random
+        keys (a uniform k-subset; ties broken by position)."""
+        keys = self.u64(n)
+        return np.sort(np.argsort(keys, kind="stable")[:k]).astype(np.int64)
+
+
+def _sample_sorted(rng, n: int, k: int) -> np.ndarray:
+    if isinstance(rng, Rng):
+        return rng.sample(n, k)
+    return np.sort(rng.choice(n, size=k, replace=False)).astype(np.int64)
+
+
+def workload_digest(w: dict) -> str:
+    """SHA-256 over a workload's arrays (BSR index arrays and values, dense
+    operands) in key order, with each array's dtype and shape."""
+    h = hashlib.sha256()
+    for key in sorted(w):
+        v = w[key]
+        parts = []
+        if isinstance(v, BsrArrays):
+            parts = [("indptr", v.indptr), ("indices", v.indices), ("data", v.data)]
+        elif isinstance(v, np.ndarray):
+            parts = [("", v)]
+        for name, arr in parts:
+            if arr is None:
+                continue
+            arr = np.ascontiguousarray(arr)
+            h.update(f"{key}.{name}:{arr.dtype.str}:{arr.shape}".encode())
+            h.update(arr.tobytes())
+    return h.hexdigest()
 
 
 # ---------------------------------------------------------------------------
@@ -188,7 +292,7 @@ def random_positions(H, W, R, C, nblocks, rng: np.random.Generator) -> BsrArrays
     constructor, sparse_common/bsr_matrix.hpp:619-679, with a seeded
     generator), columns sorted within each row."""
     nbr, nbc = H // R, W // C
-    flat = np.sort(rng.choice(nbr * nbc, size=nblocks, replace=False))
+    flat = _sample_sorted(rng, nbr * nbc, nblocks)
     return _from_positions(H, W, R, C, flat // nbc, flat % nbc)
 
 
@@ -258,7 +362,7 @@ def zipf_row_counts(nbr: int, nbc: int, density: float, s: float, cap: int,
 def spmm_workload(M, K, N, R, C, density: float, seed: int, value_range=1.0, zipf=None) -> dict:
     """A (BSR, random positions or Zipf rows) and B dense, both bf16
     U[-value_range, value_range]."""
-    rng = np.random.default_rng(seed)
+    rng = Rng(seed)
     nbr, nbc = M // R, K // C
     if zipf is None:
         nnzb = int(round(density * nbr * nbc))
@@ -266,10 +370,16 @@ def spmm_workload(M, K, N, R, C, density: float, seed: int, value_range=1.0, zip
     else:
         s, cap = zipf
         counts = zipf_row_counts(nbr, nbc, density, s, cap, rng)
+        # Row i's columns: the cnt smallest of its nbc random keys (a uniform
+        # subset per row, as _sample_sorted draws one).
+        keys = rng.u64(nbr * nbc).reshape(nbr, nbc) if isinstance(rng, Rng) else None
         rows, cols = [], []
         for i, cnt in enumerate(counts):
             if cnt:
-                cs = np.sort(rng.choice(nbc, size=int(cnt), replace=False))
+                if keys is not None:
+                    cs = np.sort(np.argsort(keys[i], kind="stable")[: int(cnt)]).astype(np.int64)
+                else:
+                    cs = _sample_sorted(rng, nbc, int(cnt))
                 rows.append(np.full(cnt, i))
                 cols.append(cs)
         a = _from_positions(M, K, R, C, np.concatenate(rows), np.concatenate(cols))
@@ -303,7 +413,7 @@ def workload_spmm_sweep(density: float) -> dict:
 def workload_sddmm(M=4096, N=4096, K=256, density=0.10, seed=SEED_BASE + 2) -> dict:
     """mask M x N (32x32 blocks, uniform positions, values 1.0), X M x K and
     Y K x N, both N(0,1) bf16."""
-    rng = np.random.default_rng(seed)
+    rng = Rng(seed)
     nnzb = int(round(density * (M // 32) * (N // 32)))
     mask = random_positions(M, N, 32, 32, nnzb, rng)
     mask.data = bf16_from_f32(np.ones(nnzb * 1024, np.float32))
@@ -316,7 +426,7 @@ def workload_spgemm(n=8192, block=32, density=0.05, seed=SEED_BASE + 6) -> dict:
     """A and B n x n, block x block blocks at uniform-random positions with
     `density` each, values U[-1, 1] bf16 (A * B with 32x32 blocks at 5%: about
     47% of the output blocks are stored, 0.64 block pairs each on average)."""
-    rng = np.random.default_rng(seed)
+    rng = Rng(seed)
     nnzb = int(round(density * (n // block) ** 2))
     a = random_positions(n, n, block, block, nnzb, rng)
     a.data = bf16_from_f32(uniform_f32(rng, nnzb * block * block))
@@ -341,7 +451,7 @@ def band_global_mask(seq: int, block: int, bands: int, global_density: float,
     band = (i - j >= 0) & (i - j < bands)
     outside = np.flatnonzero(~band.ravel())
     ng = int(round(global_density * nb * nb))
-    pick = rng.choice(outside, size=ng, replace=False)
+    pick = outside[_sample_sorted(rng, outside.size, ng)]
     flat = np.sort(np.concatenate([np.flatnonzero(band.ravel()), pick]))
     return _from_positions(seq, seq, block, block, flat // nb, flat % nb)
 
@@ -349,7 +459,7 @@ def band_global_mask(seq: int, block: int, bands: int, global_density: float,
 def workload_attention(seq=8192, d=128, seed=SEED_BASE + 4) -> dict:
     """Q, K, V seq x d, N(0, std = d^-1/2) bf16; mask = 8 causal block
     diagonals + 1% global blocks, values 1.0."""
-    rng = np.random.default_rng(seed)
+    rng = Rng(seed)
     mask = band_global_mask(seq, 32, 8, 0.01, rng)
     mask.data = bf16_from_f32(np.ones(mask.nblocks * 1024, np.float32))
     std = d ** -0.5
