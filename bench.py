@@ -168,12 +168,14 @@ def plan_summary(info):
 # (profiles/*_traffic.md: FETCH_SIZE and WRITE_SIZE per dispatch, scaled by
 # kernels of known traffic).
 def committed_traffic() -> dict:
+    """{workload key: measured bytes per launch} from the `traffic_record:`
+    lines (one JSON object each) of profiles/*_traffic.md."""
     out = {}
     for f in sorted((REPO / "profiles").glob("*_traffic.md")):
-        kv = dict(line.split(": ", 1) for line in f.read_text().splitlines() if line.startswith("traffic_"))
-        if "traffic_workload" in kv and "traffic_bytes_per_launch" in kv:
-            out[kv["traffic_workload"]] = {"file": f.name, "kernel": kv.get("traffic_kernel"),
-                                           "bytes": int(kv["traffic_bytes_per_launch"])}
+        for line in f.read_text().splitlines():
+            if line.startswith("traffic_record: "):
+                r = json.loads(line[len("traffic_record: "):])
+                out[r["workload"]] = {"file": f.name, "kernel": r.get("kernel"), "bytes": int(r["bytes_per_launch"])}
     return out
 
 
@@ -660,10 +662,13 @@ def main():
         t3, f3, b3, _ = bench_attention(torch, capi, W, w, "f32", timer, warmup)
         fused = summarize(t3, f3, b3)
         attach_traffic(fused, f"attention seq{m.H} d{w['d']} nnzb{m.nblocks} f32")
+        s_rec, o_rec = summarize(t1, f1, b1), summarize(t2, f2, b2)
+        attach_traffic(s_rec, f"sddmm {m.H}x{m.W} r{m.R}c{m.C} nnzb{m.nblocks} K{w['d']} bf16 colmajor")
+        attach_traffic(o_rec, traffic_key_spmm(a, w["d"], "f32"))
         rec = {"workload": "seq 8192, d 128, 8 causal block bands + 1% global; S=mask(.)QK^T (bf16) then "
                            "O=S*V (fp32)",
-               "nnzb": m.nblocks, "input_sha256": W.workload_digest(w), "sddmm": summarize(t1, f1, b1),
-               "spmm": {**summarize(t2, f2, b2), "plan": plan_summary(info2)},
+               "nnzb": m.nblocks, "input_sha256": W.workload_digest(w), "sddmm": s_rec,
+               "spmm": {**o_rec, "plan": plan_summary(info2)},
                "pair_tflops": round((f1 + f2) / ((t1["launch_ms"] + t2["launch_ms"]) * 1e-3) / 1e12, 3),
                "fused": fused}
         if orc is not None:
@@ -675,8 +680,10 @@ def main():
         rows = []
         for od in ("f32", "bf16"):
             t, fl, nb, info, extra = bench_spgemm(torch, capi, W, w["a"], w["b"], od, timer, warmup)
-            rows.append({"out": od, **summarize(t, fl, nb), "grid": info["grid"], "sub_blocks": info["n_items"],
-                         "products": info["n_entries"], **extra})
+            r = {"out": od, **summarize(t, fl, nb), "grid": info["grid"], "sub_blocks": info["n_items"],
+                 "products": info["n_entries"], **extra}
+            attach_traffic(r, f"spgemm {w['a'].H}x{w['b'].W} r{w['a'].R}c{w['a'].C} nnzb{w['a'].nblocks}x{w['b'].nblocks} {od}")
+            rows.append(r)
         rec = {"workload": "SpGEMM C=A*B, A and B 8192x8192, 32x32 blocks, 5% each (3277 blocks)",
                "nnzb": w["a"].nblocks, "input_sha256": W.workload_digest(w), "runs": rows}
         if orc is not None:
@@ -706,8 +713,10 @@ def main():
         for R in (128, 64):
             w = W.workload_spmm_large_blocks(0.25, R=R)
             t, fl, nb, info, _ = bench_spmm(torch, capi, W, w["a"], w["b"], "f32", lt, max(5, warmup // 2))
-            rows.append({"R": R, "C": R, "nnzb": w["a"].nblocks, "out": "f32", **summarize(t, fl, nb),
-                         "plan": plan_summary(info)})
+            r = {"R": R, "C": R, "nnzb": w["a"].nblocks, "out": "f32", **summarize(t, fl, nb),
+                 "plan": plan_summary(info)}
+            attach_traffic(r, traffic_key_spmm(w["a"], 8192, "f32"))
+            rows.append(r)
             del w
         out["block_sizes"] = {"workload": "SpMM 8192^3, R x R blocks, 25%, fp32 C", "runs": rows}
 

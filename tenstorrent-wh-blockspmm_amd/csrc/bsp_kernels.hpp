@@ -50,7 +50,8 @@ struct SpmmStreamArgs {
     X(128, 4, 16, 4)                \
     X(256, 4, 16, 4)                \
     X(256, 5, 16, 8)                \
-    X(256, 6, 8, 8)
+    X(256, 6, 8, 8)                 \
+    X(128, 8, 16, 8)
 
 struct SpmmStreamVariant {
     int tile_n;

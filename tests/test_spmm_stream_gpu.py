@@ -12,7 +12,7 @@ from helpers import W, assert_parity, bsr_of, capi, golden_spmm, run_spmm, spmm_
 pytestmark = pytest.mark.gpu
 
 # (tile, B ring, A ring, B loader waves) of BSP_SPMM_STREAM_VARIANTS in csrc/bsp_kernels.hpp
-STREAM_VARIANTS = [(128, 6, 12, 2), (128, 6, 12, 4), (128, 4, 16, 4), (256, 4, 16, 4), (256, 5, 16, 8),
+STREAM_VARIANTS = [(128, 6, 12, 2), (128, 6, 12, 4), (128, 4, 16, 4), (128, 8, 16, 8), (256, 4, 16, 4), (256, 5, 16, 8),
                    (256, 6, 8, 8)]
 
 
