@@ -108,9 +108,11 @@ typedef struct bsp_plan_info {
                             (1; or 2, 4, 8 for blocks of R >= 64) */
     int32_t waves;       /* SpMM: waves per workgroup (fixed at plan creation) */
     int64_t workspace_bytes; /* device scratch owned by the plan */
-    int32_t persistent;  /* SpMM: 1 = persistent kernel (each workgroup streams
-                            a list of stripe x tile units; n_items counts the
-                            units, stages is the B ring depth) */
+    int32_t persistent;  /* SpMM: 0 = one work item per workgroup; 1 or 2 =
+                            persistent kernel with that many pipelines per
+                            workgroup (each pipeline streams a list of stripe x
+                            tile units; n_items counts the units, stages is the
+                            B ring depth) */
     int32_t a_stages;    /* SpMM persistent: depth of the A ring */
 } bsp_plan_info;
 

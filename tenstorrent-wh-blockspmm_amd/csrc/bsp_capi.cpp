@@ -239,34 +239,45 @@ int64_t env_int(const char* name, int64_t dflt) {
     return (end && *end == 0) ? (int64_t)x : dflt;
 }
 
+}  // namespace
+
+namespace bsp {
+
 // Whether an SpMM plan runs the persistent kernel, and which variant.  It
 // takes blocks whose stripes do not form row groups (row groups share each B
 // panel among the stripes of a block row, which the per-item group kernels
 // exploit) and N a multiple of 128.  BSP_SPMM_STREAM=0 turns it off;
-// BSP_SPMM_STREAM_VARIANT="tile,sb,sa,nbw" picks another compiled variant and
-// BSP_SPMM_STREAM_WPC the workgroups per compute unit (all read here, at plan
-// creation).
-bool choose_spmm_stream(const bsp_bsr_desc* a, int64_t N, int cus, bsp::SpmmStreamVariant* sv, int* wpc) {
+// BSP_SPMM_STREAM_VARIANT="tile,sb,sa,nbw[,pipes]" picks another compiled
+// variant and BSP_SPMM_STREAM_WPC the workgroups per compute unit (all read
+// here, at plan creation).  A two-pipeline variant runs one workgroup per
+// compute unit.
+bool choose_spmm_stream(const bsp_bsr_desc* a, int64_t N, int cus, SpmmStreamVariant* sv, int* wpc) {
     if (env_int("BSP_SPMM_STREAM", 1) == 0) return false;
     if (N % 128 != 0) return false;
     const int64_t group = env_int("BSP_SPMM_GROUP", bsp::spmm_choose_group(a->R, a->H, N, cus));
     if (group > 1 && (a->R / bsp::kSub) % group == 0) return false;
-    bsp::SpmmStreamVariant v{128, 6, 12, 2};
+    bsp::SpmmStreamVariant v{128, 6, 12, 2, 1};
     if (const char* e = std::getenv("BSP_SPMM_STREAM_VARIANT")) {
         bsp::SpmmStreamVariant w{};
-        if (std::sscanf(e, "%d,%d,%d,%d", &w.tile_n, &w.sb, &w.sa, &w.nbw) == 4 &&
-            bsp::spmm_stream_variant_supported(w))
-            v = w;
+        w.pipes = 1;
+        const int got = std::sscanf(e, "%d,%d,%d,%d,%d", &w.tile_n, &w.sb, &w.sa, &w.nbw, &w.pipes);
+        if (got >= 4 && bsp::spmm_stream_variant_supported(w)) v = w;
     }
-    if (N % v.tile_n != 0) v = bsp::SpmmStreamVariant{128, 6, 12, 2};
+    if (N % v.tile_n != 0) v = bsp::SpmmStreamVariant{128, 6, 12, 2, 1};
     const int lds = bsp::spmm_stream_lds_bytes(v);
-    int w = std::max(1, std::min(2, bsp::kLdsBytesPerCu / lds));
-    w = (int)env_int("BSP_SPMM_STREAM_WPC", w);
+    int w = v.pipes > 1 ? 1 : std::max(1, std::min(2, bsp::kLdsBytesPerCu / lds));
+    if (v.pipes == 1) w = (int)env_int("BSP_SPMM_STREAM_WPC", w);
     if (w < 1 || w * lds > bsp::kLdsBytesPerCu) w = 1;
     *sv = v;
     *wpc = w;
     return true;
 }
+
+int record_error(int status, const std::string& msg) { return fail(status, msg); }
+
+}  // namespace bsp
+
+namespace {
 
 // Plan of the persistent SpMM kernel: per-workgroup unit lists and entry
 // streams, uploaded once.
@@ -275,7 +286,7 @@ int make_spmm_stream_plan(bsp_plan** out, const bsp_bsr_desc* a, int64_t N, int 
     std::string msg;
     bsp::SpmmStream ss;
     const int cg = (int)env_int("BSP_SPMM_XCD_COLS", 0);
-    int st = bsp::build_spmm_stream(a, N, cus, sv.tile_n, wpc, ss, msg, cg);
+    int st = bsp::build_spmm_stream(a, N, cus, sv.tile_n, wpc, ss, msg, cg, sv.pipes);
     if (st != BSP_OK) return fail(st, msg);
     DeviceGuard g(device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
@@ -298,12 +309,12 @@ int make_spmm_stream_plan(bsp_plan** out, const bsp_bsr_desc* a, int64_t N, int 
     in.n_tiles = ss.n_tiles;
     in.n_items = (int32_t)(ss.units.size() - bsp::kStreamPad);
     in.n_entries = (int32_t)ss.n_entries;
-    in.grid = (int32_t)ss.wgs.size();
+    in.grid = (int32_t)(ss.wgs.size() / sv.pipes);
     in.max_item_entries = ss.max_wg_entries;
     in.stages = sv.sb;
     in.group = 1;
-    in.waves = 5 + sv.nbw;
-    in.persistent = 1;
+    in.waves = (5 + sv.nbw) * sv.pipes;
+    in.persistent = sv.pipes;
     in.a_stages = sv.sa;
     hipError_t e = upload((bsp::SpmmStreamWg**)&p->d_wgs, ss.wgs);
     if (e == hipSuccess) e = upload(&p->d_units, ss.units);
@@ -334,7 +345,7 @@ int make_spmm_plan(bsp_plan** out, int kind, const bsp_bsr_desc* a, int64_t N, i
     if (kind == 1) {
         bsp::SpmmStreamVariant sv{};
         int wpc = 1;
-        if (choose_spmm_stream(a, N, cus, &sv, &wpc)) return make_spmm_stream_plan(out, a, N, out_dtype, device, cus, sv, wpc);
+        if (bsp::choose_spmm_stream(a, N, cus, &sv, &wpc)) return make_spmm_stream_plan(out, a, N, out_dtype, device, cus, sv, wpc);
     }
     bsp::SpmmSchedule s;
     st = bsp::build_spmm_schedule(a, N, cus, s, msg, force_tile_n, kind == 3 ? 1 : 0);

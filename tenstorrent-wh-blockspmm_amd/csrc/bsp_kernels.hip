@@ -995,20 +995,47 @@ __device__ __forceinline__ void stream_loader(int n, const WT* words, Issue&& is
 
 }  // namespace spmm_detail
 
-template <int NTW, int SB, int SA, int NBW, bool OUT_BF16>
-__global__ __launch_bounds__(64 * (5 + NBW)) void spmm_stream_kernel(SpmmStreamArgs p) {
+// With PIPES = 2, one workgroup holds two such pipelines (each with its own
+// rings, MFMA waves and loaders) that share the per-entry barrier and split
+// their compute unit's entry stream in half: the unit that straddles the
+// half is accumulated by both, the second pipeline leaves its part in an LDS
+// exchange buffer (unit flag 1) and the first adds it before storing (flag 2)
+// after one last barrier.  Two independent workgroups per compute unit hold
+// one unit each, and the one with the longer row finishes alone at the rate
+// of a single workgroup's loaders; the halves end together.
+template <int NTW, int SB, int SA, int NBW, int PIPES, bool OUT_BF16>
+__global__ __launch_bounds__(64 * (5 + NBW) * PIPES) void spmm_stream_kernel(SpmmStreamArgs p) {
     using namespace spmm_detail;
     constexpr int TN = 128 * NTW;
     using Loader = BSliceLoader<TN, NBW>;
     constexpr int A_RING = SA * kA_BYTES;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[A_RING + SB * Loader::BYTES];
+    constexpr int PIPE_LDS = A_RING + SB * Loader::BYTES;
+    constexpr int WPP = 5 + NBW;                                 // waves per pipeline
+    constexpr int XCHG = PIPES > 1 ? 4 * NTW * 16 * 64 * 4 : 0;  // fp32 tile of the shared unit
+    static_assert(PIPES == 1 || PIPES == 2, "pipelines");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[PIPES * PIPE_LDS + XCHG];
 
-    const SpmmStreamWg wg = load_const(p.wgs + blockIdx.x);
-    const int n = wg.n;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t lds0 = lds_address(smem);
+    const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int pipe = PIPES > 1 ? wave_id / WPP : 0;
+    const int wave = wave_id - pipe * WPP;  // role within the pipeline
+    const SpmmStreamWg wg = load_const(p.wgs + blockIdx.x * PIPES + pipe);
+    const int n = wg.n;
+    // Barriers every wave takes: the longer pipeline's steps (+1 to close the exchange).
+    int steps = n;
+    if constexpr (PIPES > 1) {
+        const SpmmStreamWg w0 = load_const(p.wgs + blockIdx.x * PIPES);
+        const SpmmStreamWg w1 = load_const(p.wgs + blockIdx.x * PIPES + 1);
+        steps = max(w0.n, w1.n);
+    }
+    uint8_t* psmem = smem + pipe * PIPE_LDS;
+    float* xchg = (float*)(smem + PIPES * PIPE_LDS);
+    const uint32_t lds0 = lds_address(psmem);
+    auto idle_steps = [&] {
+        for (int k = n; k < steps; ++k) barrier_no_fence();
+        if constexpr (PIPES > 1) barrier_no_fence();
+    };
 
     if (wave == 4 + NBW) {
         // A loader: load j (1 KB) covers segments 2j and 2j+1 of the 32x32
@@ -1022,6 +1049,7 @@ __global__ __launch_bounds__(64 * (5 + NBW)) void spmm_stream_kernel(SpmmStreamA
             gl_lds16_s(a_voff[0], ablk, dst);
             gl_lds16_s(a_voff[1], ablk, dst + 1024);
         });
+        idle_steps();
         return;
     }
     if (wave >= 4) {
@@ -1034,6 +1062,7 @@ __global__ __launch_bounds__(64 * (5 + NBW)) void spmm_stream_kernel(SpmmStreamA
 #pragma unroll
             for (int j = 0; j < Loader::BI; ++j) gl_lds16_s(ld.voff[j], bpan, dst + j * 1024);
         });
+        idle_steps();
         return;
     }
 
@@ -1055,11 +1084,13 @@ __global__ __launch_bounds__(64 * (5 + NBW)) void spmm_stream_kernel(SpmmStreamA
     int u = 0;
     SpmmStreamUnit cur = load_const(units);
     SpmmStreamUnit nxt = load_const(units + 1);
-    auto store_cur = [&] {
-        const int64_t row0 = (int64_t)cur.row * 32;
+    SpmmStreamUnit held{};  // the shared unit, stored after the exchange (flag 2)
+    bool holding = false;
+    auto store_unit = [&](const SpmmStreamUnit& un) {
+        const int64_t row0 = (int64_t)un.row * 32;
 #pragma unroll
         for (int nt = 0; nt < NTW; ++nt) {
-            const int64_t col = cur.n0 + wave * (NTW * 32) + nt * 32 + l32;
+            const int64_t col = un.n0 + wave * (NTW * 32) + nt * 32 + l32;
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int64_t row = row0 + 8 * (v >> 2) + 4 * q + (v & 3);
@@ -1070,6 +1101,30 @@ __global__ __launch_bounds__(64 * (5 + NBW)) void spmm_stream_kernel(SpmmStreamA
             }
         }
     };
+    auto xchg_at = [&](int nt, int v) { return xchg + ((wave * NTW + nt) * 16 + v) * 64 + lane; };
+    auto zero_acc = [&] {
+#pragma unroll
+        for (int i = 0; i < NTW; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
+    };
+    // Ends unit `cur`: store it, or (two pipelines) leave it in the exchange
+    // buffer, or hold it for the exchange.
+    auto finish_cur = [&] {
+        if (PIPES > 1 && cur.pad == 1) {
+#pragma unroll
+            for (int nt = 0; nt < NTW; ++nt)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) *xchg_at(nt, v) = acc[nt][v];
+            zero_acc();
+        } else if (PIPES > 1 && cur.pad == 2) {
+            held = cur;
+            holding = true;
+        } else {
+            store_unit(cur);
+            zero_acc();
+        }
+    };
     // Moves to the next unit with entries, storing (zero) tiles of empty ones.
     auto next_unit = [&] {
         ++u;
@@ -1077,7 +1132,7 @@ __global__ __launch_bounds__(64 * (5 + NBW)) void spmm_stream_kernel(SpmmStreamA
             cur = nxt;
             nxt = load_const(units + u + 1);
             if (cur.count > 0) return cur.count;
-            store_cur();
+            store_unit(cur);
             ++u;
         }
         return 0;
@@ -1087,7 +1142,7 @@ __global__ __launch_bounds__(64 * (5 + NBW)) void spmm_stream_kernel(SpmmStreamA
         if (cur.count > 0) {
             left = cur.count;
         } else {
-            store_cur();
+            store_unit(cur);
             left = next_unit();
         }
     }
@@ -1097,10 +1152,10 @@ __global__ __launch_bounds__(64 * (5 + NBW)) void spmm_stream_kernel(SpmmStreamA
         u32x4 b[2][NTW];
     };
     auto read = [&](int k, Operands& o) {
-        const uint8_t* as = smem + (k % SA) * kA_BYTES;
+        const uint8_t* as = psmem + (k % SA) * kA_BYTES;
         o.a[0] = *(const u32x4*)(as + a_rd);
         o.a[1] = *(const u32x4*)(as + 256 + a_rd);
-        brd.read(smem + A_RING + (k % SB) * Loader::BYTES, o.b);
+        brd.read(psmem + A_RING + (k % SB) * Loader::BYTES, o.b);
     };
     auto multiply = [&](const Operands& o) {
 #pragma unroll
@@ -1108,11 +1163,7 @@ __global__ __launch_bounds__(64 * (5 + NBW)) void spmm_stream_kernel(SpmmStreamA
 #pragma unroll
             for (int nt = 0; nt < NTW; ++nt) acc[nt] = mfma32(o.a[s2], o.b[s2][nt], acc[nt]);
         if (--left == 0) {
-            store_cur();
-#pragma unroll
-            for (int i = 0; i < NTW; ++i)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
+            finish_cur();
             left = next_unit();
         }
     };
@@ -1150,6 +1201,18 @@ __global__ __launch_bounds__(64 * (5 + NBW)) void spmm_stream_kernel(SpmmStreamA
         multiply(o1);
     } else if (n > 0) {
         multiply(o0);
+    }
+    if constexpr (PIPES > 1) {
+        lds_done();  // exchange writes complete before the closing barrier
+        for (int s = n; s < steps; ++s) barrier_no_fence();
+        barrier_no_fence();
+        if (holding) {
+#pragma unroll
+            for (int nt = 0; nt < NTW; ++nt)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[nt][v] += *xchg_at(nt, v);
+            store_unit(held);
+        }
     }
 }
 
@@ -1933,14 +1996,14 @@ hipError_t launch_spmm(const SpmmArgs& a, const SpmmVariant& v, bool out_bf16, i
 hipError_t launch_spmm_stream(const SpmmStreamArgs& a, const SpmmStreamVariant& v, bool out_bf16, int grid,
                               hipStream_t stream) {
     if (grid <= 0) return hipSuccess;
-#define BSP_STREAM_CASE(TN, SB, SA, NB)                                                                         \
-    if (v.tile_n == TN && v.sb == SB && v.sa == SA && v.nbw == NB) {                                           \
+#define BSP_STREAM_CASE(TN, SB, SA, NB, PP)                                                                     \
+    if (v.tile_n == TN && v.sb == SB && v.sa == SA && v.nbw == NB && v.pipes == PP) {                          \
         if (out_bf16)                                                                                          \
-            hipLaunchKernelGGL((spmm_stream_kernel<TN / 128, SB, SA, NB, true>), dim3(grid), dim3(64 * (5 + NB)), 0, \
-                               stream, a);                                                                     \
+            hipLaunchKernelGGL((spmm_stream_kernel<TN / 128, SB, SA, NB, PP, true>), dim3(grid),                 \
+                               dim3(64 * (5 + NB) * PP), 0, stream, a);                                        \
         else                                                                                                   \
-            hipLaunchKernelGGL((spmm_stream_kernel<TN / 128, SB, SA, NB, false>), dim3(grid), dim3(64 * (5 + NB)), \
-                               0, stream, a);                                                                  \
+            hipLaunchKernelGGL((spmm_stream_kernel<TN / 128, SB, SA, NB, PP, false>), dim3(grid),                \
+                               dim3(64 * (5 + NB) * PP), 0, stream, a);                                        \
         return hipGetLastError();                                                                              \
     }
     BSP_SPMM_STREAM_VARIANTS(BSP_STREAM_CASE)

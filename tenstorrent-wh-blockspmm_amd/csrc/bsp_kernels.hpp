@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <string>
 
 #include "bsp_schedule.hpp"
 
@@ -42,36 +43,50 @@ struct SpmmStreamArgs {
 };
 
 // Compiled persistent SpMM variants: tile width, B ring depth, A ring depth,
-// B loader waves.  A workgroup has 4 MFMA waves (each 32*tile/128 columns),
-// the B loader waves and one A loader wave; LDS = 64*tile*SB + 2 KB*SA.
+// B loader waves, pipelines per workgroup.  A pipeline has 4 MFMA waves (each
+// 32*tile/128 columns), the B loader waves and one A loader wave, and LDS of
+// 64*tile*SB + 2 KB*SA; two pipelines add a 16 KB (32 KB at tile 256)
+// exchange buffer.
 #define BSP_SPMM_STREAM_VARIANTS(X) \
-    X(128, 6, 12, 2)                \
-    X(128, 6, 12, 4)                \
-    X(128, 4, 16, 4)                \
-    X(256, 4, 16, 4)                \
-    X(256, 5, 16, 8)                \
-    X(256, 6, 8, 8)                 \
-    X(128, 8, 16, 8)
+    X(128, 6, 12, 2, 1)             \
+    X(128, 6, 12, 4, 1)             \
+    X(128, 4, 16, 4, 1)             \
+    X(128, 8, 16, 8, 1)             \
+    X(256, 4, 16, 4, 1)             \
+    X(256, 5, 16, 8, 1)             \
+    X(256, 6, 8, 8, 1)              \
+    X(128, 6, 12, 2, 2)             \
+    X(128, 5, 12, 2, 2)
 
 struct SpmmStreamVariant {
     int tile_n;
     int sb;
     int sa;
     int nbw;
+    int pipes = 1;
 };
 
 inline bool spmm_stream_variant_supported(const SpmmStreamVariant& v) {
-#define BSP_SPMM_STREAM_MATCH(TN, SB, SA, NB) \
-    if (v.tile_n == TN && v.sb == SB && v.sa == SA && v.nbw == NB) return true;
+#define BSP_SPMM_STREAM_MATCH(TN, SB, SA, NB, PP) \
+    if (v.tile_n == TN && v.sb == SB && v.sa == SA && v.nbw == NB && v.pipes == PP) return true;
     BSP_SPMM_STREAM_VARIANTS(BSP_SPMM_STREAM_MATCH)
 #undef BSP_SPMM_STREAM_MATCH
     return false;
 }
 
-inline int spmm_stream_lds_bytes(const SpmmStreamVariant& v) { return 64 * v.tile_n * v.sb + 2048 * v.sa; }
+inline int spmm_stream_lds_bytes(const SpmmStreamVariant& v) {
+    return v.pipes * (64 * v.tile_n * v.sb + 2048 * v.sa) + (v.pipes > 1 ? 4 * (v.tile_n / 128) * 16 * 64 * 4 : 0);
+}
 
 hipError_t launch_spmm_stream(const SpmmStreamArgs& a, const SpmmStreamVariant& v, bool out_bf16, int grid,
                               hipStream_t stream);
+
+// Whether an SpMM plan on A (R x C blocks) and N output columns runs the
+// persistent kernel, with which variant and workgroups per compute unit
+// (bsp_capi.cpp; environment overrides are read here, at plan creation).
+bool choose_spmm_stream(const bsp_bsr_desc* a, int64_t N, int cus, SpmmStreamVariant* sv, int* wpc);
+// Sets the calling thread's last-error message (bsp_last_error) and returns status.
+int record_error(int status, const std::string& msg);
 
 // Fused attention pair: the SpMM arguments with the mask as A (a = mask
 // values), V as B (b, ldb) and O as C (c, ldc), N = head dimension; plus Q and K.

@@ -398,7 +398,7 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
 }
 
 int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n, int wg_per_cu, SpmmStream& s,
-                      std::string& msg, int col_groups) {
+                      std::string& msg, int col_groups, int pipes) {
     int st = validate_bsr(a, msg);
     if (st != BSP_OK) return st;
     if (tile_n != 128 && tile_n != 256) {
@@ -415,6 +415,11 @@ int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n,
     }
     if (num_cus <= 0) num_cus = 256;
     if (wg_per_cu < 1) wg_per_cu = 1;
+    if (pipes != 1 && pipes != 2) {
+        msg = "pipelines per workgroup must be 1 or 2";
+        return BSP_ERR_UNSUPPORTED;
+    }
+    if (pipes == 2) wg_per_cu = 1;
     const int64_t RS = a->R / kSub, CS = a->C / kSub;
     const int64_t nsr = a->H / kSub;
     const int64_t n_tiles = N / tile_n;
@@ -498,25 +503,74 @@ int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n,
                     wg_units[(size_t)(cu + w * cus_per_xcd) * kNumXcd + x] = std::move(per_wg[w]);
             }
         }
-    // Streams, workgroup by workgroup (workgroup g = bin * kNumXcd + xcd).
-    s.wgs.resize(wg_units.size());
-    for (size_t g = 0; g < wg_units.size(); ++g) {
-        SpmmStreamWg& w = s.wgs[g];
+    // A part of a unit: entries [e0, e1) of the stripe's list (in the
+    // reference's order: blocks in CSR order, then the 32-column steps).
+    struct Part {
+        SpmmStreamUnit u;
+        int32_t e0, e1;
+    };
+    // Two pipelines: the compute unit's units, empty ones first, then longest
+    // first, concatenated and cut at ceil(total / 2).
+    auto halves = [&](const std::vector<SpmmStreamUnit>& us, std::vector<Part>& p0, std::vector<Part>& p1) {
+        std::vector<SpmmStreamUnit> order(us);
+        std::stable_sort(order.begin(), order.end(),
+                         [](const SpmmStreamUnit& x, const SpmmStreamUnit& y) { return (x.count > 0) < (y.count > 0); });
+        int64_t total = 0;
+        for (const SpmmStreamUnit& u : order) total += u.count;
+        const int64_t cut = (total + 1) / 2;
+        int64_t pos = 0;
+        for (const SpmmStreamUnit& u : order) {
+            const int64_t b = pos, e = pos + u.count;
+            if (e <= cut) {
+                p0.push_back({u, 0, u.count});
+            } else if (b >= cut) {
+                p1.push_back({u, 0, u.count});
+            } else {  // straddles the cut
+                SpmmStreamUnit a0 = u, a1 = u;
+                a0.count = (int32_t)(cut - b);
+                a0.pad = 2;
+                a1.count = (int32_t)(e - cut);
+                a1.pad = 1;
+                p0.push_back({a0, 0, a0.count});
+                p1.insert(p1.begin(), {a1, a0.count, u.count});
+            }
+            pos = e;
+        }
+    };
+    auto emit = [&](const std::vector<Part>& parts) {
+        SpmmStreamWg w{};
         w.w_begin = (int32_t)s.bw.size();
         w.u_begin = (int32_t)s.units.size();
-        w.n_units = (int32_t)wg_units[g].size();
-        for (const SpmmStreamUnit& u : wg_units[g]) {
-            s.units.push_back(u);
-            const int64_t i = u.row / RS, sub = u.row % RS;
+        w.n_units = (int32_t)parts.size();
+        for (const Part& pt : parts) {
+            s.units.push_back(pt.u);
+            const int64_t i = pt.u.row / RS, sub = pt.u.row % RS;
+            int64_t e = 0;
             for (int64_t blk = a->indptr[i]; blk < a->indptr[i + 1]; ++blk)
-                for (int64_t t = 0; t < CS; ++t) {
+                for (int64_t t = 0; t < CS; ++t, ++e) {
+                    if (e < pt.e0 || e >= pt.e1) continue;
                     const int64_t brow = (int64_t)a->indices[blk] * a->C + kSub * t;
-                    s.bw.push_back(brow | ((int64_t)u.n0 << 32));
+                    s.bw.push_back(brow | ((int64_t)pt.u.n0 << 32));
                     s.aw.push_back((uint32_t)((blk * a->R * a->C + kSub * sub * a->C + kSub * t) / kSub));
                 }
         }
         w.n = (int32_t)(s.bw.size() - w.w_begin);
         s.max_wg_entries = std::max(s.max_wg_entries, w.n);
+        s.wgs.push_back(w);
+    };
+    // Streams, workgroup by workgroup (workgroup g = bin * kNumXcd + xcd);
+    // with two pipelines, records 2g and 2g+1.
+    for (size_t g = 0; g < wg_units.size(); ++g) {
+        if (pipes == 1) {
+            std::vector<Part> parts;
+            for (const SpmmStreamUnit& u : wg_units[g]) parts.push_back({u, 0, u.count});
+            emit(parts);
+        } else {
+            std::vector<Part> p0, p1;
+            halves(wg_units[g], p0, p1);
+            emit(p0);
+            emit(p1);
+        }
     }
     s.n_entries = (int64_t)s.bw.size();
     s.bw.resize(s.bw.size() + kStreamPad, 0);

@@ -88,7 +88,8 @@ struct SpmmStreamUnit {
     int32_t row;    // stripe (32 output rows)
     int32_t n0;     // first output column
     int32_t count;  // entries (0: the stripe has no nonzeros; its tile is stored as zeros)
-    int32_t pad;
+    int32_t pad;    // 0: store the tile; two pipelines: 1 = this part goes to the
+                    // exchange buffer, 2 = add the exchange buffer, then store
 };
 static_assert(sizeof(SpmmStreamUnit) == 16, "SpmmStreamUnit layout is shared with the kernels");
 
@@ -115,8 +116,12 @@ struct SpmmStream {
 // (column groups of tiles, row groups of stripes, as xcd_tile_map) and, inside
 // an XCD, longest first onto the least-loaded workgroup.  Cost of a unit:
 // entries + store_cost.
+// pipes = 2: one workgroup per compute unit with two pipelines; the compute
+// unit's units (longest first) are concatenated and cut in half, the unit
+// that straddles the cut going to both pipelines (flag 2 on the first's part,
+// flag 1 on the second's).  wgs then holds two records per workgroup.
 int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n, int wg_per_cu,
-                      SpmmStream& s, std::string& msg, int col_groups = 0);
+                      SpmmStream& s, std::string& msg, int col_groups = 0, int pipes = 1);
 // Entries packed for the kernel: first row of B | (A offset / 32) << 32.
 std::vector<int64_t> spmm_packed_entries(const SpmmSchedule& s);
 // The split stripes in slot order (a split group contributes each of its

@@ -379,51 +379,83 @@ void check_spgemm(const Bsr& a, const Bsr& b, int cus, const std::string& name) 
 // XCD whose column group holds its tile; each unit's stream entries are the
 // stripe's products in the reference's order (blocks in CSR order, then the
 // 32-column steps of a block) with the right B row, column and A offset; the
-// workgroup streams are contiguous and their lengths add up.
-void check_spmm_stream(const Bsr& a, int64_t N, int cus, int tile_n, int wpc, const std::string& name) {
+// workgroup streams are contiguous and their lengths add up.  With two
+// pipelines, a compute unit's two streams differ by at most one entry, and a
+// unit cut between them is the first pipeline's last unit (flag 2) and the
+// second's first (flag 1), the two parts covering its entries once, in order.
+void check_spmm_stream(const Bsr& a, int64_t N, int cus, int tile_n, int wpc, const std::string& name, int pipes = 1) {
     SpmmStream s;
     std::string msg;
     const bsp_bsr_desc d = a.desc();
-    const int st = build_spmm_stream(&d, N, cus, tile_n, wpc, s, msg);
+    const int st = build_spmm_stream(&d, N, cus, tile_n, wpc, s, msg, 0, pipes);
     expect(st == BSP_OK, name + ": build (" + msg + ")");
     if (st != BSP_OK) return;
     const int64_t RS = a.R / kSub, CS = a.C / kSub, nsr = a.H / kSub, n_tiles = N / tile_n;
-    expect((int64_t)s.wgs.size() == (int64_t)(cus / kNumXcd) * wpc * kNumXcd, name + ": grid");
-    std::vector<int> seen(nsr * n_tiles, 0);
+    const int64_t grid = (int64_t)(cus / kNumXcd) * (pipes == 2 ? 1 : wpc) * kNumXcd;
+    expect((int64_t)s.wgs.size() == grid * pipes, name + ": grid");
+    std::vector<int> seen(nsr * n_tiles, 0);  // entries seen per unit (as a count of parts' coverage)
+    std::vector<int64_t> covered(nsr * n_tiles, 0);
     int64_t w = 0, u = 0;
     const int64_t tpg = n_tiles / s.col_groups;
-    for (size_t g = 0; g < s.wgs.size(); ++g) {
-        const SpmmStreamWg& wg = s.wgs[g];
+    for (size_t r = 0; r < s.wgs.size(); ++r) {
+        const SpmmStreamWg& wg = s.wgs[r];
+        const int64_t g = (int64_t)r / pipes, pipe = (int64_t)r % pipes;
         expect(wg.w_begin == w && wg.u_begin == u, name + ": contiguous streams");
         int64_t e = wg.w_begin, total = 0;
         for (int32_t j = 0; j < wg.n_units; ++j) {
             const SpmmStreamUnit& un = s.units[wg.u_begin + j];
             const int64_t tile = un.n0 / tile_n;
             expect(un.n0 % tile_n == 0 && tile < n_tiles && un.row < nsr, name + ": unit fields");
-            ++seen[un.row * n_tiles + tile];
-            // XCD g % 8 is column group (g % 8) % col_groups.
             expect(tile / tpg == (int64_t)((g % kNumXcd) % s.col_groups), name + ": unit on its column group's XCD");
             const int64_t i = un.row / RS, sub = un.row % RS;
-            expect(un.count == (a.indptr[i + 1] - a.indptr[i]) * CS, name + ": unit count");
+            const int64_t full = (a.indptr[i + 1] - a.indptr[i]) * CS;
+            int64_t e0 = 0, e1 = full;
+            if (un.pad == 0) {
+                expect(un.count == full, name + ": unit count");
+                ++seen[un.row * n_tiles + tile];
+            } else {
+                expect(pipes == 2, name + ": flags only with two pipelines");
+                expect(un.pad == 2 ? (pipe == 0 && j == wg.n_units - 1) : (pipe == 1 && j == 0),
+                       name + ": cut unit is the first pipeline's last and the second's first");
+                if (un.pad == 2) {
+                    e1 = un.count;
+                } else {
+                    e0 = full - un.count;
+                    ++seen[un.row * n_tiles + tile];
+                }
+            }
+            covered[un.row * n_tiles + tile] += e1 - e0;
+            int64_t idx = 0;
             for (int64_t blk = a.indptr[i]; blk < a.indptr[i + 1]; ++blk)
-                for (int64_t t = 0; t < CS; ++t, ++e) {
+                for (int64_t t = 0; t < CS; ++t, ++idx) {
+                    if (idx < e0 || idx >= e1) continue;
                     const int64_t brow = (int64_t)a.indices[blk] * a.C + kSub * t;
                     const int64_t aoff = blk * a.R * a.C + kSub * sub * a.C + kSub * t;
                     expect((s.bw[e] & 0xffffffffLL) == brow && (s.bw[e] >> 32) == un.n0, name + ": B word");
                     expect((int64_t)s.aw[e] * kSub == aoff, name + ": A word");
+                    ++e;
                 }
             total += un.count;
         }
         expect(total == wg.n && e == wg.w_begin + wg.n, name + ": stream length");
+        if (pipes == 2 && pipe == 1)
+            expect(s.wgs[r - 1].n - wg.n == 0 || s.wgs[r - 1].n - wg.n == 1, name + ": halves within one entry");
         w += wg.n;
         u += wg.n_units;
     }
     expect(std::all_of(seen.begin(), seen.end(), [](int v) { return v == 1; }), name + ": every unit once");
+    bool cov = true;
+    for (int64_t sr = 0; sr < nsr; ++sr)
+        for (int64_t t = 0; t < n_tiles; ++t) {
+            const int64_t i = sr / RS;
+            cov = cov && covered[sr * n_tiles + t] == (a.indptr[i + 1] - a.indptr[i]) * CS;
+        }
+    expect(cov, name + ": every entry of every unit once");
     expect(w == s.n_entries && (int64_t)s.bw.size() == w + kStreamPad && (int64_t)s.aw.size() == w + kStreamPad &&
                (int64_t)s.units.size() == u + kStreamPad,
            name + ": padding");
-    std::printf("%-34s units %6lld entries %8lld grid %zu cg %d max wg %d\n", name.c_str(), (long long)u,
-                (long long)s.n_entries, s.wgs.size(), s.col_groups, s.max_wg_entries);
+    std::printf("%-34s units %6lld entries %8lld grid %lld cg %d max wg %d\n", name.c_str(), (long long)u,
+                (long long)s.n_entries, (long long)grid, s.col_groups, s.max_wg_entries);
 }
 
 }  // namespace
@@ -454,6 +486,11 @@ int main() {
     check_spmm_stream(uniform(2048, 1024, 64, 128, 60, 7), 256, cus, 256, 1, "stream 64x128 blocks");
     check_spmm_stream(uniform(1024, 1024, 32, 32, 0, 9), 256, cus, 128, 1, "stream empty");
     check_spmm_stream(uniform(1024, 1024, 32, 32, 30, 9), 128, 8, 128, 2, "stream 8 CUs");
+    check_spmm_stream(uniform(4096, 4096, 32, 32, 4096, 1), 512, cus, 128, 1, "stream 25% two pipelines", 2);
+    check_spmm_stream(skewed(16384, 16384, 32, 32, 5243, 5), 1024, cus, 128, 1, "stream skewed two pipelines", 2);
+    check_spmm_stream(uniform(4096, 4096, 32, 32, 164, 3), 512, cus, 128, 1, "stream 1% two pipelines", 2);
+    check_spmm_stream(uniform(1024, 1024, 32, 32, 0, 9), 256, cus, 128, 1, "stream empty two pipelines", 2);
+    check_spmm_stream(uniform(1024, 1024, 32, 32, 30, 9), 128, 8, 128, 1, "stream 8 CUs two pipelines", 2);
     check_sddmm(uniform(4096, 4096, 32, 32, 1638, 10), 256, cus, "sddmm 4096^2 10% K=256");
     check_sddmm(skewed(2048, 2048, 64, 32, 300, 11), 128, cus, "sddmm 64x32 blocks, skewed");
     check_sddmm(uniform(1024, 1024, 128, 128, 20, 12), 64, cus, "sddmm 128x128 blocks");

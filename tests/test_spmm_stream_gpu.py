@@ -12,12 +12,13 @@ from helpers import W, assert_parity, bsr_of, capi, golden_spmm, run_spmm, spmm_
 pytestmark = pytest.mark.gpu
 
 # (tile, B ring, A ring, B loader waves) of BSP_SPMM_STREAM_VARIANTS in csrc/bsp_kernels.hpp
-STREAM_VARIANTS = [(128, 6, 12, 2), (128, 6, 12, 4), (128, 4, 16, 4), (128, 8, 16, 8), (256, 4, 16, 4), (256, 5, 16, 8),
-                   (256, 6, 8, 8)]
+# (tile, B ring, A ring, B loader waves, pipelines per workgroup)
+STREAM_VARIANTS = [(128, 6, 12, 2, 1), (128, 6, 12, 4, 1), (128, 4, 16, 4, 1), (128, 8, 16, 8, 1),
+                   (256, 4, 16, 4, 1), (256, 5, 16, 8, 1), (256, 6, 8, 8, 1), (128, 6, 12, 2, 2), (128, 5, 12, 2, 2)]
 
 
 def _lds(v):
-    return 64 * v[0] * v[1] + 2048 * v[2]
+    return v[4] * (64 * v[0] * v[1] + 2048 * v[2]) + (16384 * v[0] // 128 if v[4] > 1 else 0)
 
 
 def _stream_env(monkeypatch, v, wpc=None):
@@ -30,9 +31,10 @@ def _stream_env(monkeypatch, v, wpc=None):
 def _check(a, b, out_dtype, what, v=None, wpc=None):
     plan = capi.SpmmPlan(bsr_of(a), b.shape[1], out_dtype)
     info = plan.info()
-    assert info["persistent"] == 1, f"{what}: plan is not persistent ({info})"
+    assert info["persistent"] >= 1, f"{what}: plan is not persistent ({info})"
     if v is not None:
-        assert (info["tile_n"], info["stages"], info["a_stages"], info["waves"]) == (v[0], v[1], v[2], 5 + v[3])
+        assert (info["tile_n"], info["stages"], info["a_stages"], info["waves"], info["persistent"]) == \
+            (v[0], v[1], v[2], (5 + v[3]) * v[4], v[4])
     if wpc is not None:
         assert info["grid"] == 256 * wpc
     got = run_spmm(a, b, out_dtype, plan=plan)
@@ -48,7 +50,7 @@ def test_stream_variants(monkeypatch, v, density):
     """Every variant, with as many workgroups per compute unit as its LDS
     allows (one or two), both output types."""
     for wpc in (1, 2):
-        if wpc * _lds(v) > 160 * 1024:
+        if wpc * _lds(v) > 160 * 1024 or (v[4] > 1 and wpc > 1):
             continue
         _stream_env(monkeypatch, v, wpc)
         w = W.spmm_workload(2048, 2048, 512, 32, 32, density, seed=80 + wpc)
@@ -56,7 +58,7 @@ def test_stream_variants(monkeypatch, v, density):
             _check(w["a"], w["b"], od, f"variant={v} wpc={wpc} d={density} {od}", v, wpc)
 
 
-@pytest.mark.parametrize("v", [(128, 6, 12, 2), (256, 4, 16, 4)])
+@pytest.mark.parametrize("v", [(128, 6, 12, 2, 1), (256, 4, 16, 4, 1), (128, 6, 12, 2, 2)])
 def test_stream_many_units_per_workgroup(monkeypatch, v):
     """32768 rows x 1024 columns at 0.2%: 8192 or 4096 units on 256-512
     workgroups (16 per workgroup), many of them empty stripes, stored as zeros."""
@@ -67,7 +69,7 @@ def test_stream_many_units_per_workgroup(monkeypatch, v):
     _check(a, w["b"], "f32", f"many units {v}")
 
 
-@pytest.mark.parametrize("v", [(128, 6, 12, 2), (256, 5, 16, 8)])
+@pytest.mark.parametrize("v", [(128, 6, 12, 2, 1), (256, 5, 16, 8, 1), (128, 6, 12, 2, 2)])
 def test_stream_long_rows(monkeypatch, v):
     """A few rows of 200-400 entries (streams far longer than the ring and the
     word prefetch) among short ones."""
@@ -87,18 +89,22 @@ def test_stream_long_rows(monkeypatch, v):
 
 def test_stream_fewer_units_than_workgroups(monkeypatch):
     """A 64x128 problem: 2 units for 512 workgroups; the rest stream nothing."""
-    _stream_env(monkeypatch, (128, 6, 12, 2), 2)
+    _stream_env(monkeypatch, (128, 6, 12, 2, 1), 2)
     w = W.spmm_workload(64, 256, 128, 32, 32, 0.5, seed=93)
     _check(w["a"], w["b"], "f32", "2 units")
 
 
-def test_stream_empty_matrix(monkeypatch):
+@pytest.mark.parametrize("pipes", [1, 2])
+def test_stream_empty_matrix(monkeypatch, pipes):
     """No stored blocks: every unit is an empty stripe, every tile stored as zeros."""
-    _stream_env(monkeypatch, (128, 6, 12, 2))
+    _stream_env(monkeypatch, (128, 6, 12, 2, pipes))
     a = W.BsrArrays(1024, 1024, 32, 32, np.zeros(33, np.int32), np.zeros(0, np.int32))
     a.data = np.zeros(0, np.uint16)
     b = W.dense_content(1024, 256, "RAND", np.random.default_rng(94))
-    got = run_spmm(a, b, "f32")
+    plan = capi.SpmmPlan(bsr_of(a), 256, "f32")
+    assert plan.info()["persistent"] == pipes
+    got = run_spmm(a, b, "f32", plan=plan)
+    plan.close()
     assert np.all(got == 0.0)
 
 
@@ -106,6 +112,6 @@ def test_stream_empty_matrix(monkeypatch):
 def test_stream_other_block_shapes(monkeypatch, R, C):
     """Blocks other than 32x32 cut into 32-row stripes (no row groups)."""
     monkeypatch.setenv("BSP_SPMM_GROUP", "1")
-    _stream_env(monkeypatch, (128, 6, 12, 2))
+    _stream_env(monkeypatch, (128, 6, 12, 2, 2))
     w = W.spmm_workload(1536, 1536, 256, R, C, 0.2, seed=95 + R + C)
     _check(w["a"], w["b"], "f32", f"R={R} C={C}")
