@@ -261,6 +261,24 @@ int bsp_host_spgemm(const bsp_bsr_desc* a, const uint16_t* a_vals, const bsp_bsr
                     const uint16_t* b_vals, int32_t* out_indptr, int32_t* out_indices,
                     void* out_vals, int out_dtype, int device);
 
+/* ---- SpMM without device allocation ------------------------------------------
+ * No counterpart in the reference: an entry point for callers that cannot
+ * allocate device memory (serving loops that must not touch the allocator,
+ * harnesses that forbid hipMalloc).  C = A * B as bsp_spmm computes it (the
+ * same persistent kernel and schedule a plan would use), without a plan: the
+ * schedule is built on the host and staged in a static device array of
+ * BSP_NOALLOC_SCRATCH_BYTES that the library holds on every GPU it runs on
+ * until the process ends.  It calls no hipMalloc or hipFree.  The call waits
+ * for the schedule's copy on `stream` (and the stream's earlier work), then
+ * launches asynchronously.  Calls on one GPU share the array: two calls that
+ * overlap on one GPU race (order them on one stream, and let a launch finish
+ * before the next call from another stream).  A schedule above the limit
+ * returns BSP_ERR_UNSUPPORTED; so does N not a multiple of 128.
+ * a: host BSR structure; a_vals, b, c: device pointers as for bsp_spmm. */
+#define BSP_NOALLOC_SCRATCH_BYTES (16 << 20)
+int bsp_spmm_noalloc(const bsp_bsr_desc* a, const uint16_t* a_vals, const uint16_t* b, int64_t N,
+                     int64_t ldb, void* c, int64_t ldc, int out_dtype, int device, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

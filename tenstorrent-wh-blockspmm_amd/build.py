@@ -31,7 +31,7 @@ HIP_FLAGS = [
     "-Wall",
 ]
 
-SOURCES = ["bsp_kernels.hip", "bsp_capi.cpp", "bsp_schedule.cpp"]
+SOURCES = ["bsp_kernels.hip", "bsp_capi.cpp", "bsp_schedule.cpp", "bsp_noalloc.hip"]
 
 
 def _run(cmd: list[str]) -> None:

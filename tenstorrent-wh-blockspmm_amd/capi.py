@@ -95,7 +95,10 @@ SIGNATURES = {
     "bsp_spgemm_structure": (c_int, [c_void_p, _I64P, _I32P, _I32P]),
     "bsp_spgemm": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "bsp_host_spgemm": (c_int, [_DESC_P, c_void_p, _DESC_P, c_void_p, _I32P, _I32P, c_void_p, c_int, c_int]),
+    "bsp_spmm_noalloc": (c_int, [_DESC_P, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int, c_int,
+                                 c_void_p]),
 }
+NOALLOC_SCRATCH_BYTES = 16 << 20  # BSP_NOALLOC_SCRATCH_BYTES of include/bsparse.h
 
 _lib: Optional[ctypes.CDLL] = None
 

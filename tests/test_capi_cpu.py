@@ -392,3 +392,22 @@ def test_library_first_then_torch_shares_one_hip_runtime():
         "print('ok', float(x.sum()))\n" % str(REPO))
     p = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
     assert p.returncode == 0 and "ok 4.0" in p.stdout, p.stdout[-2000:] + p.stderr[-2000:]
+
+
+def test_noalloc_rejects_a_schedule_above_its_scratch_before_any_device_work():
+    """bsp_spmm_noalloc checks its schedule against BSP_NOALLOC_SCRATCH_BYTES
+    (and N against its tile) before it touches a device: 1M blocks times two
+    tiles need about 24 MB of entry words."""
+    nbr = 1024
+    indptr = np.arange(nbr + 1, dtype=np.int32) * 1024
+    indices = np.tile(np.arange(1024, dtype=np.int32), nbr)
+    d = capi.Bsr(nbr * 32, 1024 * 32, 32, 32, indptr, indices).desc()
+    lib = capi.load()
+    buf = ctypes.c_void_p(16)  # never dereferenced: the call fails before any device work
+    st = lib.bsp_spmm_noalloc(ctypes.byref(d), buf, buf, 256, 256, buf, 256, capi.DTYPE_F32, 0, None)
+    assert st == capi.BSP_ERR_UNSUPPORTED
+    assert "no-allocation scratch" in capi.last_error()
+    small = capi.Bsr(64, 64, 32, 32, np.array([0, 1, 1], np.int32), np.array([0], np.int32)).desc()
+    st = lib.bsp_spmm_noalloc(ctypes.byref(small), buf, buf, 96, 96, buf, 96, capi.DTYPE_F32, 0, None)
+    assert st == capi.BSP_ERR_UNSUPPORTED and "multiple of 128" in capi.last_error()
+    assert capi.NOALLOC_SCRATCH_BYTES == 16 << 20
