@@ -6,6 +6,7 @@ this file; tests, bench.py and the C++ host tools load it from there.
 from __future__ import annotations
 
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -34,11 +35,27 @@ HIP_FLAGS = [
 SOURCES = ["bsp_kernels.hip", "bsp_capi.cpp", "bsp_schedule.cpp", "bsp_noalloc.hip"]
 
 
-def _run(cmd: list[str]) -> None:
+def _run(cmd: list[str]) -> str:
     proc = subprocess.run(cmd, cwd=str(PKG_DIR), capture_output=True, text=True)
     if proc.returncode != 0:
         sys.stderr.write(proc.stdout + proc.stderr)
         raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}")
+    return proc.stderr
+
+
+def check_no_scratch(remarks: str, src: str) -> None:
+    """Fails the build when a kernel of `src` spills to scratch memory (the
+    compiler's kernel-resource-usage remarks report ScratchSize per kernel)."""
+    spills, name = [], None
+    for line in remarks.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and int(m.group(1)) > 0:
+            spills.append(f"{name}: {m.group(1)} bytes/lane")
+    if spills:
+        raise RuntimeError(f"{src}: kernels spill to scratch:\n  " + "\n  ".join(spills))
 
 
 def build_library(verbose: bool = False) -> Path:
@@ -50,11 +67,13 @@ def build_library(verbose: bool = False) -> Path:
     objs = []
     for src in SOURCES:
         obj = build_dir / (src + ".o")
-        lang = ["-x", "hip"] if src.endswith(".hip") else []
+        lang = ["-x", "hip", "-Rpass-analysis=kernel-resource-usage"] if src.endswith(".hip") else []
         cmd = [HIPCC, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", *lang, "-c", str(CSRC / src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd))
-        _run(cmd)
+        remarks = _run(cmd)
+        if src.endswith(".hip"):
+            check_no_scratch(remarks, src)
         objs.append(str(obj))
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)]

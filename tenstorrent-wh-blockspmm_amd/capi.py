@@ -187,14 +187,57 @@ def validate(bsr: Bsr) -> int:
 
 
 def _ptr(x) -> Optional[int]:
-    """Device/host address of a torch tensor or numpy array (or an int)."""
+    """Address of a torch tensor (or a raw device address given as an int)."""
     if x is None:
         return None
     if isinstance(x, int):
         return x
-    if isinstance(x, np.ndarray):
-        return x.ctypes.data
     return x.data_ptr()
+
+
+def _operand(x, name: str, esize: int, rows: int, cols: int, ld: Optional[int], device: int):
+    """Checks a device operand of `rows` x `cols` elements of `esize` bytes
+    with row stride `ld` (elements) and returns (address, ld).
+
+    A torch tensor must live on the plan's GPU, hold elements of `esize`
+    bytes, have unit stride along its last dimension and cover
+    (rows - 1) * ld + cols elements from its first one; a 2-D tensor's row
+    stride is its stride(0) unless `ld` is given (they must then agree).  A
+    raw int is taken as a device address as is (the caller vouches for it).
+    Host arrays are refused: the kernels would read them as device addresses."""
+    if x is None:
+        raise ValueError(f"{name}: a device tensor is required")
+    if isinstance(x, int):
+        return x, (ld if ld is not None else cols)
+    if isinstance(x, np.ndarray):
+        raise TypeError(f"{name}: a numpy array is host memory; pass a torch tensor on the GPU")
+    if not hasattr(x, "data_ptr") or not hasattr(x, "is_cuda"):
+        raise TypeError(f"{name}: expected a torch tensor, got {type(x).__name__}")
+    if not x.is_cuda:
+        raise ValueError(f"{name}: tensor is on {x.device}, not on a GPU")
+    if x.device.index is not None and x.device.index != device:
+        raise ValueError(f"{name}: tensor is on cuda:{x.device.index}, the plan on device {device}")
+    if x.element_size() != esize:
+        raise ValueError(f"{name}: elements of {x.element_size()} bytes, expected {esize}")
+    if x.dim() >= 1 and x.numel() > 0 and x.stride(-1) != 1:
+        raise ValueError(f"{name}: the last dimension must be contiguous (stride 1), got stride {x.stride(-1)}")
+    if x.dim() == 2:
+        if x.shape[1] < cols and rows > 1:
+            raise ValueError(f"{name}: {x.shape[1]} columns, need {cols}")
+        st0 = x.stride(0)
+        if ld is None:
+            ld = st0 if x.shape[0] > 1 else cols
+        elif x.shape[0] > 1 and ld != st0:
+            raise ValueError(f"{name}: ld = {ld} but the tensor's row stride is {st0}")
+    elif ld is None:
+        ld = cols
+    if x.dim() > 2:
+        raise ValueError(f"{name}: expected a 1-D or 2-D tensor")
+    need = (rows - 1) * ld + cols if rows > 0 and cols > 0 else 0
+    avail = x.untyped_storage().nbytes() // esize - x.storage_offset()
+    if need > avail:
+        raise ValueError(f"{name}: covers {avail} elements from its start, the operand needs {need}")
+    return x.data_ptr(), ld
 
 
 def _dtype_code(out_dtype) -> int:
@@ -237,15 +280,21 @@ class SpmmPlan(_Plan):
 
     def __init__(self, bsr: Bsr, N: int, out_dtype="f32", device: int = 0):
         super().__init__()
-        self.bsr, self.N, self.out_dtype = bsr, int(N), _dtype_code(out_dtype)
+        self.bsr, self.N, self.out_dtype, self.device = bsr, int(N), _dtype_code(out_dtype), device
         d = bsr.desc()
         check(load().bsp_spmm_plan_create(ctypes.byref(self._h), ctypes.byref(d), self.N, ROW_MAJOR,
                                           self.out_dtype, device))
 
     def run(self, a_vals, b, c, ldb: Optional[int] = None, ldc: Optional[int] = None,
             stream: Optional[int] = None) -> None:
-        check(load().bsp_spmm(self.handle, _ptr(a_vals), _ptr(b), ldb or self.N, _ptr(c),
-                              ldc or self.N, stream))
+        """a_vals: nblocks*R*C bf16; b: K x N bf16; c: M x N fp32 or bf16 (as
+        planned); torch tensors on the plan's GPU (row strides from stride(0))."""
+        bs = self.bsr
+        nv = bs.nblocks * bs.R * bs.C
+        pa = _operand(a_vals, "a_vals", 2, 1, nv, nv, self.device)[0] if nv else _ptr(a_vals)
+        pb, ldb = _operand(b, "b", 2, bs.W, self.N, ldb, self.device)
+        pc, ldc = _operand(c, "c", 4 if self.out_dtype == DTYPE_F32 else 2, bs.H, self.N, ldc, self.device)
+        check(load().bsp_spmm(self.handle, pa, pb, ldb, pc, ldc, stream))
 
 
 class SddmmPlan(_Plan):
@@ -253,7 +302,7 @@ class SddmmPlan(_Plan):
 
     def __init__(self, mask: Bsr, K: int, y_layout: int = ROW_MAJOR, out_dtype="f32", device: int = 0):
         super().__init__()
-        self.mask, self.K, self.y_layout = mask, int(K), int(y_layout)
+        self.mask, self.K, self.y_layout, self.device = mask, int(K), int(y_layout), device
         self.out_dtype = _dtype_code(out_dtype)
         d = mask.desc()
         check(load().bsp_sddmm_plan_create(ctypes.byref(self._h), ctypes.byref(d), self.K, self.y_layout,
@@ -261,10 +310,20 @@ class SddmmPlan(_Plan):
 
     def run(self, mask_vals, x, y, out_vals, ldx: Optional[int] = None, ldy: Optional[int] = None,
             stream: Optional[int] = None) -> None:
-        if ldy is None:
-            ldy = self.mask.W if self.y_layout == ROW_MAJOR else self.K
-        check(load().bsp_sddmm(self.handle, _ptr(mask_vals), _ptr(x), ldx or self.K, _ptr(y), ldy,
-                               _ptr(out_vals), stream))
+        """mask_vals: nblocks*R*C bf16; x: M x K bf16; y: K x N (ROW_MAJOR) or
+        N x K (COL_MAJOR) bf16; out_vals: nblocks*R*C fp32 or bf16; torch
+        tensors on the plan's GPU."""
+        m = self.mask
+        nv = m.nblocks * m.R * m.C
+        if nv == 0:
+            check(load().bsp_sddmm(self.handle, None, None, 0, None, 0, None, stream))
+            return
+        pm = _operand(mask_vals, "mask_vals", 2, 1, nv, nv, self.device)[0]
+        px, ldx = _operand(x, "x", 2, m.H, self.K, ldx, self.device)
+        yr, yc = (self.K, m.W) if self.y_layout == ROW_MAJOR else (m.W, self.K)
+        py, ldy = _operand(y, "y", 2, yr, yc, ldy, self.device)
+        po = _operand(out_vals, "out_vals", 4 if self.out_dtype == DTYPE_F32 else 2, 1, nv, nv, self.device)[0]
+        check(load().bsp_sddmm(self.handle, pm, px, ldx, py, ldy, po, stream))
 
 
 class AttentionPlan(_Plan):
@@ -273,16 +332,23 @@ class AttentionPlan(_Plan):
 
     def __init__(self, mask: Bsr, head_dim: int, out_dtype="f32", device: int = 0):
         super().__init__()
-        self.mask, self.d, self.out_dtype = mask, int(head_dim), _dtype_code(out_dtype)
+        self.mask, self.d, self.out_dtype, self.device = mask, int(head_dim), _dtype_code(out_dtype), device
         dsc = mask.desc()
         check(load().bsp_attention_plan_create(ctypes.byref(self._h), ctypes.byref(dsc), self.d,
                                                self.out_dtype, device))
 
     def run(self, mask_vals, q, k, v, out, ldq: Optional[int] = None, ldk: Optional[int] = None,
             ldv: Optional[int] = None, ldo: Optional[int] = None, stream: Optional[int] = None) -> None:
-        d = self.d
-        check(load().bsp_attention(self.handle, _ptr(mask_vals), _ptr(q), ldq or d, _ptr(k), ldk or d,
-                                   _ptr(v), ldv or d, _ptr(out), ldo or d, stream))
+        """mask_vals: nblocks*R*C bf16; q: queries x d, k and v: keys x d bf16;
+        out: queries x d fp32 or bf16; torch tensors on the plan's GPU."""
+        m, d = self.mask, self.d
+        nv = m.nblocks * m.R * m.C
+        pm = _operand(mask_vals, "mask_vals", 2, 1, nv, nv, self.device)[0] if nv else _ptr(mask_vals)
+        pq, ldq = _operand(q, "q", 2, m.H, d, ldq, self.device)
+        pk, ldk = _operand(k, "k", 2, m.W, d, ldk, self.device)
+        pv, ldv = _operand(v, "v", 2, m.W, d, ldv, self.device)
+        po, ldo = _operand(out, "out", 4 if self.out_dtype == DTYPE_F32 else 2, m.H, d, ldo, self.device)
+        check(load().bsp_attention(self.handle, pm, pq, ldq, pk, ldk, pv, ldv, po, ldo, stream))
 
 
 def _structure(fn, nbrows: int, *args):
@@ -309,7 +375,7 @@ class SpgemmPlan(_Plan):
 
     def __init__(self, a: Bsr, b: Bsr, out_dtype="f32", device: int = 0):
         super().__init__()
-        self.a, self.b, self.out_dtype = a, b, _dtype_code(out_dtype)
+        self.a, self.b, self.out_dtype, self.device = a, b, _dtype_code(out_dtype), device
         da, db = a.desc(), b.desc()
         check(load().bsp_spgemm_plan_create(ctypes.byref(self._h), ctypes.byref(da), ctypes.byref(db),
                                             self.out_dtype, device))
@@ -321,7 +387,14 @@ class SpgemmPlan(_Plan):
         return self.structure.nblocks * self.a.R * self.b.C
 
     def run(self, a_vals, b_vals, out_vals, stream: Optional[int] = None) -> None:
-        check(load().bsp_spgemm(self.handle, _ptr(a_vals), _ptr(b_vals), _ptr(out_vals), stream))
+        """a_vals, b_vals: the operands' block values (bf16); out_vals:
+        out_values fp32 or bf16; torch tensors on the plan's GPU."""
+        na, nb, no = self.a.nblocks * self.a.R * self.a.C, self.b.nblocks * self.b.R * self.b.C, self.out_values
+        pa = _operand(a_vals, "a_vals", 2, 1, na, na, self.device)[0] if na else _ptr(a_vals)
+        pb = _operand(b_vals, "b_vals", 2, 1, nb, nb, self.device)[0] if nb else _ptr(b_vals)
+        po = _operand(out_vals, "out_vals", 4 if self.out_dtype == DTYPE_F32 else 2, 1, no, no, self.device)[0] \
+            if no else _ptr(out_vals)
+        check(load().bsp_spgemm(self.handle, pa, pb, po, stream))
 
 
 def _schedule(fn_name: str, bsr: Bsr, n: int, num_cus: int) -> dict:

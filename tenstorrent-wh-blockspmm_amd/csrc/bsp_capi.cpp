@@ -140,12 +140,13 @@ void fill_info_spmm(const bsp::SpmmSchedule& s, bsp_plan_info* info) {
     info->stages = v.stages;
     info->group = s.group;
     // Row groups on 256-column tiles run eight waves (two per SIMD) unless
-    // BSP_SPMM_WIDE_WAVES=4 asks for four; read here, once, so that a plan
+    // BSP_SPMM_WIDE_WAVES=4 asks for four (groups of 2 or 4 stripes only: four
+    // waves holding 8 stripes spill); read here, once, so that a plan
     // launches the same kernel every time (a captured graph included).
     info->waves = 4;
     if (s.group > 1 && s.tile_n == 256) {
         const char* ww = std::getenv("BSP_SPMM_WIDE_WAVES");
-        info->waves = (ww && std::atoi(ww) == 4) ? 4 : 8;
+        info->waves = (ww && std::atoi(ww) == 4 && s.group != 8) ? 4 : 8;
     }
     info->workspace_bytes =
         (int64_t)s.n_slots * s.n_tiles * bsp::spmm_partial_floats(s.tile_n) * (int64_t)sizeof(float);

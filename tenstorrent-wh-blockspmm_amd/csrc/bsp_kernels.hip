@@ -1943,9 +1943,11 @@ static void launch_spmm_t(const SpmmArgs& a, bool out_bf16, int grid, int n_spli
             hipLaunchKernelGGL((spmm_kernel<NTW, S, false>), dim3(grid), dim3(256), 0, stream, a);
     } else if constexpr (NTW == 2) {
         // Eight waves (two per SIMD, 32*RW/2 x 64 outputs each), or four as the
-        // plan fixed; A fetched in entry pairs when C is a multiple of 64 (the
-        // plan then starts every item at an even entry of its block).
-        const bool four = waves == 4;
+        // plan fixed (not at RW = 8: four waves of 256 accumulators each spill
+        // there); A fetched in entry pairs when C is a multiple of 64 (the plan
+        // then starts every item at an even entry of its block).
+        constexpr bool four_ok = G != 8;
+        const bool four = four_ok && waves == 4;
         const bool pair = a.lda % 64 == 0;
 #define BSP_WIDE(NW_, PAIR_)                                                                                  \
     do {                                                                                                      \
@@ -1956,10 +1958,15 @@ static void launch_spmm_t(const SpmmArgs& a, bool out_bf16, int grid, int n_spli
             hipLaunchKernelGGL((spmm_group_wide_kernel<G, S, false, NW_, PAIR_>), dim3(grid), dim3(64 * NW_), 0, \
                                stream, a);                                                                    \
     } while (0)
-        if (four) {
-            if (pair) BSP_WIDE(4, true);
-            else BSP_WIDE(4, false);
-        } else {
+        bool launched = false;
+        if constexpr (four_ok) {
+            if (four) {
+                if (pair) BSP_WIDE(4, true);
+                else BSP_WIDE(4, false);
+                launched = true;
+            }
+        }
+        if (!launched) {
             if (pair) BSP_WIDE(8, true);
             else BSP_WIDE(8, false);
         }

@@ -138,9 +138,12 @@ inline int64_t spmm_partial_floats(int tile_n) { return (int64_t)tile_n * 32; }
 
 // Compiled SpMM kernel variants: workgroup tile width (4 waves of 32 or 64
 // columns), ring depth (entries in flight + 1) and row group (32-row stripes
-// of one block row per workgroup; groups use 128-column tiles).  LDS per
-// workgroup = (2 KB * group + 64 * tile_n bytes) * stages; two workgroups
-// share a compute unit while that is at most 80 KB.
+// of one block row per workgroup; groups take 128-column tiles, or 256 in the
+// wide group kernel).  LDS per workgroup = (2 KB * group + 64 * tile_n bytes)
+// * stages, except that the wide kernel fetching A in entry pairs (C a
+// multiple of 64) keeps 2 * (stages / 2 + 1) A slots: group 8 with three
+// stages takes 112 KB, not 96.  Two workgroups share a compute unit while
+// that is at most 80 KB (the wide kernel: groups of 2 and 4 with three stages).
 #define BSP_SPMM_VARIANTS(X) \
     X(128, 4, 1)             \
     X(128, 6, 1)             \

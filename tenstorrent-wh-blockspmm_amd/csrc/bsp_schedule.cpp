@@ -233,8 +233,9 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
     if (group != 1 && group != 2 && group != 4 && group != 8) group = 1;
     if (RS % group != 0) group = 1;
     s.group = group;
-    // Row groups take 256-column tiles (the wide group kernel, one workgroup
-    // per compute unit) when N is a multiple of 256 and the groups' tiles
+    // Row groups take 256-column tiles (the wide group kernel: two workgroups
+    // per compute unit for groups of 2 and 4 with a three-stage ring, else
+    // one) when N is a multiple of 256 and the groups' tiles
     // still fill every compute unit, else 128-column tiles.
     // (BSP_SPMM_WIDE_GROUP: 0 never, 2 whenever N allows it.)
     if (group > 1) {

@@ -411,3 +411,55 @@ def test_noalloc_rejects_a_schedule_above_its_scratch_before_any_device_work():
     st = lib.bsp_spmm_noalloc(ctypes.byref(small), buf, buf, 96, 96, buf, 96, capi.DTYPE_F32, 0, None)
     assert st == capi.BSP_ERR_UNSUPPORTED and "multiple of 128" in capi.last_error()
     assert capi.NOALLOC_SCRATCH_BYTES == 16 << 20
+
+
+class _OnGpu:
+    """A CPU tensor presented as if it lived on cuda:`index` (the binding's
+    operand checks read only these attributes), so that the checks run
+    without a GPU."""
+
+    def __init__(self, t, index=0):
+        self._t, self._i = t, index
+        self.is_cuda = True
+        self.shape = t.shape
+
+    @property
+    def device(self):
+        import torch
+        return torch.device("cuda", self._i)
+
+    def __getattr__(self, name):
+        return getattr(self._t, name)
+
+
+def test_binding_refuses_host_memory_and_mismatched_tensors():
+    """The ctypes binding's run() operands: host arrays, CPU tensors, tensors on
+    another GPU, wrong element size, a strided last dimension, a row stride
+    that disagrees with ld, and a tensor too small for its operand are refused
+    before anything reaches the library; a 2-D tensor's row stride becomes ld."""
+    import torch
+    op = capi._operand
+    with pytest.raises(TypeError, match="numpy array is host memory"):
+        op(np.zeros((4, 8), np.uint16), "b", 2, 4, 8, None, 0)
+    with pytest.raises(ValueError, match="not on a GPU"):
+        op(torch.zeros((4, 8), dtype=torch.int16), "b", 2, 4, 8, None, 0)
+    with pytest.raises(ValueError, match="the plan on device 0"):
+        op(_OnGpu(torch.zeros((4, 8), dtype=torch.int16), 1), "b", 2, 4, 8, None, 0)
+    with pytest.raises(ValueError, match="elements of 4 bytes, expected 2"):
+        op(_OnGpu(torch.zeros((4, 8), dtype=torch.float32)), "b", 2, 4, 8, None, 0)
+    with pytest.raises(ValueError, match="last dimension must be contiguous"):
+        op(_OnGpu(torch.zeros((8, 4), dtype=torch.int16).t()), "b", 2, 4, 8, None, 0)
+    with pytest.raises(ValueError, match="row stride is 16"):
+        op(_OnGpu(torch.zeros((4, 16), dtype=torch.int16)), "b", 2, 4, 8, 8, 0)
+    with pytest.raises(ValueError, match="need 8"):
+        op(_OnGpu(torch.zeros((4, 6), dtype=torch.int16)), "b", 2, 4, 8, None, 0)
+    with pytest.raises(ValueError, match="covers 30 elements"):
+        op(_OnGpu(torch.zeros(30, dtype=torch.int16)), "a_vals", 2, 1, 32, 32, 0)
+    # a view that starts inside its storage: coverage counts from the view's start
+    base = torch.zeros((5, 16), dtype=torch.int16)
+    with pytest.raises(ValueError, match="covers"):
+        op(_OnGpu(base[2:]), "b", 2, 4, 16, None, 0)
+    # accepted: the row stride of a wider tensor becomes ld
+    t = torch.zeros((4, 24), dtype=torch.int16)
+    addr, ld = op(_OnGpu(t[:, :16]), "b", 2, 4, 16, None, 0)
+    assert ld == 24 and addr == t.data_ptr()

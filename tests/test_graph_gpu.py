@@ -81,12 +81,12 @@ def test_graph_keeps_the_plans_kernel_after_an_environment_change(monkeypatch, w
     gives the eager result bit for bit."""
     import torch
     monkeypatch.setenv("BSP_SPMM_WIDE_WAVES", str(waves))
-    monkeypatch.setenv("BSP_SPMM_GROUP", "8")
+    monkeypatch.setenv("BSP_SPMM_GROUP", "4")
     monkeypatch.setenv("BSP_SPMM_WIDE_GROUP", "2")
-    w = W.spmm_workload(2048, 2048, 512, 256, 256, 0.25, seed=33)
+    w = W.spmm_workload(2048, 2048, 512, 128, 128, 0.25, seed=33)
     a = w["a"]
     plan = capi.SpmmPlan(bsr_of(a), 512, "f32")
-    assert plan.info()["waves"] == waves and plan.info()["group"] == 8
+    assert plan.info()["waves"] == waves and plan.info()["group"] == 4
     da, db = _dev(torch, a.data), _dev(torch, w["b"])
     eager = torch.empty((2048, 512), dtype=torch.float32, device="cuda")
     plan.run(da, db, eager, stream=torch.cuda.current_stream().cuda_stream)

@@ -71,3 +71,20 @@ def test_spgemm_host_mirror_on_gpu():
     p = _run([_tool("test_spgemm"), "-1", "0"], 300)
     assert p.returncode == 0, p.stdout[-3000:] + p.stderr[-2000:]
     assert "Passed: 10 / 10" in p.stdout
+
+
+def test_build_fails_on_kernels_that_spill():
+    """The build reads the compiler's kernel-resource-usage remarks and stops
+    at any kernel with a nonzero ScratchSize (a kernel that spills runs far
+    below its roofline without any other sign)."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("bsp_build", REPO / "tenstorrent-wh-blockspmm_amd" / "build.py")
+    build = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(build)
+    clean = ("remark: k.hip:1:0: Function Name: _Z1av [-Rpass-analysis=kernel-resource-usage]\n"
+             "remark: k.hip:1:0:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]\n")
+    build.check_no_scratch(clean, "k.hip")
+    spill = clean + ("remark: k.hip:9:0: Function Name: _Z1bv [-Rpass-analysis=kernel-resource-usage]\n"
+                     "remark: k.hip:9:0:     ScratchSize [bytes/lane]: 132 [-Rpass-analysis=kernel-resource-usage]\n")
+    with pytest.raises(RuntimeError, match=r"_Z1bv: 132 bytes/lane"):
+        build.check_no_scratch(spill, "k.hip")

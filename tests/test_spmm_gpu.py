@@ -323,6 +323,13 @@ def test_row_group_chosen_for_large_blocks(R):
     sub = W.BsrArrays(rows, a.W, R, R, np.ascontiguousarray(a.indptr[:rows // R + 1]),
                       a.indices[:nb], a.data[:nb * R * R])
     assert_parity(got[:rows], golden_spmm(sub, w["b"]), spmm_k_eff(sub), f"8192^3 R={R} prefix")
+    # Every row, on a column slice: output column j depends only on column j
+    # of B, so the oracle on B's first 64 columns checks all 8192 rows of the
+    # default plan (two workgroups per compute unit, reversed second rounds,
+    # the row-band map) at a small cost.
+    cols = 64
+    gold = golden_spmm(a, np.ascontiguousarray(w["b"][:, :cols]))
+    assert_parity(got[:, :cols], gold, spmm_k_eff(a), f"8192^3 R={R} all rows, columns 0..{cols - 1}")
 
 
 @pytest.mark.parametrize("R,C", [(256, 256), (256, 128), (256, 64), (256, 32), (128, 128), (128, 64), (128, 32),
@@ -346,6 +353,7 @@ def test_row_group_wide_tile(monkeypatch, R, C, waves, split, out_dtype):
     plan = capi.SpmmPlan(bsr_of(w["a"]), 512, out_dtype)
     info = plan.info()
     assert info["group"] == R // 32 and info["tile_n"] == 256
+    assert info["waves"] == (8 if R == 256 else waves)  # four waves of eight stripes would spill
     assert (info["n_split_rows"] > 0) == bool(split)
     got = run_spmm(w["a"], w["b"], out_dtype, plan=plan)
     again = run_spmm(w["a"], w["b"], out_dtype, plan=plan)
@@ -353,3 +361,23 @@ def test_row_group_wide_tile(monkeypatch, R, C, waves, split, out_dtype):
     assert_parity(got, golden_spmm(w["a"], w["b"]), spmm_k_eff(w["a"]),
                   f"wide group R={R} C={C} waves={waves} split={split} {out_dtype}")
     np.testing.assert_array_equal(got, again)
+
+
+@pytest.mark.parametrize("R,stages", [(256, 3), (256, 4), (128, 3), (64, 3)])
+@pytest.mark.parametrize("split", [0, 3])
+def test_row_group_wide_ring_depths(monkeypatch, R, stages, split):
+    """Every compiled (group, ring depth) of the 256-column group kernel,
+    forced through BSP_SPMM_STAGES, among them the odd three-stage ring of
+    eight-stripe groups (two entry-pair slots), with and without split rows."""
+    monkeypatch.setenv("BSP_SPMM_GROUP", str(R // 32))
+    monkeypatch.setenv("BSP_SPMM_WIDE_GROUP", "2")
+    monkeypatch.setenv("BSP_SPMM_STAGES", str(stages))
+    monkeypatch.setenv("BSP_SPMM_SPLIT", str(split or 100000))
+    w = W.spmm_workload(2048, 2048, 512, R, R, 0.3, seed=110 + R + stages + split)
+    plan = capi.SpmmPlan(bsr_of(w["a"]), 512, "f32")
+    info = plan.info()
+    assert (info["group"], info["tile_n"], info["stages"]) == (R // 32, 256, stages)
+    assert (info["n_split_rows"] > 0) == bool(split)
+    got = run_spmm(w["a"], w["b"], "f32", plan=plan)
+    plan.close()
+    assert_parity(got, golden_spmm(w["a"], w["b"]), spmm_k_eff(w["a"]), f"R={R} stages={stages} split={split}")
