@@ -192,32 +192,20 @@ __device__ __forceinline__ u32x4 ld_tr_b16(const uint8_t* lds) {
 
 }  // namespace spmm_detail
 
-// Output stores write through the L2 (agent scope: a relaxed atomic store at
-// agent scope is a global store with sc1 on gfx950).  The output is written
-// once and never read by the kernel; written through, it streams out while
-// the kernel runs instead of being written back from every XCD's L2 at the
-// kernel's end.  8 MB of fp32 tiles from 512 workgroups, per launch in a
-// graph: plain or non-temporal stores 2.98 us, write-through 2.40 us (32 MB:
-// 7.0-7.2 -> 5.7 us).
-// A write-through store completes only when it has left the L2, so a wave
-// that waits on vmcnt for loads issued after its stores (the SpGEMM ring)
-// waits for that too: such a kernel stores with store_out_nt instead
-// (non-temporal, completing at the L2; SpGEMM 8192^2 fp32: 108 -> 28 us).
+// Output stores are non-temporal (global stores with nt: streamed through the
+// L2 without displacing the operands it holds, completing at the L2).  The
+// output is written once and never read by the kernel.  Against write-through
+// stores (sc1: a store that completes only when it has left the L2), measured
+// in one process on one MI355X, graph replay of the persistent SpMM kernel
+// with cold operands: 4096^2 x 512 fp32 C at 1% 5.50 -> 3.88 us, 5%
+// 6.29 -> 5.97 us, 25% 14.40 -> 14.10 us; the skewed 16384^2 x 1024 workload
+// 43.3 -> 39.7 us; the attention SDDMM 6.93 -> 6.55 us; the group kernels and
+// the fused attention kernel within 1%.  A wave that waits on vmcnt for loads
+// issued after its stores (the SpGEMM ring) would also wait for write-through
+// stores to leave the L2 (SpGEMM 8192^2 fp32: 108 us with them, 28 us with
+// non-temporal stores).
 template <typename T>
 __device__ __forceinline__ void store_out(T* p, T v) {
-    if constexpr (sizeof(T) <= 8) {
-        __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-        static_assert(sizeof(T) == 16, "16-byte or scalar stores");
-        const uint64_t* w = (const uint64_t*)&v;
-        uint64_t* d = (uint64_t*)p;
-        __hip_atomic_store(d, w[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(d + 1, w[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-}
-
-template <typename T>
-__device__ __forceinline__ void store_out_nt(T* p, T v) {
     __builtin_nontemporal_store(v, p);
 }
 
@@ -1589,9 +1577,9 @@ __global__ __launch_bounds__(256) void sddmm_kernel(SddmmArgs p) {
                 const float val = sum * bf16_to_f32((uint16_t)mcur[j]);
                 const int64_t idx = off + (int64_t)(8 * wave + 4 * q + j) * p.ldo + l32;
                 if (OUT_BF16)
-                    store_out_nt(&((uint16_t*)p.out)[idx], f32_to_bf16_rne(val));
+                    store_out(&((uint16_t*)p.out)[idx], f32_to_bf16_rne(val));
                 else
-                    store_out_nt(&((float*)p.out)[idx], val);
+                    store_out(&((float*)p.out)[idx], val);
             }
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
@@ -1928,7 +1916,7 @@ __global__ __launch_bounds__(256) void spgemm_kernel(SpgemmArgs p) {
             const u32x4 val = *(const u32x4*)(tile + 16 * c);
             const int r = c / (ROW / 16), col = (c % (ROW / 16)) * (16 / ESZ);
             const int64_t idx = off + (int64_t)r * p.ldo + col;
-            store_out_nt((u32x4*)((uint8_t*)p.out + idx * ESZ), val);
+            store_out((u32x4*)((uint8_t*)p.out + idx * ESZ), val);
         }
     }
 }
