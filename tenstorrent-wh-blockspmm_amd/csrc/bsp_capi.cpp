@@ -317,7 +317,7 @@ int make_spmm_stream_plan(bsp_plan** out, const bsp_bsr_desc* a, int64_t N, int 
     in.waves = (5 + sv.nbw) * sv.pipes;
     in.persistent = sv.pipes;
     in.a_stages = sv.sa;
-    hipError_t e = upload((bsp::SpmmStreamWg**)&p->d_wgs, ss.wgs);
+    hipError_t e = upload((bsp::SpmmStreamHead**)&p->d_wgs, ss.heads);
     if (e == hipSuccess) e = upload(&p->d_units, ss.units);
     if (e == hipSuccess) e = upload(&p->d_ent_off, ss.bw);
     if (e == hipSuccess) e = upload(&p->d_aw, ss.aw);
@@ -444,7 +444,7 @@ int bsp_spmm(const bsp_plan* p, const uint16_t* a_vals, const uint16_t* b, int64
         sa.a = a_vals;
         sa.b = b;
         sa.c = c;
-        sa.wgs = (const bsp::SpmmStreamWg*)p->d_wgs;
+        sa.heads = (const bsp::SpmmStreamHead*)p->d_wgs;
         sa.units = p->d_units;
         sa.bw = p->d_ent_off;
         sa.aw = p->d_aw;

@@ -941,26 +941,28 @@ struct BSliceLoader {
 // (P per wave) into stage e % S; the wave takes part in the n barriers.  The
 // entry words come from plan memory through scalar loads, eight at a time and
 // two chunks ahead of use (a scalar-cache miss on the step that needs the
-// word would otherwise stall the issue on every eighth entry).  The word
-// arrays are padded past every stream's end, so the chunks ahead need no
-// bounds test.
+// word would otherwise stall the issue on every eighth entry).  The first two
+// chunks come from the workgroup's head (`head`, loaded with its record), the
+// rest from the stream (`words`).  The word arrays are padded past every
+// stream's end, so the chunks ahead need no bounds test.
 template <int S, int P, typename WT, class Issue>
-__device__ __forceinline__ void stream_loader(int n, const WT* words, Issue&& issue) {
+__device__ __forceinline__ void stream_loader(int n, const WT* head, const WT* words, Issue&& issue) {
     static_assert(P * (S - 2) < 64, "vmcnt budget");
-    static_assert(S - 1 <= 16, "the prologue takes its words from the first two chunks");
+    static_assert(S - 1 <= 16 && kHeadWords == 16, "the prologue takes its words from the head's two chunks");
     struct W8 {
         WT w[8];
     };
+    const W8* hc = (const W8*)head;
     const W8* ch = (const W8*)words;
     {
-        const W8 c0 = load_const(ch), c1 = load_const(ch + 1);
+        const W8 c0 = load_const(hc), c1 = load_const(hc + 1);
 #pragma unroll
         for (int e = 0; e < S - 1; ++e)
             if (e < n) issue(e, e < 8 ? c0.w[e] : c1.w[e - 8]);
     }
     // Steps 8m .. 8m+7 issue entries 8m+S-1 .. 8m+S+6: chunks m+OFF and m+OFF+1.
     constexpr int OFF = (S - 1) / 8, R0 = (S - 1) % 8;
-    W8 ca = load_const(ch + OFF), cb = load_const(ch + OFF + 1);
+    W8 ca = load_const((OFF < 2 ? hc : ch) + OFF), cb = load_const((OFF + 1 < 2 ? hc : ch) + OFF + 1);
     for (int k0 = 0; k0 < n; k0 += 8) {
         const W8 cc = load_const(ch + k0 / 8 + OFF + 2);
 #pragma unroll
@@ -1008,13 +1010,14 @@ __global__ __launch_bounds__(64 * (5 + NBW) * PIPES) void spmm_stream_kernel(Spm
     const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int pipe = PIPES > 1 ? wave_id / WPP : 0;
     const int wave = wave_id - pipe * WPP;  // role within the pipeline
-    const SpmmStreamWg wg = load_const(p.wgs + blockIdx.x * PIPES + pipe);
+    const SpmmStreamHead* head = p.heads + blockIdx.x * PIPES + pipe;
+    const SpmmStreamWg wg = load_const(&head->wg);
     const int n = wg.n;
     // Barriers every wave takes: the longer pipeline's steps (+1 to close the exchange).
     int steps = n;
     if constexpr (PIPES > 1) {
-        const SpmmStreamWg w0 = load_const(p.wgs + blockIdx.x * PIPES);
-        const SpmmStreamWg w1 = load_const(p.wgs + blockIdx.x * PIPES + 1);
+        const SpmmStreamWg w0 = load_const(&p.heads[blockIdx.x * PIPES].wg);
+        const SpmmStreamWg w1 = load_const(&p.heads[blockIdx.x * PIPES + 1].wg);
         steps = max(w0.n, w1.n);
     }
     uint8_t* psmem = smem + pipe * PIPE_LDS;
@@ -1031,7 +1034,7 @@ __global__ __launch_bounds__(64 * (5 + NBW) * PIPES) void spmm_stream_kernel(Spm
         uint32_t a_voff[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) a_voff[j] = 2 * a_load_offset(2 * j + (lane >> 5), lane, p.lda);
-        stream_loader<SA, 2>(n, p.aw + wg.w_begin, [&](int e, uint32_t w) {
+        stream_loader<SA, 2>(n, head->aw, p.aw + wg.w_begin, [&](int e, uint32_t w) {
             const uint16_t* ablk = p.a + (int64_t)w * 32;
             const uint32_t dst = lds0 + (uint32_t)(e % SA) * kA_BYTES;
             gl_lds16_s(a_voff[0], ablk, dst);
@@ -1044,7 +1047,7 @@ __global__ __launch_bounds__(64 * (5 + NBW) * PIPES) void spmm_stream_kernel(Spm
         const int wb = wave - 4;
         const Loader ld(wb, lane, p.ldb);
         const uint32_t b_lds = lds0 + A_RING + wb * Loader::BI * 1024;
-        stream_loader<SB, Loader::BI>(n, p.bw + wg.w_begin, [&](int e, int64_t w) {
+        stream_loader<SB, Loader::BI>(n, head->bw, p.bw + wg.w_begin, [&](int e, int64_t w) {
             const uint16_t* bpan = p.b + (int64_t)(uint32_t)w * p.ldb + (int32_t)(w >> 32);
             const uint32_t dst = b_lds + (uint32_t)(e % SB) * Loader::BYTES;
 #pragma unroll
@@ -1070,8 +1073,8 @@ __global__ __launch_bounds__(64 * (5 + NBW) * PIPES) void spmm_stream_kernel(Spm
     // records ahead are valid reads even past the last unit.)
     const SpmmStreamUnit* units = p.units + wg.u_begin;
     int u = 0;
-    SpmmStreamUnit cur = load_const(units);
-    SpmmStreamUnit nxt = load_const(units + 1);
+    SpmmStreamUnit cur = load_const(&head->u[0]);  // = units[0], units[1]
+    SpmmStreamUnit nxt = load_const(&head->u[1]);
     SpmmStreamUnit held{};  // the shared unit, stored after the exchange (flag 2)
     bool holding = false;
     auto store_unit = [&](const SpmmStreamUnit& un) {

@@ -32,7 +32,7 @@ struct SpmmStreamArgs {
     const uint16_t* a;             // A block values (bf16)
     const uint16_t* b;             // B (bf16), row-major K x N, leading dim ldb
     void* c;                       // C (fp32 or bf16), row-major M x N, leading dim ldc
-    const SpmmStreamWg* wgs;       // one per workgroup
+    const SpmmStreamHead* heads;   // one per workgroup (per pipeline)
     const SpmmStreamUnit* units;   // unit records (padded)
     const int64_t* bw;             // per stream entry: first row of B | first column << 32 (padded)
     const uint32_t* aw;            // per stream entry: A sub-block offset / 32 (padded)

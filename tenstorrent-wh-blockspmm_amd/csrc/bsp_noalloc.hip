@@ -1,8 +1,8 @@
 // bsp_spmm_noalloc: SpMM without any device allocation, for callers that
 // cannot allocate (serving loops that must not touch the allocator, harnesses
 // that forbid hipMalloc).  It runs the persistent SpMM kernel of bsp_spmm with
-// the kernel's schedule -- the per-workgroup records, unit records and entry
-// words that a plan uploads into memory it allocates -- staged instead in
+// the kernel's schedule -- the per-workgroup head records, unit records and
+// entry words that a plan uploads into memory it allocates -- staged instead in
 // `scratch`, a file-scope device array of BSP_NOALLOC_SCRATCH_BYTES that every
 // GPU the library runs on holds from module load to the end of the process.
 //
@@ -102,7 +102,7 @@ extern "C" int bsp_spmm_noalloc(const bsp_bsr_desc* a, const uint16_t* a_vals, c
     std::string msg;
     int st = bsp::build_spmm_stream(a, N, cus, sv.tile_n, wpc, ss, msg, 0, 1);
     if (st != BSP_OK) return bsp::record_error(st, msg);
-    const size_t o_units = align256(ss.wgs.size() * sizeof(bsp::SpmmStreamWg));
+    const size_t o_units = align256(ss.heads.size() * sizeof(bsp::SpmmStreamHead));
     const size_t o_bw = align256(o_units + ss.units.size() * sizeof(bsp::SpmmStreamUnit));
     const size_t o_aw = align256(o_bw + ss.bw.size() * sizeof(int64_t));
     const size_t total = align256(o_aw + ss.aw.size() * sizeof(uint32_t));
@@ -118,7 +118,7 @@ extern "C" int bsp_spmm_noalloc(const bsp_bsr_desc* a, const uint16_t* a_vals, c
     if (st != BSP_OK) return st;
     // Host staging of the schedule in the scratch array's layout.
     std::vector<unsigned char> host(total);
-    put(host, 0, ss.wgs);
+    put(host, 0, ss.heads);
     put(host, o_units, ss.units);
     put(host, o_bw, ss.bw);
     put(host, o_aw, ss.aw);
@@ -133,7 +133,7 @@ extern "C" int bsp_spmm_noalloc(const bsp_bsr_desc* a, const uint16_t* a_vals, c
         args.a = a_vals;
         args.b = b;
         args.c = c;
-        args.wgs = (const bsp::SpmmStreamWg*)base;
+        args.heads = (const bsp::SpmmStreamHead*)base;
         args.units = (const bsp::SpmmStreamUnit*)(base + o_units);
         args.bw = (const int64_t*)(base + o_bw);
         args.aw = (const uint32_t*)(base + o_aw);

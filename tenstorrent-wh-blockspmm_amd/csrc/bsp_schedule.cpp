@@ -577,6 +577,17 @@ int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n,
     s.bw.resize(s.bw.size() + kStreamPad, 0);
     s.aw.resize(s.aw.size() + kStreamPad, 0);
     s.units.resize(s.units.size() + kStreamPad, SpmmStreamUnit{0, 0, 0, 0});
+    s.heads.assign(s.wgs.size(), SpmmStreamHead{});
+    for (size_t g = 0; g < s.wgs.size(); ++g) {
+        SpmmStreamHead& h = s.heads[g];
+        const SpmmStreamWg& w = s.wgs[g];
+        h.wg = w;
+        for (int j = 0; j < 2; ++j) h.u[j] = s.units[(size_t)w.u_begin + j];
+        for (int j = 0; j < kHeadWords; ++j) {
+            h.bw[j] = s.bw[(size_t)w.w_begin + j];
+            h.aw[j] = s.aw[(size_t)w.w_begin + j];
+        }
+    }
     return BSP_OK;
 }
 

@@ -97,6 +97,24 @@ static_assert(sizeof(SpmmStreamUnit) == 16, "SpmmStreamUnit layout is shared wit
 // prefetch a few records ahead without a bounds test.
 constexpr int kStreamPad = 64;
 
+// What a workgroup reads first, in 256 contiguous bytes of its own: its
+// record, its first two unit records and the first kHeadWords words of each
+// of its entry streams (copies of the arrays' records and words, which the
+// arrays keep as well).  The kernel loads them all at once from an address
+// that depends only on the workgroup id, so the first entry's loads follow
+// one round trip to memory instead of two dependent ones (record, then
+// words).
+constexpr int kHeadWords = 16;
+struct SpmmStreamHead {
+    SpmmStreamWg wg;
+    SpmmStreamUnit u[2];
+    int32_t pad[4];
+    int64_t bw[kHeadWords];
+    uint32_t aw[kHeadWords];
+};
+static_assert(sizeof(SpmmStreamHead) == 256, "SpmmStreamHead layout is shared with the kernels");
+static_assert(kStreamPad >= kHeadWords && kStreamPad >= 2, "heads copy words and units from the padded arrays");
+
 struct SpmmStream {
     int32_t tile_n = 0;
     int32_t n_tiles = 0;
@@ -105,6 +123,7 @@ struct SpmmStream {
     int32_t max_wg_entries = 0;    // longest workgroup stream
     int64_t n_entries = 0;         // sum over units (entries x tiles)
     std::vector<SpmmStreamWg> wgs;        // one per workgroup; workgroup g runs on XCD g % kNumXcd
+    std::vector<SpmmStreamHead> heads;    // one per record of wgs, what the kernel reads first
     std::vector<SpmmStreamUnit> units;    // + kStreamPad zero records
     std::vector<int64_t> bw;              // per stream entry: first row of B | first column << 32 (+ pad)
     std::vector<uint32_t> aw;             // per stream entry: A sub-block element offset / 32 (+ pad)

@@ -12,6 +12,7 @@
 //
 //   test_schedule          exit status 0 when every check passes
 #include <algorithm>
+#include <cstring>
 #include <cstdio>
 #include <cstdlib>
 #include <map>
@@ -392,7 +393,7 @@ void check_spmm_stream(const Bsr& a, int64_t N, int cus, int tile_n, int wpc, co
     if (st != BSP_OK) return;
     const int64_t RS = a.R / kSub, CS = a.C / kSub, nsr = a.H / kSub, n_tiles = N / tile_n;
     const int64_t grid = (int64_t)(cus / kNumXcd) * (pipes == 2 ? 1 : wpc) * kNumXcd;
-    expect((int64_t)s.wgs.size() == grid * pipes, name + ": grid");
+    expect((int64_t)s.wgs.size() == grid * pipes && s.heads.size() == s.wgs.size(), name + ": grid");
     std::vector<int> seen(nsr * n_tiles, 0);  // entries seen per unit (as a count of parts' coverage)
     std::vector<int64_t> covered(nsr * n_tiles, 0);
     int64_t w = 0, u = 0;
@@ -438,6 +439,16 @@ void check_spmm_stream(const Bsr& a, int64_t N, int cus, int tile_n, int wpc, co
             total += un.count;
         }
         expect(total == wg.n && e == wg.w_begin + wg.n, name + ": stream length");
+        // The head repeats the record, the first two unit records and the
+        // first kHeadWords words of both streams (past the stream's end: the
+        // arrays' padding or the next stream's words, as the kernel would
+        // have read them from the arrays).
+        const SpmmStreamHead& h = s.heads[r];
+        expect(std::memcmp(&h.wg, &wg, sizeof wg) == 0, name + ": head record");
+        for (int j = 0; j < 2; ++j)
+            expect(std::memcmp(&h.u[j], &s.units[wg.u_begin + j], sizeof(SpmmStreamUnit)) == 0, name + ": head units");
+        for (int j = 0; j < kHeadWords; ++j)
+            expect(h.bw[j] == s.bw[wg.w_begin + j] && h.aw[j] == s.aw[wg.w_begin + j], name + ": head words");
         if (pipes == 2 && pipe == 1)
             expect(s.wgs[r - 1].n - wg.n == 0 || s.wgs[r - 1].n - wg.n == 1, name + ": halves within one entry");
         w += wg.n;
