@@ -267,6 +267,25 @@ bool choose_spmm_stream(const bsp_bsr_desc* a, int64_t N, int cus, SpmmStreamVar
     if (N % v.tile_n != 0) v = bsp::SpmmStreamVariant{128, 6, 12, 2, 1};
     const int lds = bsp::spmm_stream_lds_bytes(v);
     int w = v.pipes > 1 ? 1 : std::max(1, std::min(2, bsp::kLdsBytesPerCu / lds));
+    // Many units per workgroup with some longer than a workgroup's share (a
+    // skewed row distribution): one workgroup per compute unit with four B
+    // loaders streams the compute unit's units back to back, where two
+    // workgroups would leave one of them running alone behind its longest
+    // unit.  (Zipf(1.2) 16384^2 x 1024: 40.6-41.0 -> 39.0 us; with one unit
+    // per workgroup, as at uniform 1-50%, two workgroups stay faster: 25%
+    // 14.2 against 16.0 us.)
+    if (!std::getenv("BSP_SPMM_STREAM_VARIANT") && v.tile_n == 128 && a->R == bsp::kSub) {
+        const int64_t n_tiles = N / 128, stripes = a->H / bsp::kSub;
+        int64_t longest = 0;
+        for (int64_t i = 0; i < a->H / a->R; ++i) longest = std::max<int64_t>(longest, a->indptr[i + 1] - a->indptr[i]);
+        longest *= a->C / bsp::kSub;
+        const int64_t total = a->nblocks * (a->C / bsp::kSub) * n_tiles;
+        const int64_t wgs = 2 * (int64_t)cus;
+        if (stripes * n_tiles >= 4 * wgs && longest * wgs > total) {
+            v = bsp::SpmmStreamVariant{128, 6, 12, 4, 1};
+            w = 1;
+        }
+    }
     if (v.pipes == 1) w = (int)env_int("BSP_SPMM_STREAM_WPC", w);
     if (w < 1 || w * lds > bsp::kLdsBytesPerCu) w = 1;
     *sv = v;
