@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define BSP_ABI_VERSION 4
+#define BSP_ABI_VERSION 5
 
 typedef enum bsp_status {
     BSP_OK = 0,
@@ -114,6 +114,9 @@ typedef struct bsp_plan_info {
                             tile units; n_items counts the units, stages is the
                             B ring depth) */
     int32_t a_stages;    /* SpMM persistent: depth of the A ring */
+    int32_t step_entries;/* SpMM: entries per ring step, i.e. per workgroup
+                            barrier (1, or 2 for the persistent kernel's
+                            paired steps); 0 for other kinds */
 } bsp_plan_info;
 
 /* ---- library ------------------------------------------------------------- */

@@ -138,6 +138,7 @@ void fill_info_spmm(const bsp::SpmmSchedule& s, bsp_plan_info* info) {
         if (bsp::spmm_variant_supported(w)) v = w;
     }
     info->stages = v.stages;
+    info->step_entries = 1;
     info->group = s.group;
     // Row groups on 256-column tiles run eight waves (two per SIMD) unless
     // BSP_SPMM_WIDE_WAVES=4 asks for four (groups of 2 or 4 stripes only: four
@@ -248,33 +249,34 @@ namespace bsp {
 // takes blocks whose stripes do not form row groups (row groups share each B
 // panel among the stripes of a block row, which the per-item group kernels
 // exploit) and N a multiple of 128.  BSP_SPMM_STREAM=0 turns it off;
-// BSP_SPMM_STREAM_VARIANT="tile,sb,sa,nbw[,pipes]" picks another compiled
-// variant and BSP_SPMM_STREAM_WPC the workgroups per compute unit (all read
-// here, at plan creation).  A two-pipeline variant runs one workgroup per
-// compute unit.
+// BSP_SPMM_STREAM_VARIANT="tile,sb,sa,nbw[,pipes[,entries per step]]" picks
+// another compiled variant and BSP_SPMM_STREAM_WPC the workgroups per compute
+// unit (all read here, at plan creation).  A two-pipeline variant runs one
+// workgroup per compute unit.
 bool choose_spmm_stream(const bsp_bsr_desc* a, int64_t N, int cus, SpmmStreamVariant* sv, int* wpc) {
     if (env_int("BSP_SPMM_STREAM", 1) == 0) return false;
     if (N % 128 != 0) return false;
     const int64_t group = env_int("BSP_SPMM_GROUP", bsp::spmm_choose_group(a->R, a->H, N, cus));
     if (group > 1 && (a->R / bsp::kSub) % group == 0) return false;
-    bsp::SpmmStreamVariant v{128, 6, 12, 2, 1};
-    if (const char* e = std::getenv("BSP_SPMM_STREAM_VARIANT")) {
+    bsp::SpmmStreamVariant v = bsp::kSpmmStreamDefault;
+    const char* forced = std::getenv("BSP_SPMM_STREAM_VARIANT");
+    if (forced) {
         bsp::SpmmStreamVariant w{};
-        w.pipes = 1;
-        const int got = std::sscanf(e, "%d,%d,%d,%d,%d", &w.tile_n, &w.sb, &w.sa, &w.nbw, &w.pipes);
-        if (got >= 4 && bsp::spmm_stream_variant_supported(w)) v = w;
+        const int got = std::sscanf(forced, "%d,%d,%d,%d,%d,%d", &w.tile_n, &w.sb, &w.sa, &w.nbw, &w.pipes, &w.eps);
+        if (got < 5) w.pipes = 1;
+        if (got < 6) w.eps = 1;
+        if (got >= 4 && bsp::spmm_stream_variant_supported(w) && N % w.tile_n == 0) v = w;
     }
-    if (N % v.tile_n != 0) v = bsp::SpmmStreamVariant{128, 6, 12, 2, 1};
-    const int lds = bsp::spmm_stream_lds_bytes(v);
-    int w = v.pipes > 1 ? 1 : std::max(1, std::min(2, bsp::kLdsBytesPerCu / lds));
+    int w = -1;
     // Many units per workgroup with some longer than a workgroup's share (a
     // skewed row distribution): one workgroup per compute unit with four B
-    // loaders streams the compute unit's units back to back, where two
-    // workgroups would leave one of them running alone behind its longest
-    // unit.  (Zipf(1.2) 16384^2 x 1024: 40.6-41.0 -> 39.0 us; with one unit
-    // per workgroup, as at uniform 1-50%, two workgroups stay faster: 25%
-    // 14.2 against 16.0 us.)
-    if (!std::getenv("BSP_SPMM_STREAM_VARIANT") && v.tile_n == 128 && a->R == bsp::kSub) {
+    // loaders and deep rings streams the compute unit's units back to back,
+    // where two workgroups would leave one of them running alone behind its
+    // longest unit.  (Zipf(1.2) 16384^2 x 1024: 40.6-41.0 us with two
+    // workgroups, 37.7-38.2 with this variant; with one unit per workgroup,
+    // as at uniform 1-50%, two workgroups stay faster: 25% 14.2 against 16.0
+    // us.)
+    if (!forced && a->R == bsp::kSub) {
         const int64_t n_tiles = N / 128, stripes = a->H / bsp::kSub;
         int64_t longest = 0;
         for (int64_t i = 0; i < a->H / a->R; ++i) longest = std::max<int64_t>(longest, a->indptr[i + 1] - a->indptr[i]);
@@ -282,10 +284,12 @@ bool choose_spmm_stream(const bsp_bsr_desc* a, int64_t N, int cus, SpmmStreamVar
         const int64_t total = a->nblocks * (a->C / bsp::kSub) * n_tiles;
         const int64_t wgs = 2 * (int64_t)cus;
         if (stripes * n_tiles >= 4 * wgs && longest * wgs > total) {
-            v = bsp::SpmmStreamVariant{128, 6, 12, 4, 1};
+            v = bsp::kSpmmStreamSkewed;
             w = 1;
         }
     }
+    const int lds = bsp::spmm_stream_lds_bytes(v);
+    if (w < 0) w = v.pipes > 1 ? 1 : std::max(1, std::min(2, bsp::kLdsBytesPerCu / lds));
     if (v.pipes == 1) w = (int)env_int("BSP_SPMM_STREAM_WPC", w);
     if (w < 1 || w * lds > bsp::kLdsBytesPerCu) w = 1;
     *sv = v;
@@ -336,6 +340,7 @@ int make_spmm_stream_plan(bsp_plan** out, const bsp_bsr_desc* a, int64_t N, int 
     in.waves = (5 + sv.nbw) * sv.pipes;
     in.persistent = sv.pipes;
     in.a_stages = sv.sa;
+    in.step_entries = sv.eps;
     hipError_t e = upload((bsp::SpmmStreamHead**)&p->d_wgs, ss.heads);
     if (e == hipSuccess) e = upload(&p->d_units, ss.units);
     if (e == hipSuccess) e = upload(&p->d_ent_off, ss.bw);

@@ -913,7 +913,9 @@ __global__ __launch_bounds__(64 * NW, RW <= 4 && S == 3 ? 2 : 1) void spmm_group
 // then refill the stage of entry k-1 with entry k+S-1; the MFMA waves read
 // entry k's operands (into the set not in use) and multiply entry k-1, then
 // wait for their LDS reads (the stage of entry k is refilled after X_{k+1}).
-// Every wave executes the same n barriers.
+// Every wave executes the same n barriers.  With two entries per step the
+// same holds per pair: ceil(n/2) barriers, the stages of entries k-2 and k-1
+// refilled after step k (stream_loader2).
 namespace spmm_detail {
 
 // The B slice pieces (1 KB each) of B loader wave wb: piece p = wb*BI + j of
@@ -983,6 +985,57 @@ __device__ __forceinline__ void stream_loader(int n, const WT* head, const WT* w
     }
 }
 
+// The same with two entries per step (S even): step k (k = 0, 2, 4, ...)
+// waits until entries k and k+1 have landed, passes one barrier, then refills
+// the stages of entries k-2 and k-1 (read by the MFMA waves during step k-2)
+// with entries k+S-2 and k+S-1.  The prologue fills all S stages; ceil(n/2)
+// barriers in all.
+template <int S, int P, typename WT, class Issue>
+__device__ __forceinline__ void stream_loader2(int n, const WT* head, const WT* words, Issue&& issue) {
+    static_assert(S % 2 == 0 && S >= 4, "two entries per step need an even ring of at least 4 stages");
+    static_assert(S <= 16 && kHeadWords == 16, "the prologue takes its words from the head's two chunks");
+    static_assert(P * (S - 2) < 64, "vmcnt budget");
+    struct W8 {
+        WT w[8];
+    };
+    const W8* hc = (const W8*)head;
+    const W8* ch = (const W8*)words;
+    {
+        const W8 c0 = load_const(hc), c1 = load_const(hc + 1);
+#pragma unroll
+        for (int e = 0; e < S; ++e)
+            if (e < n) issue(e, e < 8 ? c0.w[e] : c1.w[e - 8]);
+    }
+    if (n <= 0) return;
+    wait_stages<P, S - 2>(max(0, min(S, n) - 2));  // entries 0 and 1 landed
+    barrier_no_fence();
+    // Steps s0+2 .. s0+8 issue entries s0+S .. s0+S+7: positions R0 .. R0+7 of
+    // chunks s0/8+OFF and s0/8+OFF+1 (R0 even, so a pair never straddles them).
+    constexpr int OFF = S / 8, R0 = S % 8;
+    W8 ca = load_const((OFF < 2 ? hc : ch) + OFF), cb = load_const((OFF + 1 < 2 ? hc : ch) + OFF + 1);
+    for (int s0 = 0; s0 + 2 < n; s0 += 8) {
+        const W8 cc = load_const(ch + s0 / 8 + OFF + 2);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int k = s0 + 2 + 2 * i;  // the step's first entry
+            if (k >= n) break;
+            const int e = k + S - 2, r = R0 + 2 * i;
+            if (e + 1 < n) {
+                wait_vmcnt<P * (S - 4)>();  // entries k, k+1 landed (k+2 .. k+S-3 may be in flight)
+                barrier_no_fence();
+                issue(e, r < 8 ? ca.w[r] : cb.w[r - 8]);
+                issue(e + 1, r + 1 < 8 ? ca.w[r + 1] : cb.w[r + 1 - 8]);
+            } else {
+                wait_stages<P, S - 4>(max(0, min(n, e) - (k + 2)));
+                barrier_no_fence();
+                if (e < n) issue(e, r < 8 ? ca.w[r] : cb.w[r - 8]);
+            }
+        }
+        ca = cb;
+        cb = cc;
+    }
+}
+
 }  // namespace spmm_detail
 
 // With PIPES = 2, one workgroup holds two such pipelines (each with its own
@@ -993,9 +1046,13 @@ __device__ __forceinline__ void stream_loader(int n, const WT* head, const WT* w
 // after one last barrier.  Two independent workgroups per compute unit hold
 // one unit each, and the one with the longer row finishes alone at the rate
 // of a single workgroup's loaders; the halves end together.
-template <int NTW, int SB, int SA, int NBW, int PIPES, bool OUT_BF16>
+// With EPS = 2 (one pipeline) every step covers two entries: one barrier per
+// pair, the MFMA waves reading both entries of a step into one register set
+// while multiplying the previous pair from the other (stream_loader2).
+template <int NTW, int SB, int SA, int NBW, int PIPES, bool OUT_BF16, int EPS>
 __global__ __launch_bounds__(64 * (5 + NBW) * PIPES) void spmm_stream_kernel(SpmmStreamArgs p) {
     using namespace spmm_detail;
+    static_assert(EPS == 1 || (EPS == 2 && PIPES == 1), "two entries per step with one pipeline");
     constexpr int TN = 128 * NTW;
     using Loader = BSliceLoader<TN, NBW>;
     constexpr int A_RING = SA * kA_BYTES;
@@ -1034,12 +1091,16 @@ __global__ __launch_bounds__(64 * (5 + NBW) * PIPES) void spmm_stream_kernel(Spm
         uint32_t a_voff[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) a_voff[j] = 2 * a_load_offset(2 * j + (lane >> 5), lane, p.lda);
-        stream_loader<SA, 2>(n, head->aw, p.aw + wg.w_begin, [&](int e, uint32_t w) {
+        auto issue_a = [&](int e, uint32_t w) {
             const uint16_t* ablk = p.a + (int64_t)w * 32;
             const uint32_t dst = lds0 + (uint32_t)(e % SA) * kA_BYTES;
             gl_lds16_s(a_voff[0], ablk, dst);
             gl_lds16_s(a_voff[1], ablk, dst + 1024);
-        });
+        };
+        if constexpr (EPS == 2)
+            stream_loader2<SA, 2>(n, head->aw, p.aw + wg.w_begin, issue_a);
+        else
+            stream_loader<SA, 2>(n, head->aw, p.aw + wg.w_begin, issue_a);
         idle_steps();
         return;
     }
@@ -1047,12 +1108,16 @@ __global__ __launch_bounds__(64 * (5 + NBW) * PIPES) void spmm_stream_kernel(Spm
         const int wb = wave - 4;
         const Loader ld(wb, lane, p.ldb);
         const uint32_t b_lds = lds0 + A_RING + wb * Loader::BI * 1024;
-        stream_loader<SB, Loader::BI>(n, head->bw, p.bw + wg.w_begin, [&](int e, int64_t w) {
+        auto issue_b = [&](int e, int64_t w) {
             const uint16_t* bpan = p.b + (int64_t)(uint32_t)w * p.ldb + (int32_t)(w >> 32);
             const uint32_t dst = b_lds + (uint32_t)(e % SB) * Loader::BYTES;
 #pragma unroll
             for (int j = 0; j < Loader::BI; ++j) gl_lds16_s(ld.voff[j], bpan, dst + j * 1024);
-        });
+        };
+        if constexpr (EPS == 2)
+            stream_loader2<SB, Loader::BI>(n, head->bw, p.bw + wg.w_begin, issue_b);
+        else
+            stream_loader<SB, Loader::BI>(n, head->bw, p.bw + wg.w_begin, issue_b);
         idle_steps();
         return;
     }
@@ -1160,6 +1225,44 @@ __global__ __launch_bounds__(64 * (5 + NBW) * PIPES) void spmm_stream_kernel(Spm
     };
     auto fence_sched = [] { __builtin_amdgcn_sched_barrier(0); };
     auto lds_done = [] { __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); };
+    if constexpr (EPS == 2) {
+        struct Pair {
+            Operands e0, e1;
+        };
+        Pair pa, pb;
+        if (n > 0) {
+            barrier_no_fence();  // step 0
+            read(0, pa.e0);
+            if (1 < n) read(1, pa.e1);
+            lds_done();
+        }
+        // Step k: read entries k and k+1 into `in`, multiply entries k-2 and
+        // k-1 (both exist, as k < n) from `out`.
+        auto step2 = [&](int k, Pair& in, Pair& out) {
+            barrier_no_fence();
+            read(k, in.e0);
+            if (k + 1 < n) read(k + 1, in.e1);
+            fence_sched();
+            multiply(out.e0);
+            multiply(out.e1);
+            fence_sched();
+            lds_done();
+        };
+        int k = 2;
+        for (; k + 2 < n; k += 4) {
+            step2(k, pb, pa);
+            step2(k + 2, pa, pb);
+        }
+        if (k < n) {
+            step2(k, pb, pa);
+            multiply(pb.e0);
+            if (k + 1 < n) multiply(pb.e1);
+        } else if (n > 0) {
+            multiply(pa.e0);  // entries k-2 and, if it exists, k-1
+            if (k - 1 < n) multiply(pa.e1);
+        }
+        return;
+    }
     Operands o0, o1;
     int k = 0;
     if (n > 0) {
@@ -1994,15 +2097,15 @@ hipError_t launch_spmm(const SpmmArgs& a, const SpmmVariant& v, bool out_bf16, i
 hipError_t launch_spmm_stream(const SpmmStreamArgs& a, const SpmmStreamVariant& v, bool out_bf16, int grid,
                               hipStream_t stream) {
     if (grid <= 0) return hipSuccess;
-#define BSP_STREAM_CASE(TN, SB, SA, NB, PP)                                                                     \
-    if (v.tile_n == TN && v.sb == SB && v.sa == SA && v.nbw == NB && v.pipes == PP) {                          \
-        if (out_bf16)                                                                                          \
-            hipLaunchKernelGGL((spmm_stream_kernel<TN / 128, SB, SA, NB, PP, true>), dim3(grid),                 \
-                               dim3(64 * (5 + NB) * PP), 0, stream, a);                                        \
-        else                                                                                                   \
-            hipLaunchKernelGGL((spmm_stream_kernel<TN / 128, SB, SA, NB, PP, false>), dim3(grid),                \
-                               dim3(64 * (5 + NB) * PP), 0, stream, a);                                        \
-        return hipGetLastError();                                                                              \
+#define BSP_STREAM_CASE(TN, SB, SA, NB, PP, EPS)                                                                  \
+    if (v.tile_n == TN && v.sb == SB && v.sa == SA && v.nbw == NB && v.pipes == PP && v.eps == EPS) {            \
+        if (out_bf16)                                                                                            \
+            hipLaunchKernelGGL((spmm_stream_kernel<TN / 128, SB, SA, NB, PP, true, EPS>), dim3(grid),              \
+                               dim3(64 * (5 + NB) * PP), 0, stream, a);                                          \
+        else                                                                                                     \
+            hipLaunchKernelGGL((spmm_stream_kernel<TN / 128, SB, SA, NB, PP, false, EPS>), dim3(grid),             \
+                               dim3(64 * (5 + NB) * PP), 0, stream, a);                                          \
+        return hipGetLastError();                                                                                \
     }
     BSP_SPMM_STREAM_VARIANTS(BSP_STREAM_CASE)
 #undef BSP_STREAM_CASE

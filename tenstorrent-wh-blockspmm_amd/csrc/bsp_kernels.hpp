@@ -43,20 +43,25 @@ struct SpmmStreamArgs {
 };
 
 // Compiled persistent SpMM variants: tile width, B ring depth, A ring depth,
-// B loader waves, pipelines per workgroup.  A pipeline has 4 MFMA waves (each
-// 32*tile/128 columns), the B loader waves and one A loader wave, and LDS of
-// 64*tile*SB + 2 KB*SA; two pipelines add a 16 KB (32 KB at tile 256)
-// exchange buffer.
+// B loader waves, pipelines per workgroup, entries per ring step.  A pipeline
+// has 4 MFMA waves (each 32*tile/128 columns), the B loader waves and one A
+// loader wave, and LDS of 64*tile*SB + 2 KB*SA; two pipelines add a 16 KB
+// (32 KB at tile 256) exchange buffer.  With two entries per step (one
+// pipeline, even ring depths of at most 16) the workgroup passes one barrier
+// per pair of entries.
 #define BSP_SPMM_STREAM_VARIANTS(X) \
-    X(128, 6, 12, 2, 1)             \
-    X(128, 6, 12, 4, 1)             \
-    X(128, 4, 16, 4, 1)             \
-    X(128, 8, 16, 8, 1)             \
-    X(256, 4, 16, 4, 1)             \
-    X(256, 5, 16, 8, 1)             \
-    X(256, 6, 8, 8, 1)              \
-    X(128, 6, 12, 2, 2)             \
-    X(128, 5, 12, 2, 2)
+    X(128, 8, 8, 2, 1, 2)           \
+    X(128, 14, 16, 4, 1, 2)         \
+    X(128, 6, 12, 2, 1, 2)          \
+    X(128, 6, 12, 2, 1, 1)          \
+    X(128, 6, 12, 4, 1, 1)          \
+    X(128, 4, 16, 4, 1, 1)          \
+    X(128, 8, 16, 8, 1, 1)          \
+    X(256, 4, 16, 4, 1, 1)          \
+    X(256, 5, 16, 8, 1, 1)          \
+    X(256, 6, 8, 8, 1, 1)           \
+    X(128, 6, 12, 2, 2, 1)          \
+    X(128, 5, 12, 2, 2, 1)
 
 struct SpmmStreamVariant {
     int tile_n;
@@ -64,11 +69,16 @@ struct SpmmStreamVariant {
     int sa;
     int nbw;
     int pipes = 1;
+    int eps = 1;  // entries per ring step
 };
 
+// The default (uniform rows) and the skewed-row choice of choose_spmm_stream.
+constexpr SpmmStreamVariant kSpmmStreamDefault{128, 8, 8, 2, 1, 2};
+constexpr SpmmStreamVariant kSpmmStreamSkewed{128, 14, 16, 4, 1, 2};
+
 inline bool spmm_stream_variant_supported(const SpmmStreamVariant& v) {
-#define BSP_SPMM_STREAM_MATCH(TN, SB, SA, NB, PP) \
-    if (v.tile_n == TN && v.sb == SB && v.sa == SA && v.nbw == NB && v.pipes == PP) return true;
+#define BSP_SPMM_STREAM_MATCH(TN, SB, SA, NB, PP, EPS) \
+    if (v.tile_n == TN && v.sb == SB && v.sa == SA && v.nbw == NB && v.pipes == PP && v.eps == EPS) return true;
     BSP_SPMM_STREAM_VARIANTS(BSP_SPMM_STREAM_MATCH)
 #undef BSP_SPMM_STREAM_MATCH
     return false;

@@ -92,10 +92,10 @@ extern "C" int bsp_spmm_noalloc(const bsp_bsr_desc* a, const uint16_t* a_vals, c
         int n = 0;
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && n > 0) cus = n;
     }
-    bsp::SpmmStreamVariant sv{128, 6, 12, 2, 1};
+    bsp::SpmmStreamVariant sv = bsp::kSpmmStreamDefault;
     int wpc = 2;
     if (!bsp::choose_spmm_stream(a, N, cus, &sv, &wpc) || sv.pipes != 1) {
-        sv = bsp::SpmmStreamVariant{128, 6, 12, 2, 1};
+        sv = bsp::kSpmmStreamDefault;
         wpc = 2;
     }
     bsp::SpmmStream ss;

@@ -144,8 +144,10 @@ def test_skewed_workload_full_size(monkeypatch, kernel, split):
     assert (info["n_split_rows"] > 0) == bool(split)
     if kernel == "persistent":
         # eight units per workgroup, the longest (101 entries) above a
-        # workgroup's share: one workgroup per compute unit, four B loaders
-        assert (info["grid"], info["waves"]) == (256, 9), info
+        # workgroup's share: one workgroup per compute unit, four B loaders,
+        # deep rings, two entries per step
+        assert (info["grid"], info["waves"], info["stages"], info["a_stages"], info["step_entries"]) == \
+            (256, 9, 14, 16, 2), info
     got1 = run_spmm(a, w["b"], "f32", plan=plan)
     got2 = run_spmm(a, w["b"], "f32", plan=plan)
     np.testing.assert_array_equal(got1, got2)  # counters reset, summation order fixed

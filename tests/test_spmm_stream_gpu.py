@@ -11,10 +11,14 @@ from helpers import W, assert_parity, bsr_of, capi, golden_spmm, run_spmm, spmm_
 
 pytestmark = pytest.mark.gpu
 
-# (tile, B ring, A ring, B loader waves) of BSP_SPMM_STREAM_VARIANTS in csrc/bsp_kernels.hpp
-# (tile, B ring, A ring, B loader waves, pipelines per workgroup)
-STREAM_VARIANTS = [(128, 6, 12, 2, 1), (128, 6, 12, 4, 1), (128, 4, 16, 4, 1), (128, 8, 16, 8, 1),
-                   (256, 4, 16, 4, 1), (256, 5, 16, 8, 1), (256, 6, 8, 8, 1), (128, 6, 12, 2, 2), (128, 5, 12, 2, 2)]
+# (tile, B ring, A ring, B loader waves, pipelines per workgroup, entries per
+# ring step) of BSP_SPMM_STREAM_VARIANTS in csrc/bsp_kernels.hpp
+STREAM_VARIANTS = [(128, 8, 8, 2, 1, 2), (128, 14, 16, 4, 1, 2), (128, 6, 12, 2, 1, 2),
+                   (128, 6, 12, 2, 1, 1), (128, 6, 12, 4, 1, 1), (128, 4, 16, 4, 1, 1), (128, 8, 16, 8, 1, 1),
+                   (256, 4, 16, 4, 1, 1), (256, 5, 16, 8, 1, 1), (256, 6, 8, 8, 1, 1), (128, 6, 12, 2, 2, 1),
+                   (128, 5, 12, 2, 2, 1)]
+DEFAULT = (128, 8, 8, 2, 1, 2)   # uniform rows
+SKEWED = (128, 14, 16, 4, 1, 2)  # skewed rows: one workgroup per compute unit
 
 
 def _lds(v):
@@ -33,8 +37,8 @@ def _check(a, b, out_dtype, what, v=None, wpc=None):
     info = plan.info()
     assert info["persistent"] >= 1, f"{what}: plan is not persistent ({info})"
     if v is not None:
-        assert (info["tile_n"], info["stages"], info["a_stages"], info["waves"], info["persistent"]) == \
-            (v[0], v[1], v[2], (5 + v[3]) * v[4], v[4])
+        assert (info["tile_n"], info["stages"], info["a_stages"], info["waves"], info["persistent"],
+                info["step_entries"]) == (v[0], v[1], v[2], (5 + v[3]) * v[4], v[4], v[5])
     if wpc is not None:
         assert info["grid"] == 256 * wpc
     got = run_spmm(a, b, out_dtype, plan=plan)
@@ -58,7 +62,7 @@ def test_stream_variants(monkeypatch, v, density):
             _check(w["a"], w["b"], od, f"variant={v} wpc={wpc} d={density} {od}", v, wpc)
 
 
-@pytest.mark.parametrize("v", [(128, 6, 12, 2, 1), (256, 4, 16, 4, 1), (128, 6, 12, 2, 2)])
+@pytest.mark.parametrize("v", [DEFAULT, SKEWED, (128, 6, 12, 2, 1, 1), (256, 4, 16, 4, 1, 1), (128, 6, 12, 2, 2, 1)])
 def test_stream_many_units_per_workgroup(monkeypatch, v):
     """32768 rows x 1024 columns at 0.2%: 8192 or 4096 units on 256-512
     workgroups (16 per workgroup), many of them empty stripes, stored as zeros."""
@@ -69,7 +73,7 @@ def test_stream_many_units_per_workgroup(monkeypatch, v):
     _check(a, w["b"], "f32", f"many units {v}")
 
 
-@pytest.mark.parametrize("v", [(128, 6, 12, 2, 1), (256, 5, 16, 8, 1), (128, 6, 12, 2, 2)])
+@pytest.mark.parametrize("v", [DEFAULT, SKEWED, (128, 6, 12, 2, 1, 1), (256, 5, 16, 8, 1, 1), (128, 6, 12, 2, 2, 1)])
 def test_stream_long_rows(monkeypatch, v):
     """A few rows of 200-400 entries (streams far longer than the ring and the
     word prefetch) among short ones."""
@@ -87,17 +91,42 @@ def test_stream_long_rows(monkeypatch, v):
     _check(a, b, "bf16", f"long rows {v} bf16")
 
 
-def test_stream_fewer_units_than_workgroups(monkeypatch):
+@pytest.mark.parametrize("v", [DEFAULT, (128, 6, 12, 2, 1, 1)])
+def test_stream_fewer_units_than_workgroups(monkeypatch, v):
     """A 64x128 problem: 2 units for 512 workgroups; the rest stream nothing."""
-    _stream_env(monkeypatch, (128, 6, 12, 2, 1), 2)
+    _stream_env(monkeypatch, v, 2)
     w = W.spmm_workload(64, 256, 128, 32, 32, 0.5, seed=93)
     _check(w["a"], w["b"], "f32", "2 units")
 
 
-@pytest.mark.parametrize("pipes", [1, 2])
-def test_stream_empty_matrix(monkeypatch, pipes):
+@pytest.mark.parametrize("v", [DEFAULT, SKEWED, (128, 6, 12, 2, 1, 2), (128, 6, 12, 2, 1, 1)])
+def test_stream_step_tails(monkeypatch, v):
+    """One unit per workgroup with every stream length from 0 to 40 entries:
+    with two entries per step, odd and even lengths end differently, and
+    lengths below the ring depth never reach the steady state."""
+    _stream_env(monkeypatch, v)
+    rng = np.random.default_rng(97)
+    counts = np.arange(41)
+    rng.shuffle(counts)
+    nbc = 64
+    indices = np.concatenate([np.sort(rng.choice(nbc, c, replace=False)) for c in counts]).astype(np.int32)
+    indptr = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    a = W.BsrArrays(len(counts) * 32, nbc * 32, 32, 32, indptr, indices)
+    a.data = W.block_content(a.nblocks, 32, 32, "RAND", rng)
+    b = W.dense_content(nbc * 32, 128, "RAND", rng)
+    plan = capi.SpmmPlan(bsr_of(a), 128, "f32")
+    info = plan.info()
+    plan.close()
+    assert info["n_items"] == len(counts) and info["grid"] >= len(counts)  # one unit per workgroup
+    _check(a, b, "f32", f"tails {v}")
+    _check(a, b, "bf16", f"tails {v} bf16")
+
+
+@pytest.mark.parametrize("v", [DEFAULT, (128, 6, 12, 2, 2, 1)])
+def test_stream_empty_matrix(monkeypatch, v):
     """No stored blocks: every unit is an empty stripe, every tile stored as zeros."""
-    _stream_env(monkeypatch, (128, 6, 12, 2, pipes))
+    pipes = v[4]
+    _stream_env(monkeypatch, v)
     a = W.BsrArrays(1024, 1024, 32, 32, np.zeros(33, np.int32), np.zeros(0, np.int32))
     a.data = np.zeros(0, np.uint16)
     b = W.dense_content(1024, 256, "RAND", np.random.default_rng(94))
@@ -108,10 +137,25 @@ def test_stream_empty_matrix(monkeypatch, pipes):
     assert np.all(got == 0.0)
 
 
+@pytest.mark.parametrize("v", [DEFAULT, (128, 6, 12, 2, 2, 1)])
 @pytest.mark.parametrize("R,C", [(64, 64), (32, 96), (96, 32)])
-def test_stream_other_block_shapes(monkeypatch, R, C):
+def test_stream_other_block_shapes(monkeypatch, R, C, v):
     """Blocks other than 32x32 cut into 32-row stripes (no row groups)."""
     monkeypatch.setenv("BSP_SPMM_GROUP", "1")
-    _stream_env(monkeypatch, (128, 6, 12, 2, 2))
+    _stream_env(monkeypatch, v)
     w = W.spmm_workload(1536, 1536, 256, R, C, 0.2, seed=95 + R + C)
     _check(w["a"], w["b"], "f32", f"R={R} C={C}")
+
+
+@pytest.mark.parametrize("density", W.SPMM_SWEEP_DENSITIES)
+def test_default_plan_variant(density):
+    """The density sweep's plans take the default variant, two workgroups per
+    compute unit (what the sweep tests and the bench run)."""
+    w = W.workload_spmm_sweep(density)
+    a = w["a"]
+    plan = capi.SpmmPlan(bsr_of(a), w["b"].shape[1], "f32")
+    info = plan.info()
+    plan.close()
+    v = DEFAULT
+    assert (info["persistent"], info["tile_n"], info["stages"], info["a_stages"], info["waves"],
+            info["step_entries"], info["grid"]) == (1, v[0], v[1], v[2], 5 + v[3], v[5], 512), info
