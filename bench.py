@@ -159,7 +159,7 @@ def summarize(t, flops, nbytes):
 
 
 def plan_summary(info):
-    keys = ("tile_n", "stages", "group", "grid", "waves", "persistent", "a_stages", "n_split_rows")
+    keys = ("tile_n", "stages", "group", "grid", "waves", "persistent", "a_stages", "step_entries", "n_split_rows")
     return {k: info[k] for k in keys if k in info}
 
 
