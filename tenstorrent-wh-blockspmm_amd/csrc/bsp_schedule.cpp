@@ -626,7 +626,7 @@ int build_sddmm_schedule(const bsp_bsr_desc* m, int64_t K, int num_cus, SddmmSch
     // over all XCDs).  An item is a run of at most q entries of one stripe
     // and one band.
     const int64_t ncol32 = m->W / kSub;
-    auto build = [&](int64_t bands, SddmmSchedule& o) {
+    auto build = [&](int64_t bands, bool by_items, SddmmSchedule& o) {
         o.chunk = (int32_t)q;
         o.items.clear();
         o.ent_col.clear();
@@ -668,18 +668,52 @@ int build_sddmm_schedule(const bsp_bsr_desc* m, int64_t K, int num_cus, SddmmSch
             o.wgmap = xcd_lpt_map(cost, 1);
             return;
         }
-        // Stripes longest first onto the least-loaded of 8 / bands row groups.
+        // Stripes onto the 8 / bands row groups: longest first onto the
+        // least-loaded group (by_items false), or, so that every XCD's item
+        // count stays within one round of workgroups, most items first onto
+        // the group whose fullest XCD would hold the fewest items afterwards
+        // (by_items true; a stripe adds items to one XCD per band).
         const int rgs = (int)(kNumXcd / bands);
         std::vector<int32_t> order(nsr);
         std::iota(order.begin(), order.end(), 0);
-        std::stable_sort(order.begin(), order.end(),
-                         [&](int32_t x, int32_t y) { return stripe_cost[x] > stripe_cost[y]; });
         std::vector<int32_t> stripe_rg(nsr, 0);
-        std::vector<int64_t> load(rgs, 0);
-        for (int32_t sr : order) {
-            const int g = (int)(std::min_element(load.begin(), load.end()) - load.begin());
-            stripe_rg[sr] = g;
-            load[g] += stripe_cost[sr];
+        if (!by_items) {
+            std::stable_sort(order.begin(), order.end(),
+                             [&](int32_t x, int32_t y) { return stripe_cost[x] > stripe_cost[y]; });
+            std::vector<int64_t> load(rgs, 0);
+            for (int32_t sr : order) {
+                const int g = (int)(std::min_element(load.begin(), load.end()) - load.begin());
+                stripe_rg[sr] = g;
+                load[g] += stripe_cost[sr];
+            }
+        } else {
+            std::vector<int64_t> n_items(nsr * bands, 0);  // items of stripe sr in band b
+            for (size_t u = 0; u < o.items.size(); ++u) ++n_items[(int64_t)item_stripe[u] * bands + item_band[u]];
+            std::vector<int64_t> tot(nsr, 0), most(nsr, 0);
+            for (int64_t sr = 0; sr < nsr; ++sr)
+                for (int64_t b = 0; b < bands; ++b) {
+                    tot[sr] += n_items[sr * bands + b];
+                    most[sr] = std::max(most[sr], n_items[sr * bands + b]);
+                }
+            std::stable_sort(order.begin(), order.end(), [&](int32_t x, int32_t y) {
+                return tot[x] != tot[y] ? tot[x] > tot[y] : most[x] > most[y];
+            });
+            std::vector<int64_t> load(rgs * bands, 0);
+            for (int32_t sr : order) {
+                int best = 0;
+                int64_t best_max = INT64_MAX, best_sum = INT64_MAX;
+                for (int g = 0; g < rgs; ++g) {
+                    int64_t mx = 0, sum = 0;
+                    for (int64_t b = 0; b < bands; ++b) {
+                        const int64_t v = load[g * bands + b] + n_items[sr * bands + b];
+                        mx = std::max(mx, v);
+                        sum += v;
+                    }
+                    if (mx < best_max || (mx == best_max && sum < best_sum)) best = g, best_max = mx, best_sum = sum;
+                }
+                stripe_rg[sr] = best;
+                for (int64_t b = 0; b < bands; ++b) load[best * bands + b] += n_items[sr * bands + b];
+            }
         }
         std::vector<std::vector<int32_t>> bins(kNumXcd);
         for (size_t u = 0; u < o.items.size(); ++u)
@@ -701,12 +735,15 @@ int build_sddmm_schedule(const bsp_bsr_desc* m, int64_t K, int num_cus, SddmmSch
     const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(8, (160 * 1024) / (320 * K)));
     const int64_t slots = per_cu * num_cus;
     int64_t best_bands = 1, best_rounds = 0, best_bytes = 0;
+    bool best_by_items = false;
     const int64_t forced = env_int("BSP_SDDMM_XCD_COLS", 0);
-    for (int64_t bands : {1, 2, 4}) {
+    for (int64_t cand = 0; cand < 5; ++cand) {
+        const int64_t bands = cand == 0 ? 1 : (cand + 1) / 2 * 2;  // 1, 2, 2, 4, 4
+        const bool by_items = cand > 0 && cand % 2 == 0;
         if (forced && bands != forced) continue;
         if (bands > 1 && ncol32 < 2 * bands) continue;
         SddmmSchedule t;
-        build(bands, t);
+        build(bands, by_items, t);
         const int64_t rounds = ((int64_t)t.wgmap.size() + slots - 1) / slots;
         int64_t worst = 0;
         for (int x = 0; x < kNumXcd; ++x) {
@@ -722,13 +759,14 @@ int build_sddmm_schedule(const bsp_bsr_desc* m, int64_t K, int num_cus, SddmmSch
             }
             worst = std::max(worst, n * 64 * K);
         }
-        if (bands == 1 || forced || rounds < best_rounds || (rounds == best_rounds && worst < best_bytes)) {
+        if (best_rounds == 0 || rounds < best_rounds || (rounds == best_rounds && worst < best_bytes)) {
             best_bands = bands;
+            best_by_items = by_items;
             best_rounds = rounds;
             best_bytes = worst;
         }
     }
-    build(best_bands, s);
+    build(best_bands, best_by_items, s);
     return BSP_OK;
 }
 

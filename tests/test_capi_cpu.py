@@ -272,6 +272,20 @@ def test_sddmm_schedule_covers_every_output_sub_block_once():
         np.testing.assert_array_equal(np.sort(wg[wg >= 0]), np.arange(len(sch["items"])))
 
 
+def test_sddmm_schedule_uniform_mask_two_column_bands_one_round():
+    """The 4096^2 10% mask at K=256: stripes balanced by item count over four
+    row groups let each XCD take one half of the mask's columns (half of Y)
+    with every item still in one round of two workgroups per compute unit."""
+    m = W.workload_sddmm()["mask"]
+    sch = capi.sddmm_schedule(capi.Bsr(m.H, m.W, m.R, m.C, m.indptr, m.indices), 256, 256)
+    assert sch["info"]["grid"] <= 2 * 256
+    wg, items, cols = sch["wgmap"], sch["items"], sch["ent_row"]
+    for x in range(8):
+        us = wg[x::8]
+        halves = {int(cols[e]) * 2 // m.W for u in us[us >= 0] for e in range(items[u][1], items[u][2])}
+        assert len(halves) == 1, f"XCD {x} reads both column halves"
+
+
 @pytest.mark.parametrize("group,R,C", [(2, 64, 64), (4, 128, 32), (8, 256, 256), (2, 128, 64)])
 @pytest.mark.parametrize("split", [None, 2])
 def test_spmm_schedule_row_groups(monkeypatch, group, R, C, split):
