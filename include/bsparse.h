@@ -117,6 +117,10 @@ typedef struct bsp_plan_info {
     int32_t step_entries;/* SpMM: entries per ring step, i.e. per workgroup
                             barrier (1, or 2 for the persistent kernel's
                             paired steps); 0 for other kinds */
+    int32_t stripes_per_unit; /* SpMM: 32-row stripes per persistent unit (2:
+                            stripe pairs that share one B slice per shared
+                            block column; n_items then counts pair x tile
+                            units); 1 otherwise; 0 for other kinds */
 } bsp_plan_info;
 
 /* ---- library ------------------------------------------------------------- */

@@ -64,6 +64,7 @@ class PlanInfo(ctypes.Structure):
         ("persistent", c_int32),
         ("a_stages", c_int32),
         ("step_entries", c_int32),
+        ("stripes_per_unit", c_int32),
     ]
 
     def as_dict(self) -> dict:

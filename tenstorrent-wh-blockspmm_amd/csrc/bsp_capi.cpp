@@ -33,10 +33,11 @@ struct bsp_plan {
     int32_t wg_per_xcd = 0;
     int32_t sddmm_one_shot = 0;  // SDDMM: the one-shot kernel runs this plan
     // SpMM persistent kernel: variant, unit records and A words (the B words
-    // go in d_ent_off, the workgroup records in d_wgs).
+    // go in d_ent_off, the workgroup heads in d_wgs; d_apw with stripe pairs).
     bsp::SpmmStreamVariant stream_variant{};
     bsp::SpmmStreamUnit* d_units = nullptr;
     uint32_t* d_aw = nullptr;
+    uint64_t* d_apw = nullptr;
 };
 
 namespace {
@@ -85,8 +86,10 @@ void free_plan_buffers(bsp_plan* p) {
     if (p->d_runs) (void)hipFree(p->d_runs);
     if (p->d_units) (void)hipFree(p->d_units);
     if (p->d_aw) (void)hipFree(p->d_aw);
+    if (p->d_apw) (void)hipFree(p->d_apw);
     p->d_units = nullptr;
     p->d_aw = nullptr;
+    p->d_apw = nullptr;
     p->d_terms = nullptr;
     p->d_runs = nullptr;
     p->d_wgs = nullptr;
@@ -139,6 +142,7 @@ void fill_info_spmm(const bsp::SpmmSchedule& s, bsp_plan_info* info) {
     }
     info->stages = v.stages;
     info->step_entries = 1;
+    info->stripes_per_unit = 1;
     info->group = s.group;
     // Row groups on 256-column tiles run eight waves (two per SIMD) unless
     // BSP_SPMM_WIDE_WAVES=4 asks for four (groups of 2 or 4 stripes only: four
@@ -259,15 +263,40 @@ bool choose_spmm_stream(const bsp_bsr_desc* a, int64_t N, int cus, SpmmStreamVar
     const int64_t group = env_int("BSP_SPMM_GROUP", bsp::spmm_choose_group(a->R, a->H, N, cus));
     if (group > 1 && (a->R / bsp::kSub) % group == 0) return false;
     bsp::SpmmStreamVariant v = bsp::kSpmmStreamDefault;
+    // Stripe pairs (32x32 blocks): one workgroup per compute unit streams a
+    // pair's union of block columns, so they pay only when the pairs share
+    // most of their columns (block rows with near-identical patterns: 4096^2
+    // x 512 with identical pairs, 14.3-14.9 against 18.3-19.4 us) and still
+    // give every compute unit a unit of its own.  On uniform-random rows the
+    // pairs share 20% (25% density) or 30% (50%) of their blocks, and the
+    // single-stripe kernel stays faster (13.1-13.4 against 16.4-16.7 us; 21.5
+    // -22.8 against 23.7-23.9).  Taken at 40% shared and more.
+    // BSP_SPMM_PAIRS=0 turns them off, 2 takes them whenever the structure
+    // allows.
+    const int64_t pairs_mode = env_int("BSP_SPMM_PAIRS", 1);
+    bool pairs_ok = false;
+    if (pairs_mode > 0 && N % 128 == 0) {
+        std::vector<std::pair<int32_t, int32_t>> pl;
+        int64_t shared = 0;
+        if (bsp::spmm_stripe_pairs(a, 2048, pl, &shared))
+            pairs_ok = pairs_mode == 2 ||
+                       (10 * shared >= 4 * a->nblocks && (int64_t)pl.size() * (N / 128) >= (int64_t)cus);
+    }
     const char* forced = std::getenv("BSP_SPMM_STREAM_VARIANT");
     if (forced) {
         bsp::SpmmStreamVariant w{};
-        const int got = std::sscanf(forced, "%d,%d,%d,%d,%d,%d", &w.tile_n, &w.sb, &w.sa, &w.nbw, &w.pipes, &w.eps);
+        const int got = std::sscanf(forced, "%d,%d,%d,%d,%d,%d,%d", &w.tile_n, &w.sb, &w.sa, &w.nbw, &w.pipes, &w.eps,
+                                    &w.sr);
         if (got < 5) w.pipes = 1;
         if (got < 6) w.eps = 1;
-        if (got >= 4 && bsp::spmm_stream_variant_supported(w) && N % w.tile_n == 0) v = w;
+        if (got < 7) w.sr = 1;
+        if (got >= 4 && bsp::spmm_stream_variant_supported(w) && N % w.tile_n == 0 && (w.sr == 1 || pairs_ok)) v = w;
     }
     int w = -1;
+    if (!forced && pairs_ok) {
+        v = bsp::kSpmmStreamPairs;
+        w = 1;
+    }
     // Many units per workgroup with some longer than a workgroup's share (a
     // skewed row distribution): one workgroup per compute unit with four B
     // loaders and deep rings streams the compute unit's units back to back,
@@ -276,7 +305,7 @@ bool choose_spmm_stream(const bsp_bsr_desc* a, int64_t N, int cus, SpmmStreamVar
     // workgroups, 37.7-38.2 with this variant; with one unit per workgroup,
     // as at uniform 1-50%, two workgroups stay faster: 25% 14.2 against 16.0
     // us.)
-    if (!forced && a->R == bsp::kSub) {
+    if (!forced && !pairs_ok && a->R == bsp::kSub) {
         const int64_t n_tiles = N / 128, stripes = a->H / bsp::kSub;
         int64_t longest = 0;
         for (int64_t i = 0; i < a->H / a->R; ++i) longest = std::max<int64_t>(longest, a->indptr[i + 1] - a->indptr[i]);
@@ -290,7 +319,8 @@ bool choose_spmm_stream(const bsp_bsr_desc* a, int64_t N, int cus, SpmmStreamVar
     }
     const int lds = bsp::spmm_stream_lds_bytes(v);
     if (w < 0) w = v.pipes > 1 ? 1 : std::max(1, std::min(2, bsp::kLdsBytesPerCu / lds));
-    if (v.pipes == 1) w = (int)env_int("BSP_SPMM_STREAM_WPC", w);
+    if (v.pipes == 1 && v.sr == 1) w = (int)env_int("BSP_SPMM_STREAM_WPC", w);
+    if (v.sr == 2) w = 1;  // one unit (a stripe pair) per compute unit
     if (w < 1 || w * lds > bsp::kLdsBytesPerCu) w = 1;
     *sv = v;
     *wpc = w;
@@ -310,7 +340,7 @@ int make_spmm_stream_plan(bsp_plan** out, const bsp_bsr_desc* a, int64_t N, int 
     std::string msg;
     bsp::SpmmStream ss;
     const int cg = (int)env_int("BSP_SPMM_XCD_COLS", 0);
-    int st = bsp::build_spmm_stream(a, N, cus, sv.tile_n, wpc, ss, msg, cg, sv.pipes);
+    int st = bsp::build_spmm_stream(a, N, cus, sv.tile_n, wpc, ss, msg, cg, sv.pipes, sv.sr == 2);
     if (st != BSP_OK) return fail(st, msg);
     DeviceGuard g(device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
@@ -337,14 +367,15 @@ int make_spmm_stream_plan(bsp_plan** out, const bsp_bsr_desc* a, int64_t N, int 
     in.max_item_entries = ss.max_wg_entries;
     in.stages = sv.sb;
     in.group = 1;
-    in.waves = (5 + sv.nbw) * sv.pipes;
+    in.waves = (4 * sv.sr + 1 + sv.nbw) * sv.pipes;
     in.persistent = sv.pipes;
     in.a_stages = sv.sa;
     in.step_entries = sv.eps;
+    in.stripes_per_unit = sv.sr;
     hipError_t e = upload((bsp::SpmmStreamHead**)&p->d_wgs, ss.heads);
     if (e == hipSuccess) e = upload(&p->d_units, ss.units);
     if (e == hipSuccess) e = upload(&p->d_ent_off, ss.bw);
-    if (e == hipSuccess) e = upload(&p->d_aw, ss.aw);
+    if (e == hipSuccess) e = ss.pairs ? upload(&p->d_apw, ss.apw) : upload(&p->d_aw, ss.aw);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         free_plan_buffers(p);
@@ -472,6 +503,7 @@ int bsp_spmm(const bsp_plan* p, const uint16_t* a_vals, const uint16_t* b, int64
         sa.units = p->d_units;
         sa.bw = p->d_ent_off;
         sa.aw = p->d_aw;
+        sa.apw = p->d_apw;
         sa.ldb = ldb;
         sa.ldc = ldc;
         sa.lda = (int32_t)p->C;

@@ -150,6 +150,17 @@ __device__ __forceinline__ void gl_lds16_s(uint32_t voff_bytes, const void* sbas
         : "memory");
 }
 
+// The same with 4 bytes per lane (lane i's dword lands at M0 + 4i).
+__device__ __forceinline__ void gl_lds4_s(uint32_t voff_bytes, const void* sbase, uint32_t lds_wave_base) {
+    const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_wave_base);
+    __asm__ volatile(
+        "s_mov_b32 m0, %2\n\t"
+        "global_load_lds_dword %0, %1"
+        :
+        : "v"(voff_bytes), "s"(sbase), "s"(lds)
+        : "memory");
+}
+
 // Workgroup barrier without a memory fence (a fence would wait for all
 // outstanding loads); the empty asm statements keep the compiler from moving
 // memory accesses across it.
@@ -901,6 +912,11 @@ __global__ __launch_bounds__(64 * NW, RW <= 4 && S == 3 ? 2 : 1) void spmm_group
 //     their stores never sit in front of a load in a wave's queue;
 //   - waves 4 .. 4+NBW-1 (B loaders) issue the B slice of each entry;
 //   - wave 4+NBW (A loader) issues the entry's A sub-block.
+// With stripe pairs (SR = 2) a unit is two stripes that share block columns
+// and an entry is one block column of their union: one B slice serves both
+// stripes.  The A stage holds both stripes' sub-blocks, waves 0-3 work for the
+// first stripe and waves 4-7 for the second (the loaders follow them), and a
+// wave whose stripe has no block in the entry's column skips its products.
 // A sub-blocks mostly miss to HBM while B slices mostly hit in L2.  A wave's
 // loads return in order, so an A miss at the head of a wave's queue holds back
 // the B hits behind it: with the two in separate waves, a 2 MB L2-resident
@@ -1049,15 +1065,22 @@ __device__ __forceinline__ void stream_loader2(int n, const WT* head, const WT* 
 // With EPS = 2 (one pipeline) every step covers two entries: one barrier per
 // pair, the MFMA waves reading both entries of a step into one register set
 // while multiplying the previous pair from the other (stream_loader2).
-template <int NTW, int SB, int SA, int NBW, int PIPES, bool OUT_BF16, int EPS>
-__global__ __launch_bounds__(64 * (5 + NBW) * PIPES) void spmm_stream_kernel(SpmmStreamArgs p) {
+template <int NTW, int SB, int SA, int NBW, int PIPES, bool OUT_BF16, int EPS, int SR>
+__global__ __launch_bounds__(64 * (4 * SR + 1 + NBW) * PIPES) void spmm_stream_kernel(SpmmStreamArgs p) {
     using namespace spmm_detail;
     static_assert(EPS == 1 || (EPS == 2 && PIPES == 1), "two entries per step with one pipeline");
+    static_assert(SR == 1 || (SR == 2 && EPS == 2), "stripe pairs run two entries per step");
     constexpr int TN = 128 * NTW;
     using Loader = BSliceLoader<TN, NBW>;
-    constexpr int A_RING = SA * kA_BYTES;
-    constexpr int PIPE_LDS = A_RING + SB * Loader::BYTES;
-    constexpr int WPP = 5 + NBW;                                 // waves per pipeline
+    constexpr int A_STAGE = SR * kA_BYTES;  // one A sub-block per stripe of the unit
+    constexpr int A_RING = SA * A_STAGE;
+    // Stripe pairs: the entry's 8-byte A word per A stage (a half equal to
+    // kNoBlock: that stripe has no block in the entry's column), after the
+    // rings.
+    constexpr int FLAGS = A_RING + SB * Loader::BYTES;
+    constexpr int PIPE_LDS = FLAGS + (SR > 1 ? 8 * SA : 0);
+    constexpr int MW = 4 * SR;                                   // MFMA waves: four per stripe of a unit
+    constexpr int WPP = MW + 1 + NBW;                            // waves per pipeline
     constexpr int XCHG = PIPES > 1 ? 4 * NTW * 16 * 64 * 4 : 0;  // fp32 tile of the shared unit
     static_assert(PIPES == 1 || PIPES == 2, "pipelines");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[PIPES * PIPE_LDS + XCHG];
@@ -1085,15 +1108,45 @@ __global__ __launch_bounds__(64 * (5 + NBW) * PIPES) void spmm_stream_kernel(Spm
         if constexpr (PIPES > 1) barrier_no_fence();
     };
 
-    if (wave == 4 + NBW) {
+    if (wave == MW + NBW) {
         // A loader: load j (1 KB) covers segments 2j and 2j+1 of the 32x32
         // sub-block (lanes 0-31 and 32-63), in the layout of a_load_offset.
         uint32_t a_voff[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) a_voff[j] = 2 * a_load_offset(2 * j + (lane >> 5), lane, p.lda);
+        if constexpr (SR == 2) {
+            // Stripe pairs: both halves of the stage; a half whose stripe has no
+            // block here gets two 16-byte loads by lane 0 (from the other
+            // half's sub-block, into its own stale slot), so that every entry
+            // issues the same five loads and the vmcnt waits keep their counts.
+            // The fifth brings the entry's A word into the stage's word slot
+            // (lanes 0 and 1, 4 bytes each) through the same DMA path, so the
+            // loader's wait for the entry covers it too.
+            const void* words = p.apw + wg.w_begin;
+            auto issue_pair = [&](int e, uint64_t w) {
+                const uint32_t st = (uint32_t)(e % SA);
+                const uint32_t w0 = (uint32_t)w, w1 = (uint32_t)(w >> 32);
+                const uint32_t any = w0 != kNoBlock ? w0 : w1;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t wh = h == 0 ? w0 : w1;
+                    const bool here = wh != kNoBlock;
+                    const uint16_t* ablk = p.a + (int64_t)(here ? wh : any) * 32;
+                    const uint32_t dst = lds0 + st * A_STAGE + h * kA_BYTES;
+                    if (here || lane == 0) {
+                        gl_lds16_s(a_voff[0], ablk, dst);
+                        gl_lds16_s(a_voff[1], ablk, dst + 1024);
+                    }
+                }
+                if (lane < 2) gl_lds4_s((uint32_t)e * 8 + lane * 4, words, lds0 + FLAGS + st * 8);
+            };
+            stream_loader2<SA, 5>(n, head->apw, p.apw + wg.w_begin, issue_pair);
+            idle_steps();
+            return;
+        }
         auto issue_a = [&](int e, uint32_t w) {
             const uint16_t* ablk = p.a + (int64_t)w * 32;
-            const uint32_t dst = lds0 + (uint32_t)(e % SA) * kA_BYTES;
+            const uint32_t dst = lds0 + (uint32_t)(e % SA) * A_STAGE;
             gl_lds16_s(a_voff[0], ablk, dst);
             gl_lds16_s(a_voff[1], ablk, dst + 1024);
         };
@@ -1104,8 +1157,8 @@ __global__ __launch_bounds__(64 * (5 + NBW) * PIPES) void spmm_stream_kernel(Spm
         idle_steps();
         return;
     }
-    if (wave >= 4) {
-        const int wb = wave - 4;
+    if (wave >= MW) {
+        const int wb = wave - MW;
         const Loader ld(wb, lane, p.ldb);
         const uint32_t b_lds = lds0 + A_RING + wb * Loader::BI * 1024;
         auto issue_b = [&](int e, int64_t w) {
@@ -1122,10 +1175,12 @@ __global__ __launch_bounds__(64 * (5 + NBW) * PIPES) void spmm_stream_kernel(Spm
         return;
     }
 
-    // MFMA waves: wave w owns columns w*NTW*32 .. of each unit's tile.
+    // MFMA waves: wave w owns stripe w/4 of the unit (the first stripe, or
+    // with stripe pairs the second) and columns (w%4)*NTW*32 .. of its tile.
     const int l32 = lane & 31, q = lane >> 5;
-    const BReads<TN, NTW> brd(lane, wave * NTW * 32, false);
-    const int a_rd = a_read_offset(l32, q);
+    const int half = wave >> 2, wc = wave & 3;
+    const BReads<TN, NTW> brd(lane, wc * NTW * 32, false);
+    const int a_rd = a_read_offset(l32, q) + half * kA_BYTES;
     f32x16 acc[NTW];
 #pragma unroll
     for (int i = 0; i < NTW; ++i)
@@ -1142,11 +1197,15 @@ __global__ __launch_bounds__(64 * (5 + NBW) * PIPES) void spmm_stream_kernel(Spm
     SpmmStreamUnit nxt = load_const(&head->u[1]);
     SpmmStreamUnit held{};  // the shared unit, stored after the exchange (flag 2)
     bool holding = false;
+    // Stores this wave's part of the unit's tile (with stripe pairs, of its
+    // stripe; the second stripe of an odd one out is -1).
     auto store_unit = [&](const SpmmStreamUnit& un) {
-        const int64_t row0 = (int64_t)un.row * 32;
+        const int32_t stripe = half == 0 ? un.row : un.aux;
+        if (SR > 1 && stripe < 0) return;
+        const int64_t row0 = (int64_t)stripe * 32;
 #pragma unroll
         for (int nt = 0; nt < NTW; ++nt) {
-            const int64_t col = un.n0 + wave * (NTW * 32) + nt * 32 + l32;
+            const int64_t col = un.n0 + wc * (NTW * 32) + nt * 32 + l32;
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int64_t row = row0 + 8 * (v >> 2) + 4 * q + (v & 3);
@@ -1167,13 +1226,13 @@ __global__ __launch_bounds__(64 * (5 + NBW) * PIPES) void spmm_stream_kernel(Spm
     // Ends unit `cur`: store it, or (two pipelines) leave it in the exchange
     // buffer, or hold it for the exchange.
     auto finish_cur = [&] {
-        if (PIPES > 1 && cur.pad == 1) {
+        if (PIPES > 1 && cur.aux == 1) {
 #pragma unroll
             for (int nt = 0; nt < NTW; ++nt)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) *xchg_at(nt, v) = acc[nt][v];
             zero_acc();
-        } else if (PIPES > 1 && cur.pad == 2) {
+        } else if (PIPES > 1 && cur.aux == 2) {
             held = cur;
             holding = true;
         } else {
@@ -1206,18 +1265,24 @@ __global__ __launch_bounds__(64 * (5 + NBW) * PIPES) void spmm_stream_kernel(Spm
     struct Operands {
         u32x4 a[2];
         u32x4 b[2][NTW];
+        uint32_t w;  // stripe pairs: this wave's stripe's half of the entry's A word
     };
     auto read = [&](int k, Operands& o) {
-        const uint8_t* as = psmem + (k % SA) * kA_BYTES;
+        const uint8_t* as = psmem + (k % SA) * A_STAGE;
         o.a[0] = *(const u32x4*)(as + a_rd);
         o.a[1] = *(const u32x4*)(as + 256 + a_rd);
+        if constexpr (SR > 1) o.w = *(const uint32_t*)(psmem + FLAGS + (k % SA) * 8 + half * 4);
         brd.read(psmem + A_RING + (k % SB) * Loader::BYTES, o.b);
     };
     auto multiply = [&](const Operands& o) {
+        // With stripe pairs, a wave whose stripe has no block in the entry's
+        // column skips its products (the word was read in an earlier step).
+        if (SR == 1 || __builtin_amdgcn_readfirstlane(o.w) != kNoBlock) {
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2)
+            for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-            for (int nt = 0; nt < NTW; ++nt) acc[nt] = mfma32(o.a[s2], o.b[s2][nt], acc[nt]);
+                for (int nt = 0; nt < NTW; ++nt) acc[nt] = mfma32(o.a[s2], o.b[s2][nt], acc[nt]);
+        }
         if (--left == 0) {
             finish_cur();
             left = next_unit();
@@ -2097,14 +2162,15 @@ hipError_t launch_spmm(const SpmmArgs& a, const SpmmVariant& v, bool out_bf16, i
 hipError_t launch_spmm_stream(const SpmmStreamArgs& a, const SpmmStreamVariant& v, bool out_bf16, int grid,
                               hipStream_t stream) {
     if (grid <= 0) return hipSuccess;
-#define BSP_STREAM_CASE(TN, SB, SA, NB, PP, EPS)                                                                  \
-    if (v.tile_n == TN && v.sb == SB && v.sa == SA && v.nbw == NB && v.pipes == PP && v.eps == EPS) {            \
+#define BSP_STREAM_CASE(TN, SB, SA, NB, PP, EPS, SR)                                                              \
+    if (v.tile_n == TN && v.sb == SB && v.sa == SA && v.nbw == NB && v.pipes == PP && v.eps == EPS &&            \
+        v.sr == SR) {                                                                                            \
         if (out_bf16)                                                                                            \
-            hipLaunchKernelGGL((spmm_stream_kernel<TN / 128, SB, SA, NB, PP, true, EPS>), dim3(grid),              \
-                               dim3(64 * (5 + NB) * PP), 0, stream, a);                                          \
+            hipLaunchKernelGGL((spmm_stream_kernel<TN / 128, SB, SA, NB, PP, true, EPS, SR>), dim3(grid),          \
+                               dim3(64 * (4 * SR + 1 + NB) * PP), 0, stream, a);                                 \
         else                                                                                                     \
-            hipLaunchKernelGGL((spmm_stream_kernel<TN / 128, SB, SA, NB, PP, false, EPS>), dim3(grid),             \
-                               dim3(64 * (5 + NB) * PP), 0, stream, a);                                          \
+            hipLaunchKernelGGL((spmm_stream_kernel<TN / 128, SB, SA, NB, PP, false, EPS, SR>), dim3(grid),         \
+                               dim3(64 * (4 * SR + 1 + NB) * PP), 0, stream, a);                                 \
         return hipGetLastError();                                                                                \
     }
     BSP_SPMM_STREAM_VARIANTS(BSP_STREAM_CASE)

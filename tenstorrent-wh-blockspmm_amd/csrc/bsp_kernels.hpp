@@ -27,7 +27,7 @@ struct SpmmArgs {
 };
 
 // Persistent SpMM (spmm_stream_kernel): each workgroup streams the entries of
-// its units (stripe x tile) through one ring.
+// its units (stripe or stripe pair x tile) through one ring.
 struct SpmmStreamArgs {
     const uint16_t* a;             // A block values (bf16)
     const uint16_t* b;             // B (bf16), row-major K x N, leading dim ldb
@@ -35,7 +35,8 @@ struct SpmmStreamArgs {
     const SpmmStreamHead* heads;   // one per workgroup (per pipeline)
     const SpmmStreamUnit* units;   // unit records (padded)
     const int64_t* bw;             // per stream entry: first row of B | first column << 32 (padded)
-    const uint32_t* aw;            // per stream entry: A sub-block offset / 32 (padded)
+    const uint32_t* aw;            // per stream entry: A sub-block offset / 32 (padded; one stripe)
+    const uint64_t* apw;           // stripe pairs: per stream entry, both stripes' A offsets / 32 (padded)
     int64_t ldb;
     int64_t ldc;
     int32_t lda;                   // row stride inside an A block (= C)
@@ -43,25 +44,27 @@ struct SpmmStreamArgs {
 };
 
 // Compiled persistent SpMM variants: tile width, B ring depth, A ring depth,
-// B loader waves, pipelines per workgroup, entries per ring step.  A pipeline
-// has 4 MFMA waves (each 32*tile/128 columns), the B loader waves and one A
-// loader wave, and LDS of 64*tile*SB + 2 KB*SA; two pipelines add a 16 KB
+// B loader waves, pipelines per workgroup, entries per ring step, stripes per
+// unit.  A pipeline has 4 MFMA waves (each 32*tile/128 columns), the B loader
+// waves and one A loader wave, and LDS of 64*tile*SB + 2 KB*SA*stripes (+ 8
+// bytes*SA of A words with stripe pairs); two pipelines add a 16 KB
 // (32 KB at tile 256) exchange buffer.  With two entries per step (one
 // pipeline, even ring depths of at most 16) the workgroup passes one barrier
-// per pair of entries.
+// per pair of entries; stripe pairs need two entries per step.
 #define BSP_SPMM_STREAM_VARIANTS(X) \
-    X(128, 8, 8, 2, 1, 2)           \
-    X(128, 14, 16, 4, 1, 2)         \
-    X(128, 6, 12, 2, 1, 2)          \
-    X(128, 6, 12, 2, 1, 1)          \
-    X(128, 6, 12, 4, 1, 1)          \
-    X(128, 4, 16, 4, 1, 1)          \
-    X(128, 8, 16, 8, 1, 1)          \
-    X(256, 4, 16, 4, 1, 1)          \
-    X(256, 5, 16, 8, 1, 1)          \
-    X(256, 6, 8, 8, 1, 1)           \
-    X(128, 6, 12, 2, 2, 1)          \
-    X(128, 5, 12, 2, 2, 1)
+    X(128, 8, 8, 2, 1, 2, 1)        \
+    X(128, 14, 16, 4, 1, 2, 1)      \
+    X(128, 8, 8, 2, 1, 2, 2)        \
+    X(128, 6, 12, 2, 1, 2, 1)       \
+    X(128, 6, 12, 2, 1, 1, 1)       \
+    X(128, 6, 12, 4, 1, 1, 1)       \
+    X(128, 4, 16, 4, 1, 1, 1)       \
+    X(128, 8, 16, 8, 1, 1, 1)       \
+    X(256, 4, 16, 4, 1, 1, 1)       \
+    X(256, 5, 16, 8, 1, 1, 1)       \
+    X(256, 6, 8, 8, 1, 1, 1)        \
+    X(128, 6, 12, 2, 2, 1, 1)       \
+    X(128, 5, 12, 2, 2, 1, 1)
 
 struct SpmmStreamVariant {
     int tile_n;
@@ -70,22 +73,28 @@ struct SpmmStreamVariant {
     int nbw;
     int pipes = 1;
     int eps = 1;  // entries per ring step
+    int sr = 1;   // stripes per unit (2: stripe pairs)
 };
 
-// The default (uniform rows) and the skewed-row choice of choose_spmm_stream.
-constexpr SpmmStreamVariant kSpmmStreamDefault{128, 8, 8, 2, 1, 2};
-constexpr SpmmStreamVariant kSpmmStreamSkewed{128, 14, 16, 4, 1, 2};
+// The default (uniform rows), the skewed-row and the stripe-pair choices of
+// choose_spmm_stream.
+constexpr SpmmStreamVariant kSpmmStreamDefault{128, 8, 8, 2, 1, 2, 1};
+constexpr SpmmStreamVariant kSpmmStreamSkewed{128, 14, 16, 4, 1, 2, 1};
+constexpr SpmmStreamVariant kSpmmStreamPairs{128, 8, 8, 2, 1, 2, 2};
 
 inline bool spmm_stream_variant_supported(const SpmmStreamVariant& v) {
-#define BSP_SPMM_STREAM_MATCH(TN, SB, SA, NB, PP, EPS) \
-    if (v.tile_n == TN && v.sb == SB && v.sa == SA && v.nbw == NB && v.pipes == PP && v.eps == EPS) return true;
+#define BSP_SPMM_STREAM_MATCH(TN, SB, SA, NB, PP, EPS, SR)                                           \
+    if (v.tile_n == TN && v.sb == SB && v.sa == SA && v.nbw == NB && v.pipes == PP && v.eps == EPS && \
+        v.sr == SR)                                                                                  \
+        return true;
     BSP_SPMM_STREAM_VARIANTS(BSP_SPMM_STREAM_MATCH)
 #undef BSP_SPMM_STREAM_MATCH
     return false;
 }
 
 inline int spmm_stream_lds_bytes(const SpmmStreamVariant& v) {
-    return v.pipes * (64 * v.tile_n * v.sb + 2048 * v.sa) + (v.pipes > 1 ? 4 * (v.tile_n / 128) * 16 * 64 * 4 : 0);
+    return v.pipes * (64 * v.tile_n * v.sb + 2048 * v.sa * v.sr + (v.sr > 1 ? 8 * v.sa : 0)) +
+           (v.pipes > 1 ? 4 * (v.tile_n / 128) * 16 * 64 * 4 : 0);
 }
 
 hipError_t launch_spmm_stream(const SpmmStreamArgs& a, const SpmmStreamVariant& v, bool out_bf16, int grid,

@@ -83,9 +83,11 @@ extern "C" int bsp_spmm_noalloc(const bsp_bsr_desc* a, const uint16_t* a_vals, c
         return bsp::record_error(BSP_ERR_UNSUPPORTED, "bsp_spmm_noalloc needs N a multiple of 128 (the persistent "
                                                       "kernel's tile); use a plan for other N");
 
-    // The schedule, built on the host exactly as a plan builds it (same
-    // variant choice, one pipeline per workgroup), for 256 compute units per
-    // 8 XCDs unless the device says otherwise.
+    // The schedule, built on the host as a plan builds it (same variant
+    // choice, but one pipeline per workgroup and one stripe per unit: a plan
+    // that would take stripe pairs runs the default variant here, with the
+    // same per-stripe summation order), for 256 compute units per 8 XCDs
+    // unless the device says otherwise.
     int cus = 256;
     int count = 0;
     if (hipGetDeviceCount(&count) == hipSuccess && device < count) {
@@ -94,7 +96,7 @@ extern "C" int bsp_spmm_noalloc(const bsp_bsr_desc* a, const uint16_t* a_vals, c
     }
     bsp::SpmmStreamVariant sv = bsp::kSpmmStreamDefault;
     int wpc = 2;
-    if (!bsp::choose_spmm_stream(a, N, cus, &sv, &wpc) || sv.pipes != 1) {
+    if (!bsp::choose_spmm_stream(a, N, cus, &sv, &wpc) || sv.pipes != 1 || sv.sr != 1) {
         sv = bsp::kSpmmStreamDefault;
         wpc = 2;
     }

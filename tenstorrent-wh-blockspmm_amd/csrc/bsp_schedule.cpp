@@ -398,8 +398,62 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
     return BSP_OK;
 }
 
+bool spmm_stripe_pairs(const bsp_bsr_desc* a, int64_t max_rows, std::vector<std::pair<int32_t, int32_t>>& pairs,
+                       int64_t* shared) {
+    pairs.clear();
+    if (shared) *shared = 0;
+    if (!a || a->R != kSub || a->C != kSub || a->H % kSub || a->W % kSub) return false;
+    const int64_t nbr = a->H / kSub, nbc = a->W / kSub;
+    if (nbr < 2 || nbr > max_rows) return false;
+    for (int64_t i = 0; i < nbr; ++i)
+        for (int64_t k = a->indptr[i] + 1; k < a->indptr[i + 1]; ++k)
+            if (a->indices[k] <= a->indices[k - 1]) return false;  // columns must increase strictly
+    // Shared block columns of every two block rows, through the rows of each
+    // column; give up when that costs too much host time.
+    std::vector<std::vector<int32_t>> rows_of(nbc);
+    for (int64_t i = 0; i < nbr; ++i)
+        for (int64_t k = a->indptr[i]; k < a->indptr[i + 1]; ++k) rows_of[a->indices[k]].push_back((int32_t)i);
+    int64_t work = 0;
+    for (const auto& r : rows_of) work += (int64_t)r.size() * (int64_t)r.size();
+    if (work > (int64_t)1 << 26) return false;
+    std::vector<int32_t> ov((size_t)(nbr * nbr), 0);
+    for (const auto& r : rows_of)
+        for (size_t x = 0; x < r.size(); ++x)
+            for (size_t y = x + 1; y < r.size(); ++y) ++ov[(size_t)r[x] * nbr + r[y]];
+    struct Cand {
+        int32_t n, i, j;
+    };
+    std::vector<Cand> cand;
+    for (int64_t i = 0; i < nbr; ++i)
+        for (int64_t j = i + 1; j < nbr; ++j)
+            if (ov[(size_t)i * nbr + j] > 0) cand.push_back({ov[(size_t)i * nbr + j], (int32_t)i, (int32_t)j});
+    std::stable_sort(cand.begin(), cand.end(), [](const Cand& x, const Cand& y) { return x.n > y.n; });
+    std::vector<char> used(nbr, 0);
+    int64_t sh = 0;
+    for (const Cand& c : cand)
+        if (!used[c.i] && !used[c.j]) {
+            used[c.i] = used[c.j] = 1;
+            pairs.push_back({c.i, c.j});
+            sh += c.n;
+        }
+    int32_t left = -1;
+    for (int64_t i = 0; i < nbr; ++i) {
+        if (used[i]) continue;
+        if (left < 0) {
+            left = (int32_t)i;
+        } else {
+            pairs.push_back({left, (int32_t)i});
+            left = -1;
+        }
+    }
+    if (left >= 0) pairs.push_back({left, -1});
+    std::sort(pairs.begin(), pairs.end());
+    if (shared) *shared = sh;
+    return true;
+}
+
 int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n, int wg_per_cu, SpmmStream& s,
-                      std::string& msg, int col_groups, int pipes) {
+                      std::string& msg, int col_groups, int pipes, bool pairs) {
     int st = validate_bsr(a, msg);
     if (st != BSP_OK) return st;
     if (tile_n != 128 && tile_n != 256) {
@@ -421,8 +475,16 @@ int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n,
         return BSP_ERR_UNSUPPORTED;
     }
     if (pipes == 2) wg_per_cu = 1;
+    std::vector<std::pair<int32_t, int32_t>> pair_list;
+    if (pairs) {
+        if (pipes != 1 || !spmm_stripe_pairs(a, INT32_MAX, pair_list, nullptr)) {
+            msg = "stripe pairs need one pipeline, 32x32 blocks and strictly increasing block columns";
+            return BSP_ERR_UNSUPPORTED;
+        }
+    }
     const int64_t RS = a->R / kSub, CS = a->C / kSub;
-    const int64_t nsr = a->H / kSub;
+    // The scheduled rows: stripes, or stripe pairs (row = the pair's index).
+    const int64_t nsr = pairs ? (int64_t)pair_list.size() : a->H / kSub;
     const int64_t n_tiles = N / tile_n;
     const int64_t per_stripe_total = a->nblocks * CS;  // entries summed over one stripe of every block row
     if (per_stripe_total * RS * n_tiles > INT32_MAX - kStreamPad || nsr > INT32_MAX || a->W > INT32_MAX ||
@@ -434,6 +496,7 @@ int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n,
     s.tile_n = tile_n;
     s.n_tiles = (int32_t)n_tiles;
     s.wg_per_cu = wg_per_cu;
+    s.pairs = pairs ? 1 : 0;
 
     // Column groups: the fewest (1, 2, 4, 8) that bring one XCD's slice of B
     // to at most 2 MiB, limited by the tile count (or as asked).
@@ -447,10 +510,33 @@ int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n,
 
     // Stripe entry counts; a unit costs its entries plus the store.
     constexpr int64_t kStoreCost = 2;
+    // A pair's entries: the union of its two block rows' columns, merged in
+    // column order (each row's own blocks keep their CSR order); emit(col,
+    // blk0, blk1) with -1 for a row without a block in that column.
+    auto merge = [&](int32_t r0, int32_t r1, auto&& emit_one) {
+        int64_t k0 = a->indptr[r0], k1 = r1 >= 0 ? a->indptr[r1] : 0;
+        const int64_t e0 = a->indptr[r0 + 1], e1 = r1 >= 0 ? a->indptr[r1 + 1] : 0;
+        while (k0 < e0 || k1 < e1) {
+            const int32_t c0 = k0 < e0 ? a->indices[k0] : INT32_MAX, c1 = k1 < e1 ? a->indices[k1] : INT32_MAX;
+            if (c0 == c1) {
+                emit_one(c0, k0++, k1++);
+            } else if (c0 < c1) {
+                emit_one(c0, k0++, (int64_t)-1);
+            } else {
+                emit_one(c1, (int64_t)-1, k1++);
+            }
+        }
+    };
     std::vector<int64_t> cnt(nsr);
     for (int64_t sr = 0; sr < nsr; ++sr) {
-        const int64_t i = sr / RS;
-        cnt[sr] = (int64_t)(a->indptr[i + 1] - a->indptr[i]) * CS;
+        if (pairs) {
+            int64_t n = 0;
+            merge(pair_list[sr].first, pair_list[sr].second, [&](int32_t, int64_t, int64_t) { ++n; });
+            cnt[sr] = n;
+        } else {
+            const int64_t i = sr / RS;
+            cnt[sr] = (int64_t)(a->indptr[i + 1] - a->indptr[i]) * CS;
+        }
     }
     // Stripes onto row groups, longest first onto the least-loaded group.
     std::vector<int32_t> order(nsr);
@@ -494,8 +580,13 @@ int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n,
             const int x = (int)(rg * cg + c);
             std::vector<SpmmStreamUnit> us;
             for (int32_t sr : rows[rg])  // rows[rg] is longest first
-                for (int64_t t = c * tpg; t < (c + 1) * tpg; ++t)
-                    us.push_back({sr, (int32_t)(t * tile_n), (int32_t)cnt[sr], 0});
+                for (int64_t t = c * tpg; t < (c + 1) * tpg; ++t) {
+                    if (pairs)
+                        us.push_back({pair_list[sr].first, (int32_t)(t * tile_n), (int32_t)cnt[sr],
+                                      pair_list[sr].second});
+                    else
+                        us.push_back({sr, (int32_t)(t * tile_n), (int32_t)cnt[sr], 0});
+                }
             std::vector<std::vector<SpmmStreamUnit>> per_cu, per_wg;
             lpt(us, cus_per_xcd, per_cu);
             for (int cu = 0; cu < cus_per_xcd; ++cu) {
@@ -529,9 +620,9 @@ int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n,
             } else {  // straddles the cut
                 SpmmStreamUnit a0 = u, a1 = u;
                 a0.count = (int32_t)(cut - b);
-                a0.pad = 2;
+                a0.aux = 2;
                 a1.count = (int32_t)(e - cut);
-                a1.pad = 1;
+                a1.aux = 1;
                 p0.push_back({a0, 0, a0.count});
                 p1.insert(p1.begin(), {a1, a0.count, u.count});
             }
@@ -545,6 +636,15 @@ int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n,
         w.n_units = (int32_t)parts.size();
         for (const Part& pt : parts) {
             s.units.push_back(pt.u);
+            if (pairs) {
+                merge(pt.u.row, pt.u.aux, [&](int32_t col, int64_t k0, int64_t k1) {
+                    const uint64_t w0 = k0 >= 0 ? (uint64_t)(k0 * a->R * a->C / kSub) : kNoBlock;
+                    const uint64_t w1 = k1 >= 0 ? (uint64_t)(k1 * a->R * a->C / kSub) : kNoBlock;
+                    s.bw.push_back((int64_t)col * a->C | ((int64_t)pt.u.n0 << 32));
+                    s.apw.push_back(w0 | w1 << 32);
+                });
+                continue;
+            }
             const int64_t i = pt.u.row / RS, sub = pt.u.row % RS;
             int64_t e = 0;
             for (int64_t blk = a->indptr[i]; blk < a->indptr[i + 1]; ++blk)
@@ -575,7 +675,10 @@ int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n,
     }
     s.n_entries = (int64_t)s.bw.size();
     s.bw.resize(s.bw.size() + kStreamPad, 0);
-    s.aw.resize(s.aw.size() + kStreamPad, 0);
+    if (pairs)
+        s.apw.resize(s.apw.size() + kStreamPad, 0);
+    else
+        s.aw.resize(s.aw.size() + kStreamPad, 0);
     s.units.resize(s.units.size() + kStreamPad, SpmmStreamUnit{0, 0, 0, 0});
     s.heads.assign(s.wgs.size(), SpmmStreamHead{});
     for (size_t g = 0; g < s.wgs.size(); ++g) {
@@ -585,7 +688,10 @@ int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n,
         for (int j = 0; j < 2; ++j) h.u[j] = s.units[(size_t)w.u_begin + j];
         for (int j = 0; j < kHeadWords; ++j) {
             h.bw[j] = s.bw[(size_t)w.w_begin + j];
-            h.aw[j] = s.aw[(size_t)w.w_begin + j];
+            if (pairs)
+                h.apw[j] = s.apw[(size_t)w.w_begin + j];
+            else
+                h.aw[j] = s.aw[(size_t)w.w_begin + j];
         }
     }
     return BSP_OK;

@@ -71,11 +71,12 @@ struct SpmmSchedule {
 std::vector<SpmmWg> spmm_wg_records(const SpmmSchedule& s);
 
 // ---- persistent SpMM (spmm_stream_kernel) -----------------------------------
-// A unit is one 32-row stripe times one tile of tile_n output columns.  Each
-// workgroup of the persistent grid owns a list of units and streams their
-// entries (32x32 sub-block products) back to back through one LDS ring, so
-// the ring never drains between units and a unit's store overlaps the next
-// unit's loads.
+// A unit is one 32-row stripe (or, with stripe pairs, two stripes that share
+// block columns) times one tile of tile_n output columns.  Each workgroup of
+// the persistent grid owns a list of units and streams their entries (32x32
+// sub-block products; with pairs, one B slice and the A sub-blocks of either
+// or both stripes) back to back through one LDS ring, so the ring never
+// drains between units and a unit's store overlaps the next unit's loads.
 struct SpmmStreamWg {
     int32_t w_begin;  // first word of this workgroup's entry stream
     int32_t n;        // entries in the stream (sum of its units' counts)
@@ -88,8 +89,9 @@ struct SpmmStreamUnit {
     int32_t row;    // stripe (32 output rows)
     int32_t n0;     // first output column
     int32_t count;  // entries (0: the stripe has no nonzeros; its tile is stored as zeros)
-    int32_t pad;    // 0: store the tile; two pipelines: 1 = this part goes to the
-                    // exchange buffer, 2 = add the exchange buffer, then store
+    int32_t aux;    // one stripe: 0 = store the tile; two pipelines: 1 = this part
+                    // goes to the exchange buffer, 2 = add the exchange buffer,
+                    // then store.  Stripe pairs: the second stripe (-1: none)
 };
 static_assert(sizeof(SpmmStreamUnit) == 16, "SpmmStreamUnit layout is shared with the kernels");
 
@@ -97,13 +99,13 @@ static_assert(sizeof(SpmmStreamUnit) == 16, "SpmmStreamUnit layout is shared wit
 // prefetch a few records ahead without a bounds test.
 constexpr int kStreamPad = 64;
 
-// What a workgroup reads first, in 256 contiguous bytes of its own: its
+// What a workgroup reads first, in 384 contiguous bytes of its own: its
 // record, its first two unit records and the first kHeadWords words of each
 // of its entry streams (copies of the arrays' records and words, which the
-// arrays keep as well).  The kernel loads them all at once from an address
-// that depends only on the workgroup id, so the first entry's loads follow
-// one round trip to memory instead of two dependent ones (record, then
-// words).
+// arrays keep as well; apw is zero without stripe pairs).  The kernel loads
+// them all at once from an address that depends only on the workgroup id, so
+// the first entry's loads follow one round trip to memory instead of two
+// dependent ones (record, then words).
 constexpr int kHeadWords = 16;
 struct SpmmStreamHead {
     SpmmStreamWg wg;
@@ -111,8 +113,12 @@ struct SpmmStreamHead {
     int32_t pad[4];
     int64_t bw[kHeadWords];
     uint32_t aw[kHeadWords];
+    uint64_t apw[kHeadWords];
 };
-static_assert(sizeof(SpmmStreamHead) == 256, "SpmmStreamHead layout is shared with the kernels");
+static_assert(sizeof(SpmmStreamHead) == 384, "SpmmStreamHead layout is shared with the kernels");
+
+// An absent A sub-block in a stripe pair's entry word (either half).
+constexpr uint32_t kNoBlock = 0xffffffffu;
 static_assert(kStreamPad >= kHeadWords && kStreamPad >= 2, "heads copy words and units from the padded arrays");
 
 struct SpmmStream {
@@ -120,14 +126,29 @@ struct SpmmStream {
     int32_t n_tiles = 0;
     int32_t wg_per_cu = 1;
     int32_t col_groups = 1;        // column groups of the XCD map
+    int32_t pairs = 0;             // 1: units are stripe pairs (apw holds the A words)
     int32_t max_wg_entries = 0;    // longest workgroup stream
     int64_t n_entries = 0;         // sum over units (entries x tiles)
     std::vector<SpmmStreamWg> wgs;        // one per workgroup; workgroup g runs on XCD g % kNumXcd
     std::vector<SpmmStreamHead> heads;    // one per record of wgs, what the kernel reads first
     std::vector<SpmmStreamUnit> units;    // + kStreamPad zero records
     std::vector<int64_t> bw;              // per stream entry: first row of B | first column << 32 (+ pad)
-    std::vector<uint32_t> aw;             // per stream entry: A sub-block element offset / 32 (+ pad)
+    std::vector<uint32_t> aw;             // per stream entry: A sub-block element offset / 32 (+ pad);
+                                          // empty with stripe pairs
+    std::vector<uint64_t> apw;            // stripe pairs, per stream entry: the two stripes' A offsets
+                                          // / 32 (low: the unit's row, high: its aux), kNoBlock where a
+                                          // stripe has no block in the entry's column (+ pad)
 };
+
+// Stripe pairs for the persistent SpMM (32x32 blocks with strictly increasing
+// columns in every block row): pairs of block rows, chosen greedily by the
+// number of block columns they share (most first, ties by lower indices),
+// leftovers paired in index order and an odd one alone (second = -1).
+// Returns false (and no pairs) if the structure does not qualify or the
+// problem is larger than max_rows block rows.  shared = block columns the
+// pairs share in all (the B slices the pairs save per tile).
+bool spmm_stripe_pairs(const bsp_bsr_desc* a, int64_t max_rows, std::vector<std::pair<int32_t, int32_t>>& pairs,
+                       int64_t* shared);
 
 // Persistent schedule for 32-row stripes (any R, C multiples of 32) and
 // tiles of tile_n (128 or 256) columns, N a multiple of tile_n, wg_per_cu
@@ -139,8 +160,12 @@ struct SpmmStream {
 // unit's units (longest first) are concatenated and cut in half, the unit
 // that straddles the cut going to both pipelines (flag 2 on the first's part,
 // flag 1 on the second's).  wgs then holds two records per workgroup.
+// pairs = true (pipes 1, 32x32 blocks): units are the stripe pairs of
+// spmm_stripe_pairs; a pair's entries are the union of its two stripes'
+// block columns, in column order (each stripe's own entries keep their CSR
+// order), and its cost is the union's size.
 int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n, int wg_per_cu,
-                      SpmmStream& s, std::string& msg, int col_groups = 0, int pipes = 1);
+                      SpmmStream& s, std::string& msg, int col_groups = 0, int pipes = 1, bool pairs = false);
 // Entries packed for the kernel: first row of B | (A offset / 32) << 32.
 std::vector<int64_t> spmm_packed_entries(const SpmmSchedule& s);
 // The split stripes in slot order (a split group contributes each of its

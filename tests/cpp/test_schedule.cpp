@@ -411,14 +411,14 @@ void check_spmm_stream(const Bsr& a, int64_t N, int cus, int tile_n, int wpc, co
             const int64_t i = un.row / RS, sub = un.row % RS;
             const int64_t full = (a.indptr[i + 1] - a.indptr[i]) * CS;
             int64_t e0 = 0, e1 = full;
-            if (un.pad == 0) {
+            if (un.aux == 0) {
                 expect(un.count == full, name + ": unit count");
                 ++seen[un.row * n_tiles + tile];
             } else {
                 expect(pipes == 2, name + ": flags only with two pipelines");
-                expect(un.pad == 2 ? (pipe == 0 && j == wg.n_units - 1) : (pipe == 1 && j == 0),
+                expect(un.aux == 2 ? (pipe == 0 && j == wg.n_units - 1) : (pipe == 1 && j == 0),
                        name + ": cut unit is the first pipeline's last and the second's first");
-                if (un.pad == 2) {
+                if (un.aux == 2) {
                     e1 = un.count;
                 } else {
                     e0 = full - un.count;
@@ -471,6 +471,81 @@ void check_spmm_stream(const Bsr& a, int64_t N, int cus, int tile_n, int wpc, co
 
 }  // namespace
 
+// Persistent SpMM with stripe pairs: the pairs cover every block row once
+// (one odd row alone at most); every (pair, tile) unit appears once, on its
+// column group's XCD; along a unit's entries the columns increase strictly,
+// each entry holds a block of at least one of the two rows, a column that both
+// rows hold is one entry with both, and each row's blocks appear once, in
+// CSR order, with the right B row and A offset.  The heads repeat the records
+// and the first words of the B and pair streams.
+void check_spmm_stream_pairs(const Bsr& a, int64_t N, int cus, const std::string& name) {
+    SpmmStream s;
+    std::string msg;
+    const bsp_bsr_desc d = a.desc();
+    const int st = build_spmm_stream(&d, N, cus, 128, 1, s, msg, 0, 1, true);
+    expect(st == BSP_OK, name + ": build (" + msg + ")");
+    if (st != BSP_OK) return;
+    expect(s.pairs == 1 && s.aw.empty(), name + ": pair streams");
+    const int64_t nsr = a.H / kSub, n_tiles = N / 128, tpg = n_tiles / s.col_groups;
+    std::vector<int> seen(nsr * n_tiles, 0);
+    int64_t w = 0, u = 0;
+    for (size_t g = 0; g < s.wgs.size(); ++g) {
+        const SpmmStreamWg& wg = s.wgs[g];
+        expect(wg.w_begin == w && wg.u_begin == u, name + ": contiguous streams");
+        int64_t e = wg.w_begin;
+        for (int32_t j = 0; j < wg.n_units; ++j) {
+            const SpmmStreamUnit& un = s.units[wg.u_begin + j];
+            const int64_t tile = un.n0 / 128;
+            expect(un.row >= 0 && un.row < nsr && un.aux < nsr && un.aux != un.row && tile < n_tiles,
+                   name + ": unit fields");
+            expect(tile / tpg == (int64_t)((g % kNumXcd) % s.col_groups), name + ": unit on its column group's XCD");
+            ++seen[un.row * n_tiles + tile];
+            if (un.aux >= 0) ++seen[un.aux * n_tiles + tile];
+            int64_t k[2] = {a.indptr[un.row], un.aux >= 0 ? a.indptr[un.aux] : 0};
+            const int64_t end[2] = {a.indptr[un.row + 1], un.aux >= 0 ? a.indptr[un.aux + 1] : 0};
+            int32_t last_col = -1;
+            bool ok = true;
+            for (int32_t c = 0; c < un.count; ++c, ++e) {
+                const int32_t col = (int32_t)(s.bw[e] & 0xffffffffLL) / kSub;
+                ok = ok && (s.bw[e] >> 32) == un.n0 && col > last_col && (s.bw[e] & 0xffffffffLL) % kSub == 0;
+                last_col = col;
+                bool any = false;
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t wh = (uint32_t)(s.apw[e] >> (32 * h));
+                    const bool next_here = k[h] < end[h] && a.indices[k[h]] == col;
+                    if (wh == kNoBlock) {
+                        ok = ok && !next_here;  // a shared column is one entry with both blocks
+                    } else {
+                        ok = ok && next_here && (int64_t)wh * kSub == k[h] * a.R * a.C;
+                        ++k[h];
+                        any = true;
+                    }
+                }
+                ok = ok && any;
+            }
+            expect(ok && k[0] == end[0] && k[1] == end[1], name + ": pair entries (union, CSR order, words)");
+        }
+        expect(e == wg.w_begin + wg.n, name + ": stream length");
+        const SpmmStreamHead& h = s.heads[g];
+        expect(std::memcmp(&h.wg, &wg, sizeof wg) == 0, name + ": head record");
+        for (int j = 0; j < kHeadWords; ++j)
+            expect(h.bw[j] == s.bw[wg.w_begin + j] && h.apw[j] == s.apw[wg.w_begin + j], name + ": head words");
+        w += wg.n;
+        u += wg.n_units;
+    }
+    expect(std::all_of(seen.begin(), seen.end(), [](int v) { return v == 1; }), name + ": every stripe's tile once");
+    expect((int64_t)s.bw.size() == w + kStreamPad && (int64_t)s.apw.size() == w + kStreamPad, name + ": padding");
+    int64_t shared = 0;
+    std::vector<std::pair<int32_t, int32_t>> pl;
+    expect(spmm_stripe_pairs(&d, INT32_MAX, pl, &shared), name + ": pairs");
+    int64_t singles = 0;
+    for (const auto& pr : pl) singles += pr.second < 0;
+    expect(singles == nsr % 2 && (int64_t)pl.size() == (nsr + 1) / 2, name + ": pairs cover the rows");
+    expect(w == (a.indptr[nsr] - shared) * n_tiles, name + ": entries = blocks - shared columns, per tile");
+    std::printf("%-34s pairs %5zu shared %6lld entries %8lld grid %zu\n", name.c_str(), pl.size(), (long long)shared,
+                (long long)w, s.wgs.size());
+}
+
 int main() {
     const int cus = 256;
     check_pairing();
@@ -502,6 +577,13 @@ int main() {
     check_spmm_stream(uniform(4096, 4096, 32, 32, 164, 3), 512, cus, 128, 1, "stream 1% two pipelines", 2);
     check_spmm_stream(uniform(1024, 1024, 32, 32, 0, 9), 256, cus, 128, 1, "stream empty two pipelines", 2);
     check_spmm_stream(uniform(1024, 1024, 32, 32, 30, 9), 128, 8, 128, 1, "stream 8 CUs two pipelines", 2);
+    check_spmm_stream_pairs(uniform(4096, 4096, 32, 32, 4096, 1), 512, cus, "pairs 4096^2 25%");
+    check_spmm_stream_pairs(uniform(4096, 4096, 32, 32, 8192, 2), 512, cus, "pairs 4096^2 50%");
+    check_spmm_stream_pairs(uniform(4064, 4096, 32, 32, 2000, 4), 256, cus, "pairs odd stripe count");
+    check_spmm_stream_pairs(uniform(4096, 4096, 32, 32, 164, 3), 512, cus, "pairs 1%, empty stripes");
+    check_spmm_stream_pairs(uniform(1024, 1024, 32, 32, 0, 9), 256, cus, "pairs empty");
+    check_spmm_stream_pairs(uniform(32768, 4096, 32, 32, 2000, 6), 1024, cus, "pairs many units per workgroup");
+    check_spmm_stream_pairs(uniform(1024, 1024, 32, 32, 30, 9), 128, 8, "pairs 8 CUs");
     check_sddmm(uniform(4096, 4096, 32, 32, 1638, 10), 256, cus, "sddmm 4096^2 10% K=256");
     check_sddmm(skewed(2048, 2048, 64, 32, 300, 11), 128, cus, "sddmm 64x32 blocks, skewed");
     check_sddmm(uniform(1024, 1024, 128, 128, 20, 12), 64, cus, "sddmm 128x128 blocks");

@@ -12,22 +12,30 @@ from helpers import W, assert_parity, bsr_of, capi, golden_spmm, run_spmm, spmm_
 pytestmark = pytest.mark.gpu
 
 # (tile, B ring, A ring, B loader waves, pipelines per workgroup, entries per
-# ring step) of BSP_SPMM_STREAM_VARIANTS in csrc/bsp_kernels.hpp
-STREAM_VARIANTS = [(128, 8, 8, 2, 1, 2), (128, 14, 16, 4, 1, 2), (128, 6, 12, 2, 1, 2),
-                   (128, 6, 12, 2, 1, 1), (128, 6, 12, 4, 1, 1), (128, 4, 16, 4, 1, 1), (128, 8, 16, 8, 1, 1),
-                   (256, 4, 16, 4, 1, 1), (256, 5, 16, 8, 1, 1), (256, 6, 8, 8, 1, 1), (128, 6, 12, 2, 2, 1),
-                   (128, 5, 12, 2, 2, 1)]
-DEFAULT = (128, 8, 8, 2, 1, 2)   # uniform rows
-SKEWED = (128, 14, 16, 4, 1, 2)  # skewed rows: one workgroup per compute unit
+# ring step, stripes per unit) of BSP_SPMM_STREAM_VARIANTS in csrc/bsp_kernels.hpp
+STREAM_VARIANTS = [(128, 8, 8, 2, 1, 2, 1), (128, 14, 16, 4, 1, 2, 1), (128, 8, 8, 2, 1, 2, 2),
+                   (128, 6, 12, 2, 1, 2, 1), (128, 6, 12, 2, 1, 1, 1), (128, 6, 12, 4, 1, 1, 1),
+                   (128, 4, 16, 4, 1, 1, 1), (128, 8, 16, 8, 1, 1, 1), (256, 4, 16, 4, 1, 1, 1),
+                   (256, 5, 16, 8, 1, 1, 1), (256, 6, 8, 8, 1, 1, 1), (128, 6, 12, 2, 2, 1, 1),
+                   (128, 5, 12, 2, 2, 1, 1)]
+DEFAULT = (128, 8, 8, 2, 1, 2, 1)   # uniform rows
+SKEWED = (128, 14, 16, 4, 1, 2, 1)  # skewed rows: one workgroup per compute unit
+PAIRS = (128, 8, 8, 2, 1, 2, 2)     # stripe pairs that share most block columns
 
 
 def _lds(v):
-    return v[4] * (64 * v[0] * v[1] + 2048 * v[2]) + (16384 * v[0] // 128 if v[4] > 1 else 0)
+    pairs_words = 8 * v[2] if v[6] > 1 else 0
+    return v[4] * (64 * v[0] * v[1] + 2048 * v[2] * v[6] + pairs_words) + (16384 * v[0] // 128 if v[4] > 1 else 0)
+
+
+def _waves(v):
+    return (4 * v[6] + 1 + v[3]) * v[4]
 
 
 def _stream_env(monkeypatch, v, wpc=None):
     monkeypatch.setenv("BSP_SPMM_STREAM", "1")
     monkeypatch.setenv("BSP_SPMM_STREAM_VARIANT", ",".join(map(str, v)))
+    monkeypatch.setenv("BSP_SPMM_PAIRS", "2" if v[6] > 1 else "0")
     if wpc:
         monkeypatch.setenv("BSP_SPMM_STREAM_WPC", str(wpc))
 
@@ -38,14 +46,15 @@ def _check(a, b, out_dtype, what, v=None, wpc=None):
     assert info["persistent"] >= 1, f"{what}: plan is not persistent ({info})"
     if v is not None:
         assert (info["tile_n"], info["stages"], info["a_stages"], info["waves"], info["persistent"],
-                info["step_entries"]) == (v[0], v[1], v[2], (5 + v[3]) * v[4], v[4], v[5])
+                info["step_entries"], info["stripes_per_unit"]) == (v[0], v[1], v[2], _waves(v), v[4], v[5], v[6])
     if wpc is not None:
         assert info["grid"] == 256 * wpc
     got = run_spmm(a, b, out_dtype, plan=plan)
     got2 = run_spmm(a, b, out_dtype, plan=plan)
     plan.close()
     np.testing.assert_array_equal(got, got2, err_msg=f"{what}: two runs differ")
-    return assert_parity(got, golden_spmm(a, b), spmm_k_eff(a), what)
+    assert_parity(got, golden_spmm(a, b), spmm_k_eff(a), what)
+    return got
 
 
 @pytest.mark.parametrize("density", [0.1, 0.5])
@@ -62,7 +71,7 @@ def test_stream_variants(monkeypatch, v, density):
             _check(w["a"], w["b"], od, f"variant={v} wpc={wpc} d={density} {od}", v, wpc)
 
 
-@pytest.mark.parametrize("v", [DEFAULT, SKEWED, (128, 6, 12, 2, 1, 1), (256, 4, 16, 4, 1, 1), (128, 6, 12, 2, 2, 1)])
+@pytest.mark.parametrize("v", [DEFAULT, SKEWED, PAIRS, (128, 6, 12, 2, 1, 1, 1), (256, 4, 16, 4, 1, 1, 1), (128, 6, 12, 2, 2, 1, 1)])
 def test_stream_many_units_per_workgroup(monkeypatch, v):
     """32768 rows x 1024 columns at 0.2%: 8192 or 4096 units on 256-512
     workgroups (16 per workgroup), many of them empty stripes, stored as zeros."""
@@ -73,7 +82,7 @@ def test_stream_many_units_per_workgroup(monkeypatch, v):
     _check(a, w["b"], "f32", f"many units {v}")
 
 
-@pytest.mark.parametrize("v", [DEFAULT, SKEWED, (128, 6, 12, 2, 1, 1), (256, 5, 16, 8, 1, 1), (128, 6, 12, 2, 2, 1)])
+@pytest.mark.parametrize("v", [DEFAULT, SKEWED, PAIRS, (128, 6, 12, 2, 1, 1, 1), (256, 5, 16, 8, 1, 1, 1), (128, 6, 12, 2, 2, 1, 1)])
 def test_stream_long_rows(monkeypatch, v):
     """A few rows of 200-400 entries (streams far longer than the ring and the
     word prefetch) among short ones."""
@@ -91,7 +100,7 @@ def test_stream_long_rows(monkeypatch, v):
     _check(a, b, "bf16", f"long rows {v} bf16")
 
 
-@pytest.mark.parametrize("v", [DEFAULT, (128, 6, 12, 2, 1, 1)])
+@pytest.mark.parametrize("v", [DEFAULT, PAIRS, (128, 6, 12, 2, 1, 1, 1)])
 def test_stream_fewer_units_than_workgroups(monkeypatch, v):
     """A 64x128 problem: 2 units for 512 workgroups; the rest stream nothing."""
     _stream_env(monkeypatch, v, 2)
@@ -99,7 +108,7 @@ def test_stream_fewer_units_than_workgroups(monkeypatch, v):
     _check(w["a"], w["b"], "f32", "2 units")
 
 
-@pytest.mark.parametrize("v", [DEFAULT, SKEWED, (128, 6, 12, 2, 1, 2), (128, 6, 12, 2, 1, 1)])
+@pytest.mark.parametrize("v", [DEFAULT, SKEWED, PAIRS, (128, 6, 12, 2, 1, 2, 1), (128, 6, 12, 2, 1, 1, 1)])
 def test_stream_step_tails(monkeypatch, v):
     """One unit per workgroup with every stream length from 0 to 40 entries:
     with two entries per step, odd and even lengths end differently, and
@@ -117,12 +126,13 @@ def test_stream_step_tails(monkeypatch, v):
     plan = capi.SpmmPlan(bsr_of(a), 128, "f32")
     info = plan.info()
     plan.close()
-    assert info["n_items"] == len(counts) and info["grid"] >= len(counts)  # one unit per workgroup
+    units = (len(counts) + 1) // 2 if v[6] > 1 else len(counts)
+    assert info["n_items"] == units and info["grid"] >= units  # one unit per workgroup
     _check(a, b, "f32", f"tails {v}")
     _check(a, b, "bf16", f"tails {v} bf16")
 
 
-@pytest.mark.parametrize("v", [DEFAULT, (128, 6, 12, 2, 2, 1)])
+@pytest.mark.parametrize("v", [DEFAULT, PAIRS, (128, 6, 12, 2, 2, 1, 1)])
 def test_stream_empty_matrix(monkeypatch, v):
     """No stored blocks: every unit is an empty stripe, every tile stored as zeros."""
     pipes = v[4]
@@ -137,7 +147,7 @@ def test_stream_empty_matrix(monkeypatch, v):
     assert np.all(got == 0.0)
 
 
-@pytest.mark.parametrize("v", [DEFAULT, (128, 6, 12, 2, 2, 1)])
+@pytest.mark.parametrize("v", [DEFAULT, (128, 6, 12, 2, 2, 1, 1)])
 @pytest.mark.parametrize("R,C", [(64, 64), (32, 96), (96, 32)])
 def test_stream_other_block_shapes(monkeypatch, R, C, v):
     """Blocks other than 32x32 cut into 32-row stripes (no row groups)."""
@@ -158,4 +168,68 @@ def test_default_plan_variant(density):
     plan.close()
     v = DEFAULT
     assert (info["persistent"], info["tile_n"], info["stages"], info["a_stages"], info["waves"],
-            info["step_entries"], info["grid"]) == (1, v[0], v[1], v[2], 5 + v[3], v[5], 512), info
+            info["step_entries"], info["stripes_per_unit"], info["grid"]) == \
+        (1, v[0], v[1], v[2], _waves(v), v[5], v[6], 512), info
+
+
+def _pair_structures():
+    """Block-row structures for the stripe-pair tests (128 stripes of 32x32
+    blocks over 128 block columns unless noted)."""
+    rng = np.random.default_rng(98)
+    nbc = 128
+
+    def mk(rows, nbc=nbc):
+        indices = np.concatenate([np.asarray(r, np.int32) for r in rows]) if rows else np.zeros(0, np.int32)
+        indptr = np.concatenate([[0], np.cumsum([len(r) for r in rows])]).astype(np.int32)
+        a = W.BsrArrays(len(rows) * 32, nbc * 32, 32, 32, indptr, indices)
+        a.data = W.block_content(a.nblocks, 32, 32, "RAND", rng)
+        return a
+
+    base = [np.sort(rng.choice(nbc, int(rng.integers(20, 60)), replace=False)) for _ in range(64)]
+    near = []
+    for r in base:  # each pair: the same columns, one of them moved
+        r2 = r.copy()
+        free = np.setdiff1d(np.arange(nbc), r)
+        r2[0] = free[0]
+        near += [r, np.sort(r2)]
+    return {
+        "identical pairs": mk([r for r in base for _ in range(2)]),
+        "near-identical pairs": mk(near),
+        "uniform 25%": W.workload_spmm_sweep(0.25)["a"],
+        "every second stripe empty": mk([x for r in base for x in (r, [])]),
+        "odd stripe count": mk([r for r in base for _ in range(2)][:-1]),
+    }
+
+
+@pytest.mark.parametrize("name", ["identical pairs", "near-identical pairs", "uniform 25%",
+                                  "every second stripe empty", "odd stripe count"])
+def test_stripe_pairs_bitwise_equal_to_one_stripe(monkeypatch, name):
+    """Stripe pairs keep each stripe's own summation order (its blocks in CSR
+    order), so their output is the single-stripe kernel's bit for bit, and
+    both are held to the oracle."""
+    a = _pair_structures()[name]
+    b = W.dense_content(a.W, 512, "RAND", np.random.default_rng(99))
+    outs = {}
+    for mode in ("0", "2"):
+        monkeypatch.setenv("BSP_SPMM_PAIRS", mode)
+        plan = capi.SpmmPlan(bsr_of(a), 512, "f32")
+        info = plan.info()
+        assert info["persistent"] == 1 and info["stripes_per_unit"] == (2 if mode == "2" else 1), info
+        plan.close()
+        outs[mode] = _check(a, b, "f32", f"{name} pairs={mode}")
+    np.testing.assert_array_equal(outs["0"], outs["2"], err_msg=f"{name}: pairs differ from one stripe")
+
+
+def test_stripe_pairs_chosen_only_where_columns_are_shared():
+    """The plan takes stripe pairs for block rows that share most of their
+    columns, and keeps one stripe per unit on uniform-random rows."""
+    s = _pair_structures()
+    for name, want in (("identical pairs", 2), ("near-identical pairs", 2), ("uniform 25%", 1)):
+        a = s[name]
+        plan = capi.SpmmPlan(bsr_of(a), 512, "f32")
+        info = plan.info()
+        plan.close()
+        assert info["stripes_per_unit"] == want, (name, info)
+        if want == 2:
+            assert (info["stages"], info["a_stages"], info["waves"], info["grid"]) == \
+                (PAIRS[1], PAIRS[2], _waves(PAIRS), 256), info
