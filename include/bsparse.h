@@ -272,8 +272,10 @@ int bsp_host_spgemm(const bsp_bsr_desc* a, const uint16_t* a_vals, const bsp_bsr
  * No counterpart in the reference: an entry point for callers that cannot
  * allocate device memory (serving loops that must not touch the allocator,
  * harnesses that forbid hipMalloc).  C = A * B as bsp_spmm computes it (the
- * same persistent kernel and schedule a plan would use), without a plan: the
- * schedule is built on the host and staged in a static device array of
+ * same persistent kernel and schedule a plan would use, except that a plan's
+ * stripe pairs run as single stripes here, which gives the same bits),
+ * without a plan: the schedule is built on the host and staged in a static
+ * device array of
  * BSP_NOALLOC_SCRATCH_BYTES that the library holds on every GPU it runs on
  * until the process ends.  It calls no hipMalloc or hipFree.  The call waits
  * for the schedule's copy on `stream` (and the stream's earlier work), then
