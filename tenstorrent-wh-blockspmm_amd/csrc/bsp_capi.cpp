@@ -273,14 +273,16 @@ bool choose_spmm_stream(const bsp_bsr_desc* a, int64_t N, int cus, SpmmStreamVar
     // -22.8 against 23.7-23.9).  Taken at 40% shared and more.
     // BSP_SPMM_PAIRS=0 turns them off, 2 takes them whenever the structure
     // allows.
+    // (The pairing's overlap table is quadratic in the block rows: at most
+    // 1024 of them, and only when the pairs could fill the compute units.)
     const int64_t pairs_mode = env_int("BSP_SPMM_PAIRS", 1);
     bool pairs_ok = false;
-    if (pairs_mode > 0 && N % 128 == 0) {
+    const int64_t pair_units = (a->H / bsp::kSub + 1) / 2 * (N / 128);
+    if (pairs_mode > 0 && N % 128 == 0 && (pairs_mode == 2 || pair_units >= (int64_t)cus)) {
         std::vector<std::pair<int32_t, int32_t>> pl;
         int64_t shared = 0;
-        if (bsp::spmm_stripe_pairs(a, 2048, pl, &shared))
-            pairs_ok = pairs_mode == 2 ||
-                       (10 * shared >= 4 * a->nblocks && (int64_t)pl.size() * (N / 128) >= (int64_t)cus);
+        if (bsp::spmm_stripe_pairs(a, bsp::kPairMaxRows, pl, &shared))
+            pairs_ok = pairs_mode == 2 || 10 * shared >= 4 * a->nblocks;
     }
     const char* forced = std::getenv("BSP_SPMM_STREAM_VARIANT");
     if (forced) {

@@ -477,8 +477,9 @@ int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n,
     if (pipes == 2) wg_per_cu = 1;
     std::vector<std::pair<int32_t, int32_t>> pair_list;
     if (pairs) {
-        if (pipes != 1 || !spmm_stripe_pairs(a, INT32_MAX, pair_list, nullptr)) {
-            msg = "stripe pairs need one pipeline, 32x32 blocks and strictly increasing block columns";
+        if (pipes != 1 || !spmm_stripe_pairs(a, kPairMaxRows, pair_list, nullptr)) {
+            msg = "stripe pairs need one pipeline, 32x32 blocks, strictly increasing block columns and at most "
+                  "1024 block rows";
             return BSP_ERR_UNSUPPORTED;
         }
     }

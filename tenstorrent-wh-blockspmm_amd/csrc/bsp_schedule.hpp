@@ -149,6 +149,8 @@ struct SpmmStream {
 // pairs share in all (the B slices the pairs save per tile).
 bool spmm_stripe_pairs(const bsp_bsr_desc* a, int64_t max_rows, std::vector<std::pair<int32_t, int32_t>>& pairs,
                        int64_t* shared);
+// The most block rows a pairing considers (its overlap table is quadratic).
+constexpr int64_t kPairMaxRows = 1024;
 
 // Persistent schedule for 32-row stripes (any R, C multiples of 32) and
 // tiles of tile_n (128 or 256) columns, N a multiple of tile_n, wg_per_cu

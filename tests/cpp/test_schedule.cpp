@@ -537,7 +537,7 @@ void check_spmm_stream_pairs(const Bsr& a, int64_t N, int cus, const std::string
     expect((int64_t)s.bw.size() == w + kStreamPad && (int64_t)s.apw.size() == w + kStreamPad, name + ": padding");
     int64_t shared = 0;
     std::vector<std::pair<int32_t, int32_t>> pl;
-    expect(spmm_stripe_pairs(&d, INT32_MAX, pl, &shared), name + ": pairs");
+    expect(spmm_stripe_pairs(&d, kPairMaxRows, pl, &shared), name + ": pairs");
     int64_t singles = 0;
     for (const auto& pr : pl) singles += pr.second < 0;
     expect(singles == nsr % 2 && (int64_t)pl.size() == (nsr + 1) / 2, name + ": pairs cover the rows");
