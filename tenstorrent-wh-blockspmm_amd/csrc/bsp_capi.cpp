@@ -265,12 +265,14 @@ bool choose_spmm_stream(const bsp_bsr_desc* a, int64_t N, int cus, SpmmStreamVar
     bsp::SpmmStreamVariant v = bsp::kSpmmStreamDefault;
     // Stripe pairs (32x32 blocks): one workgroup per compute unit streams a
     // pair's union of block columns, so they pay only when the pairs share
-    // most of their columns (block rows with near-identical patterns: 4096^2
-    // x 512 with identical pairs, 14.3-14.9 against 18.3-19.4 us) and still
-    // give every compute unit a unit of its own.  On uniform-random rows the
-    // pairs share 20% (25% density) or 30% (50%) of their blocks, and the
-    // single-stripe kernel stays faster (13.1-13.4 against 16.4-16.7 us; 21.5
-    // -22.8 against 23.7-23.9).  Taken at 40% shared and more.
+    // much of their blocks (4096^2 x 512: identical pairs 14.3-14.9 against
+    // 18.3-19.4 us; banded rows of 4 / 16 / 32 / 64 blocks, pairs sharing
+    // 37-49%, 5.5 / 8.7-9.1 / 12.0-12.2 / 19.9-20.4 against 5.8-6.1 / 9.6 /
+    // 14.4-14.6 / 23.1-25.0) and still give every compute unit a unit of its
+    // own.  On uniform-random rows the pairs share 20% (25% density) or 30%
+    // (50%) of their blocks, and the single-stripe kernel stays faster
+    // (13.1-13.4 against 16.4-16.7 us; 21.5-22.8 against 23.7-23.9).  Taken
+    // at 35% shared and more.
     // BSP_SPMM_PAIRS=0 turns them off, 2 takes them whenever the structure
     // allows.
     // (The pairing's overlap table is quadratic in the block rows: at most
@@ -282,7 +284,7 @@ bool choose_spmm_stream(const bsp_bsr_desc* a, int64_t N, int cus, SpmmStreamVar
         std::vector<std::pair<int32_t, int32_t>> pl;
         int64_t shared = 0;
         if (bsp::spmm_stripe_pairs(a, bsp::kPairMaxRows, pl, &shared))
-            pairs_ok = pairs_mode == 2 || 10 * shared >= 4 * a->nblocks;
+            pairs_ok = pairs_mode == 2 || 20 * shared >= 7 * a->nblocks;
     }
     const char* forced = std::getenv("BSP_SPMM_STREAM_VARIANT");
     if (forced) {

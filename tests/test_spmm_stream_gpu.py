@@ -174,7 +174,8 @@ def test_default_plan_variant(density):
 
 def _pair_structures():
     """Block-row structures for the stripe-pair tests (128 stripes of 32x32
-    blocks over 128 block columns unless noted)."""
+    blocks over 128 block columns unless noted; the 4096^2 25% sweep
+    workload)."""
     rng = np.random.default_rng(98)
     nbc = 128
 
@@ -192,7 +193,9 @@ def _pair_structures():
         free = np.setdiff1d(np.arange(nbc), r)
         r2[0] = free[0]
         near += [r, np.sort(r2)]
+    band = [np.arange(min(max(i - 8, 0), nbc - 16), min(max(i - 8, 0), nbc - 16) + 16) for i in range(128)]
     return {
+        "banded, 16 blocks a row": mk(band),
         "identical pairs": mk([r for r in base for _ in range(2)]),
         "near-identical pairs": mk(near),
         "uniform 25%": W.workload_spmm_sweep(0.25)["a"],
@@ -201,8 +204,8 @@ def _pair_structures():
     }
 
 
-@pytest.mark.parametrize("name", ["identical pairs", "near-identical pairs", "uniform 25%",
-                                  "every second stripe empty", "odd stripe count"])
+@pytest.mark.parametrize("name", ["banded, 16 blocks a row", "identical pairs", "near-identical pairs",
+                                  "uniform 25%", "every second stripe empty", "odd stripe count"])
 def test_stripe_pairs_bitwise_equal_to_one_stripe(monkeypatch, name):
     """Stripe pairs keep each stripe's own summation order (its blocks in CSR
     order), so their output is the single-stripe kernel's bit for bit, and
@@ -221,10 +224,12 @@ def test_stripe_pairs_bitwise_equal_to_one_stripe(monkeypatch, name):
 
 
 def test_stripe_pairs_chosen_only_where_columns_are_shared():
-    """The plan takes stripe pairs for block rows that share most of their
-    columns, and keeps one stripe per unit on uniform-random rows."""
+    """The plan takes stripe pairs for block rows that share much of their
+    columns (banded rows, near-identical pairs), and keeps one stripe per
+    unit on uniform-random rows."""
     s = _pair_structures()
-    for name, want in (("identical pairs", 2), ("near-identical pairs", 2), ("uniform 25%", 1)):
+    for name, want in (("banded, 16 blocks a row", 2), ("identical pairs", 2), ("near-identical pairs", 2),
+                       ("uniform 25%", 1)):
         a = s[name]
         plan = capi.SpmmPlan(bsr_of(a), 512, "f32")
         info = plan.info()
