@@ -212,15 +212,16 @@ def test_stripe_pairs_bitwise_equal_to_one_stripe(monkeypatch, name):
     both are held to the oracle."""
     a = _pair_structures()[name]
     b = W.dense_content(a.W, 512, "RAND", np.random.default_rng(99))
-    outs = {}
-    for mode in ("0", "2"):
-        monkeypatch.setenv("BSP_SPMM_PAIRS", mode)
-        plan = capi.SpmmPlan(bsr_of(a), 512, "f32")
-        info = plan.info()
-        assert info["persistent"] == 1 and info["stripes_per_unit"] == (2 if mode == "2" else 1), info
-        plan.close()
-        outs[mode] = _check(a, b, "f32", f"{name} pairs={mode}")
-    np.testing.assert_array_equal(outs["0"], outs["2"], err_msg=f"{name}: pairs differ from one stripe")
+    for od in ("f32", "bf16"):
+        outs = {}
+        for mode in ("0", "2"):
+            monkeypatch.setenv("BSP_SPMM_PAIRS", mode)
+            plan = capi.SpmmPlan(bsr_of(a), 512, od)
+            info = plan.info()
+            assert info["persistent"] == 1 and info["stripes_per_unit"] == (2 if mode == "2" else 1), info
+            plan.close()
+            outs[mode] = _check(a, b, od, f"{name} pairs={mode} {od}")
+        np.testing.assert_array_equal(outs["0"], outs["2"], err_msg=f"{name} {od}: pairs differ from one stripe")
 
 
 def test_stripe_pairs_chosen_only_where_columns_are_shared():
