@@ -264,15 +264,18 @@ bool choose_spmm_stream(const bsp_bsr_desc* a, int64_t N, int cus, SpmmStreamVar
     if (group > 1 && (a->R / bsp::kSub) % group == 0) return false;
     bsp::SpmmStreamVariant v = bsp::kSpmmStreamDefault;
     // Stripe pairs (32x32 blocks): one workgroup per compute unit streams a
-    // pair's union of block columns, so they pay only when the pairs share
-    // much of their blocks (4096^2 x 512: identical pairs 14.3-14.9 against
-    // 18.3-19.4 us; banded rows of 4 / 16 / 32 / 64 blocks, pairs sharing
-    // 37-49%, 5.5 / 8.7-9.1 / 12.0-12.2 / 19.9-20.4 against 5.8-6.1 / 9.6 /
-    // 14.4-14.6 / 23.1-25.0) and still give every compute unit a unit of its
-    // own.  On uniform-random rows the pairs share 20% (25% density) or 30%
-    // (50%) of their blocks, and the single-stripe kernel stays faster
-    // (13.1-13.4 against 16.4-16.7 us; 21.5-22.8 against 23.7-23.9).  Taken
-    // at 35% shared and more.
+    // pair's union of block columns, an 8 KB B slice per entry with one or two
+    // 2 KB A blocks, where single stripes stream 10 KB per block.  Estimated
+    // per compute unit: single = 10 KB x max(blocks x tiles / CUs, longest
+    // row); pairs = 1.2 x (8 + 2 x blocks / union entries) KB x max(union
+    // entries x tiles / CUs, largest union), the 1.2 being what one workgroup
+    // per compute unit costs.  Pairs are taken when they come out cheaper.
+    // The estimate orders every measured structure (4096^2 x 512, pairs :
+    // single us): identical rows of 51 blocks 14.3-14.9 : 18.3-19.4; banded
+    // rows of 4 / 16 / 32 / 64 blocks 5.5 / 8.7-9.1 / 12.0-12.2 / 19.9-20.4 :
+    // 5.8-6.1 / 9.6 / 14.4-14.6 / 23.1-25.0; identical pairs of rows of 20-60
+    // blocks 15.7-15.8 : 15.5-15.7 (the largest union sets the end);
+    // uniform-random 25% / 50% 16.4-16.7 / 23.7-23.9 : 13.1-13.4 / 21.5-22.8.
     // BSP_SPMM_PAIRS=0 turns them off, 2 takes them whenever the structure
     // allows.
     // (The pairing's overlap table is quadratic in the block rows: at most
@@ -282,9 +285,18 @@ bool choose_spmm_stream(const bsp_bsr_desc* a, int64_t N, int cus, SpmmStreamVar
     const int64_t pair_units = (a->H / bsp::kSub + 1) / 2 * (N / 128);
     if (pairs_mode > 0 && N % 128 == 0 && (pairs_mode == 2 || pair_units >= (int64_t)cus)) {
         std::vector<std::pair<int32_t, int32_t>> pl;
-        int64_t shared = 0;
-        if (bsp::spmm_stripe_pairs(a, bsp::kPairMaxRows, pl, &shared))
-            pairs_ok = pairs_mode == 2 || 20 * shared >= 7 * a->nblocks;
+        int64_t shared = 0, max_union = 0;
+        if (bsp::spmm_stripe_pairs(a, bsp::kPairMaxRows, pl, &shared, &max_union)) {
+            const double tiles = (double)(N / 128), nb = (double)a->nblocks;
+            const double uni = nb - (double)shared;  // union entries over all pairs
+            int64_t longest = 0;
+            for (int64_t i = 0; i < a->H / bsp::kSub; ++i)
+                longest = std::max<int64_t>(longest, a->indptr[i + 1] - a->indptr[i]);
+            const double single = 10.0 * std::max(nb * tiles / cus, (double)longest);
+            const double paired =
+                uni > 0 ? 1.2 * (8.0 + 2.0 * nb / uni) * std::max(uni * tiles / cus, (double)max_union) : single;
+            pairs_ok = pairs_mode == 2 || paired < single;
+        }
     }
     const char* forced = std::getenv("BSP_SPMM_STREAM_VARIANT");
     if (forced) {

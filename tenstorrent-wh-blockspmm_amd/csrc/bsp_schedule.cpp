@@ -399,9 +399,10 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
 }
 
 bool spmm_stripe_pairs(const bsp_bsr_desc* a, int64_t max_rows, std::vector<std::pair<int32_t, int32_t>>& pairs,
-                       int64_t* shared) {
+                       int64_t* shared, int64_t* max_union) {
     pairs.clear();
     if (shared) *shared = 0;
+    if (max_union) *max_union = 0;
     if (!a || a->R != kSub || a->C != kSub || a->H % kSub || a->W % kSub) return false;
     const int64_t nbr = a->H / kSub, nbc = a->W / kSub;
     if (nbr < 2 || nbr > max_rows) return false;
@@ -448,7 +449,16 @@ bool spmm_stripe_pairs(const bsp_bsr_desc* a, int64_t max_rows, std::vector<std:
     }
     if (left >= 0) pairs.push_back({left, -1});
     std::sort(pairs.begin(), pairs.end());
+    int64_t mu = 0;
+    for (const auto& [i, j] : pairs) {
+        const int64_t ni = a->indptr[i + 1] - a->indptr[i];
+        const int64_t nj = j >= 0 ? a->indptr[j + 1] - a->indptr[j] : 0;
+        const int64_t o = j >= 0 ? ov[(size_t)std::min(i, j) * nbr + std::max(i, j)] : 0;
+        mu = std::max(mu, ni + nj - o);
+    }
+    // Leftover pairs share no columns (any two unpaired rows that did were a candidate).
     if (shared) *shared = sh;
+    if (max_union) *max_union = mu;
     return true;
 }
 

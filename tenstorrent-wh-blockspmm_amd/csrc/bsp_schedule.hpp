@@ -146,9 +146,10 @@ struct SpmmStream {
 // leftovers paired in index order and an odd one alone (second = -1).
 // Returns false (and no pairs) if the structure does not qualify or the
 // problem is larger than max_rows block rows.  shared = block columns the
-// pairs share in all (the B slices the pairs save per tile).
+// pairs share in all (the B slices the pairs save per tile); max_union = the
+// largest pair's union of block columns (its entries per tile).
 bool spmm_stripe_pairs(const bsp_bsr_desc* a, int64_t max_rows, std::vector<std::pair<int32_t, int32_t>>& pairs,
-                       int64_t* shared);
+                       int64_t* shared, int64_t* max_union = nullptr);
 // The most block rows a pairing considers (its overlap table is quadratic).
 constexpr int64_t kPairMaxRows = 1024;
 

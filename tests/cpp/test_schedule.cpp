@@ -535,11 +535,19 @@ void check_spmm_stream_pairs(const Bsr& a, int64_t N, int cus, const std::string
     }
     expect(std::all_of(seen.begin(), seen.end(), [](int v) { return v == 1; }), name + ": every stripe's tile once");
     expect((int64_t)s.bw.size() == w + kStreamPad && (int64_t)s.apw.size() == w + kStreamPad, name + ": padding");
-    int64_t shared = 0;
+    int64_t shared = 0, max_union = -1;
     std::vector<std::pair<int32_t, int32_t>> pl;
-    expect(spmm_stripe_pairs(&d, kPairMaxRows, pl, &shared), name + ": pairs");
-    int64_t singles = 0;
-    for (const auto& pr : pl) singles += pr.second < 0;
+    expect(spmm_stripe_pairs(&d, kPairMaxRows, pl, &shared, &max_union), name + ": pairs");
+    int64_t singles = 0, largest = 0;
+    for (const auto& pr : pl) {
+        singles += pr.second < 0;
+        std::vector<int32_t> cols(a.indices.begin() + a.indptr[pr.first], a.indices.begin() + a.indptr[pr.first + 1]);
+        if (pr.second >= 0)
+            cols.insert(cols.end(), a.indices.begin() + a.indptr[pr.second], a.indices.begin() + a.indptr[pr.second + 1]);
+        std::sort(cols.begin(), cols.end());
+        largest = std::max<int64_t>(largest, std::unique(cols.begin(), cols.end()) - cols.begin());
+    }
+    expect(max_union == largest, name + ": largest union of block columns");
     expect(singles == nsr % 2 && (int64_t)pl.size() == (nsr + 1) / 2, name + ": pairs cover the rows");
     expect(w == (a.indptr[nsr] - shared) * n_tiles, name + ": entries = blocks - shared columns, per tile");
     std::printf("%-34s pairs %5zu shared %6lld entries %8lld grid %zu\n", name.c_str(), pl.size(), (long long)shared,

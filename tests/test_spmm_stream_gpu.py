@@ -194,9 +194,11 @@ def _pair_structures():
         r2[0] = free[0]
         near += [r, np.sort(r2)]
     band = [np.arange(min(max(i - 8, 0), nbc - 16), min(max(i - 8, 0), nbc - 16) + 16) for i in range(128)]
+    equal = [np.sort(rng.choice(nbc, 48, replace=False)) for _ in range(64)]
     return {
         "banded, 16 blocks a row": mk(band),
         "identical pairs": mk([r for r in base for _ in range(2)]),
+        "identical pairs, 48 blocks a row": mk([r for r in equal for _ in range(2)]),
         "near-identical pairs": mk(near),
         "uniform 25%": W.workload_spmm_sweep(0.25)["a"],
         "every second stripe empty": mk([x for r in base for x in (r, [])]),
@@ -204,8 +206,9 @@ def _pair_structures():
     }
 
 
-@pytest.mark.parametrize("name", ["banded, 16 blocks a row", "identical pairs", "near-identical pairs",
-                                  "uniform 25%", "every second stripe empty", "odd stripe count"])
+@pytest.mark.parametrize("name", ["banded, 16 blocks a row", "identical pairs", "identical pairs, 48 blocks a row",
+                                  "near-identical pairs", "uniform 25%", "every second stripe empty",
+                                  "odd stripe count"])
 def test_stripe_pairs_bitwise_equal_to_one_stripe(monkeypatch, name):
     """Stripe pairs keep each stripe's own summation order (its blocks in CSR
     order), so their output is the single-stripe kernel's bit for bit, and
@@ -224,13 +227,16 @@ def test_stripe_pairs_bitwise_equal_to_one_stripe(monkeypatch, name):
         np.testing.assert_array_equal(outs["0"], outs["2"], err_msg=f"{name} {od}: pairs differ from one stripe")
 
 
-def test_stripe_pairs_chosen_only_where_columns_are_shared():
-    """The plan takes stripe pairs for block rows that share much of their
-    columns (banded rows, near-identical pairs), and keeps one stripe per
-    unit on uniform-random rows."""
+def test_stripe_pairs_chosen_only_where_they_stream_less():
+    """The plan takes stripe pairs where its estimate of the bytes each
+    compute unit streams comes out lower for them: banded rows, identical
+    pairs of equal rows.  It keeps one stripe per unit on uniform-random rows
+    and on identical pairs of rows of 20-60 blocks, where the largest pair
+    (59 entries of 12 KB, 850 KB with the one-workgroup factor) streams more
+    than a compute unit's share of single stripes (74 entries of 10 KB)."""
     s = _pair_structures()
-    for name, want in (("banded, 16 blocks a row", 2), ("identical pairs", 2), ("near-identical pairs", 2),
-                       ("uniform 25%", 1)):
+    for name, want in (("banded, 16 blocks a row", 2), ("identical pairs, 48 blocks a row", 2),
+                       ("identical pairs", 1), ("near-identical pairs", 1), ("uniform 25%", 1)):
         a = s[name]
         plan = capi.SpmmPlan(bsr_of(a), 512, "f32")
         info = plan.info()
