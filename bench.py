@@ -448,16 +448,19 @@ def probe_lib():
 
 
 def measure_roofs(torch, steps=50):
-    """TB/s of an L2-resident DMA stream (2 MB region, 256 workgroups x 8
-    waves, 16 loads of 1 KB in flight per wave) and an HBM one (1 GB), and the
-    graph-replay time of an empty 512-workgroup kernel."""
+    """TB/s of an L2-resident DMA stream (2 MB region, 512 workgroups x 8
+    waves, two per compute unit as in the SpMM kernel, 16 loads of 1 KB in
+    flight per wave) and an HBM one (1 GB), and the graph-replay time of an
+    empty 512-workgroup kernel.  Each stream launch moves 4 GB, so the fixed
+    cost of its launch stays below 2% of its time (the floor adds that cost
+    once, as the empty launch)."""
     lib = probe_lib()
     buf = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
     buf.fill_(1)
     st = torch.cuda.current_stream()
-    iters = 256
+    grid, waves, iters = 512, 8, 1024
 
-    def graph_us(fn):
+    def graph_us(fn, steps=steps):
         for _ in range(3):
             fn(st.cuda_stream)
         torch.cuda.synchronize()
@@ -478,8 +481,8 @@ def measure_roofs(torch, steps=50):
 
     out = {}
     for name, region in (("l2_stream_tbs", 2 << 20), ("hbm_stream_tbs", 1 << 30)):
-        us = graph_us(lambda s: lib.bsp_probe_dma_stream(buf.data_ptr(), region, 256, 8, iters, s))
-        out[name] = round(256 * 8 * iters * 1024 / (us * 1e-6) / 1e12, 2)
+        us = graph_us(lambda s: lib.bsp_probe_dma_stream(buf.data_ptr(), region, grid, waves, iters, s), steps=5)
+        out[name] = round(grid * waves * iters * 1024 / (us * 1e-6) / 1e12, 2)
     out["empty_launch_us"] = round(graph_us(lambda s: lib.bsp_probe_empty(512, s)), 3)
     del buf
     return out
