@@ -518,6 +518,8 @@ int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n,
     if (cg < 1 || kNumXcd % cg != 0 || n_tiles % cg != 0) cg = 1;
     s.col_groups = (int32_t)cg;
     const int64_t rg_count = kNumXcd / cg, tpg = n_tiles / cg;
+    const bool rotate = pipes == 1 && env_int("BSP_SPMM_ROTATE", 1) != 0;
+    s.rotated = rotate ? 1 : 0;
 
     // Stripe entry counts; a unit costs its entries plus the store.
     constexpr int64_t kStoreCost = 2;
@@ -640,6 +642,18 @@ int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n,
             pos = e;
         }
     };
+    // Each unit of column group c > 0 starts at its first block column at or
+    // past c/cg of A's block columns and wraps around
+    // (spmm_stream_rotation_column); returns the offset of that entry among
+    // the unit's entries at `first`.
+    auto rotation = [&](size_t first, int32_t n0) -> int64_t {
+        if (!rotate) return 0;
+        const int64_t kcol = spmm_stream_rotation_column(a->W / a->C, (n0 / tile_n) / tpg, cg);
+        const int64_t len = (int64_t)(s.bw.size() - first);
+        int64_t off = 0;
+        while (off < len && (int64_t)((uint32_t)s.bw[first + off] / a->C) < kcol) ++off;
+        return off == len ? 0 : off;
+    };
     auto emit = [&](const std::vector<Part>& parts) {
         SpmmStreamWg w{};
         w.w_begin = (int32_t)s.bw.size();
@@ -648,15 +662,20 @@ int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n,
         for (const Part& pt : parts) {
             s.units.push_back(pt.u);
             if (pairs) {
+                const size_t first = s.bw.size();
                 merge(pt.u.row, pt.u.aux, [&](int32_t col, int64_t k0, int64_t k1) {
                     const uint64_t w0 = k0 >= 0 ? (uint64_t)(k0 * a->R * a->C / kSub) : kNoBlock;
                     const uint64_t w1 = k1 >= 0 ? (uint64_t)(k1 * a->R * a->C / kSub) : kNoBlock;
                     s.bw.push_back((int64_t)col * a->C | ((int64_t)pt.u.n0 << 32));
                     s.apw.push_back(w0 | w1 << 32);
                 });
+                const int64_t off = rotation(first, pt.u.n0);
+                std::rotate(s.bw.begin() + first, s.bw.begin() + first + off, s.bw.end());
+                std::rotate(s.apw.begin() + first, s.apw.begin() + first + off, s.apw.end());
                 continue;
             }
             const int64_t i = pt.u.row / RS, sub = pt.u.row % RS;
+            const size_t first = s.bw.size();
             int64_t e = 0;
             for (int64_t blk = a->indptr[i]; blk < a->indptr[i + 1]; ++blk)
                 for (int64_t t = 0; t < CS; ++t, ++e) {
@@ -665,6 +684,9 @@ int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n,
                     s.bw.push_back(brow | ((int64_t)pt.u.n0 << 32));
                     s.aw.push_back((uint32_t)((blk * a->R * a->C + kSub * sub * a->C + kSub * t) / kSub));
                 }
+            const int64_t off = rotation(first, pt.u.n0);
+            std::rotate(s.bw.begin() + first, s.bw.begin() + first + off, s.bw.end());
+            std::rotate(s.aw.begin() + first, s.aw.begin() + first + off, s.aw.end());
         }
         w.n = (int32_t)(s.bw.size() - w.w_begin);
         s.max_wg_entries = std::max(s.max_wg_entries, w.n);

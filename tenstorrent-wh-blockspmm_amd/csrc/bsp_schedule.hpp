@@ -127,6 +127,7 @@ struct SpmmStream {
     int32_t wg_per_cu = 1;
     int32_t col_groups = 1;        // column groups of the XCD map
     int32_t pairs = 0;             // 1: units are stripe pairs (apw holds the A words)
+    int32_t rotated = 0;           // 1: units start at spmm_stream_rotation_column (one pipeline)
     int32_t max_wg_entries = 0;    // longest workgroup stream
     int64_t n_entries = 0;         // sum over units (entries x tiles)
     std::vector<SpmmStreamWg> wgs;        // one per workgroup; workgroup g runs on XCD g % kNumXcd
@@ -166,7 +167,24 @@ constexpr int64_t kPairMaxRows = 1024;
 // pairs = true (pipes 1, 32x32 blocks): units are the stripe pairs of
 // spmm_stripe_pairs; a pair's entries are the union of its two stripes'
 // block columns, in column order (each stripe's own entries keep their CSR
-// order), and its cost is the union's size.
+// order), and its cost is the union's size.  With one pipeline, every unit's
+// entries (a stripe's in CSR order, a pair's union) are then rotated to start
+// at spmm_stream_rotation_column (above).
+// Rotation of a unit's entries (one pipeline; BSP_SPMM_ROTATE=0 turns it
+// off): a unit of column group g starts at its first entry whose block column
+// is at least spmm_stream_rotation_column(block columns of A, g, col_groups)
+// and wraps around to its first entry (no rotation when there is none).  The
+// col_groups XCDs that read a stripe's A blocks for different column groups
+// then read each block about 1/col_groups of the stripe apart in time, so all
+// but the first find it in the Infinity Cache instead of HBM.  Only the
+// summation order of a unit changes (a stripe pair rotates at the same column
+// as its two stripes, so pairs stay bit-identical to single stripes).
+// (4096^2 x 512, f32 C, graph replay: 25% 13.2-13.4 -> 12.3-12.4 us, 50%
+// 21.8-22.3 -> 20.8-21.6 us, 1%, 5% and the skewed workload unchanged.)
+inline int64_t spmm_stream_rotation_column(int64_t block_cols, int64_t group, int64_t col_groups) {
+    return col_groups > 1 ? group * block_cols / col_groups : 0;
+}
+
 int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n, int wg_per_cu,
                       SpmmStream& s, std::string& msg, int col_groups = 0, int pipes = 1, bool pairs = false);
 // Entries packed for the kernel: first row of B | (A offset / 32) << 32.

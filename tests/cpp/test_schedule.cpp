@@ -426,16 +426,26 @@ void check_spmm_stream(const Bsr& a, int64_t N, int cus, int tile_n, int wpc, co
                 }
             }
             covered[un.row * n_tiles + tile] += e1 - e0;
+            std::vector<std::pair<int64_t, int64_t>> want;  // (B row, A offset) in CSR order
             int64_t idx = 0;
             for (int64_t blk = a.indptr[i]; blk < a.indptr[i + 1]; ++blk)
-                for (int64_t t = 0; t < CS; ++t, ++idx) {
-                    if (idx < e0 || idx >= e1) continue;
-                    const int64_t brow = (int64_t)a.indices[blk] * a.C + kSub * t;
-                    const int64_t aoff = blk * a.R * a.C + kSub * sub * a.C + kSub * t;
-                    expect((s.bw[e] & 0xffffffffLL) == brow && (s.bw[e] >> 32) == un.n0, name + ": B word");
-                    expect((int64_t)s.aw[e] * kSub == aoff, name + ": A word");
-                    ++e;
-                }
+                for (int64_t t = 0; t < CS; ++t, ++idx)
+                    if (idx >= e0 && idx < e1)
+                        want.push_back({(int64_t)a.indices[blk] * a.C + kSub * t,
+                                        blk * a.R * a.C + kSub * sub * a.C + kSub * t});
+            if (s.rotated) {  // start at the first block column of the unit's rotation, wrapping around
+                expect(pipes == 1, name + ": rotation with one pipeline only");
+                const int64_t kcol = spmm_stream_rotation_column(a.W / a.C, tile / tpg, s.col_groups);
+                size_t off = 0;
+                while (off < want.size() && want[off].first / a.C < kcol) ++off;
+                if (off == want.size()) off = 0;
+                std::rotate(want.begin(), want.begin() + off, want.end());
+            }
+            for (const auto& wb : want) {
+                expect((s.bw[e] & 0xffffffffLL) == wb.first && (s.bw[e] >> 32) == un.n0, name + ": B word");
+                expect((int64_t)s.aw[e] * kSub == wb.second, name + ": A word");
+                ++e;
+            }
             total += un.count;
         }
         expect(total == wg.n && e == wg.w_begin + wg.n, name + ": stream length");
@@ -501,29 +511,34 @@ void check_spmm_stream_pairs(const Bsr& a, int64_t N, int cus, const std::string
             expect(tile / tpg == (int64_t)((g % kNumXcd) % s.col_groups), name + ": unit on its column group's XCD");
             ++seen[un.row * n_tiles + tile];
             if (un.aux >= 0) ++seen[un.aux * n_tiles + tile];
-            int64_t k[2] = {a.indptr[un.row], un.aux >= 0 ? a.indptr[un.aux] : 0};
-            const int64_t end[2] = {a.indptr[un.row + 1], un.aux >= 0 ? a.indptr[un.aux + 1] : 0};
-            int32_t last_col = -1;
-            bool ok = true;
-            for (int32_t c = 0; c < un.count; ++c, ++e) {
-                const int32_t col = (int32_t)(s.bw[e] & 0xffffffffLL) / kSub;
-                ok = ok && (s.bw[e] >> 32) == un.n0 && col > last_col && (s.bw[e] & 0xffffffffLL) % kSub == 0;
-                last_col = col;
-                bool any = false;
-                for (int h = 0; h < 2; ++h) {
-                    const uint32_t wh = (uint32_t)(s.apw[e] >> (32 * h));
-                    const bool next_here = k[h] < end[h] && a.indices[k[h]] == col;
-                    if (wh == kNoBlock) {
-                        ok = ok && !next_here;  // a shared column is one entry with both blocks
-                    } else {
-                        ok = ok && next_here && (int64_t)wh * kSub == k[h] * a.R * a.C;
-                        ++k[h];
-                        any = true;
-                    }
+            // The union in column order: one entry per column either row holds,
+            // with each row's block there (or none), rotated like a single
+            // stripe's unit.
+            std::map<int32_t, std::pair<uint32_t, uint32_t>> uni;
+            for (int h = 0; h < 2; ++h) {
+                const int32_t row = h == 0 ? un.row : un.aux;
+                if (row < 0) continue;
+                for (int64_t blk = a.indptr[row]; blk < a.indptr[row + 1]; ++blk) {
+                    auto it = uni.emplace(a.indices[blk], std::make_pair(kNoBlock, kNoBlock)).first;
+                    (h == 0 ? it->second.first : it->second.second) = (uint32_t)(blk * a.R * a.C / kSub);
                 }
-                ok = ok && any;
             }
-            expect(ok && k[0] == end[0] && k[1] == end[1], name + ": pair entries (union, CSR order, words)");
+            std::vector<std::pair<int32_t, std::pair<uint32_t, uint32_t>>> want(uni.begin(), uni.end());
+            if (s.rotated) {
+                const int64_t kcol = spmm_stream_rotation_column(a.W / a.C, tile / tpg, s.col_groups);
+                size_t off = 0;
+                while (off < want.size() && want[off].first < kcol) ++off;
+                if (off == want.size()) off = 0;
+                std::rotate(want.begin(), want.begin() + off, want.end());
+            }
+            bool ok = un.count == (int32_t)want.size();
+            for (size_t c = 0; ok && c < want.size(); ++c, ++e) {
+                const auto& wt = want[c];
+                ok = (s.bw[e] >> 32) == un.n0 && (s.bw[e] & 0xffffffffLL) == (int64_t)wt.first * a.C &&
+                     s.apw[e] == ((uint64_t)wt.second.first | (uint64_t)wt.second.second << 32);
+            }
+            if (!ok) e = wg.w_begin + wg.n;  // keep the stream-length check meaningful after a mismatch
+            expect(ok, name + ": pair entries (union, each row in CSR order, words)");
         }
         expect(e == wg.w_begin + wg.n, name + ": stream length");
         const SpmmStreamHead& h = s.heads[g];
