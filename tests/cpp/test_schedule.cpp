@@ -393,6 +393,9 @@ void check_spmm_stream(const Bsr& a, int64_t N, int cus, int tile_n, int wpc, co
     if (st != BSP_OK) return;
     const int64_t RS = a.R / kSub, CS = a.C / kSub, nsr = a.H / kSub, n_tiles = N / tile_n;
     const int64_t grid = (int64_t)(cus / kNumXcd) * (pipes == 2 ? 1 : wpc) * kNumXcd;
+    const char* rot_env = std::getenv("BSP_SPMM_ROTATE");
+    expect(s.rotated == (pipes == 1 && !(rot_env && std::atoi(rot_env) == 0) ? 1 : 0),
+           name + ": units rotated with one pipeline unless BSP_SPMM_ROTATE=0");
     expect((int64_t)s.wgs.size() == grid * pipes && s.heads.size() == s.wgs.size(), name + ": grid");
     std::vector<int> seen(nsr * n_tiles, 0);  // entries seen per unit (as a count of parts' coverage)
     std::vector<int64_t> covered(nsr * n_tiles, 0);

@@ -22,13 +22,18 @@ def _run(args, timeout):
     return p
 
 
-def test_scheduler_work_lists():
+@pytest.mark.parametrize("rotate", ["1", "0"])
+def test_scheduler_work_lists(rotate):
     """tests/cpp/test_schedule: the host scheduler's SpMM, SDDMM and SpGEMM
     work lists and workgroup maps (built from the scheduler's source with g++;
-    make rebuilds it when the source changed)."""
+    make rebuilds it when the source changed), with the persistent units
+    rotated by column group (the default) and in CSR order (BSP_SPMM_ROTATE=0)."""
+    import os
     subprocess.run(["make", "-s", "-C", str(REPO / "tests" / "cpp"), "_build/test_schedule"], check=True,
                    capture_output=True)
-    p = _run([str(BUILD / "test_schedule")], 120)
+    env = dict(os.environ, BSP_SPMM_ROTATE=rotate)
+    p = subprocess.run([str(BUILD / "test_schedule")], capture_output=True, text=True, timeout=120, env=env)
+    print(p.stdout[-4000:])
     assert p.returncode == 0, p.stdout + p.stderr
     assert "PASS (0 failed checks)" in p.stdout
 
