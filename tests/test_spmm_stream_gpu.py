@@ -245,3 +245,18 @@ def test_stripe_pairs_chosen_only_where_they_stream_less():
         if want == 2:
             assert (info["stages"], info["a_stages"], info["waves"], info["grid"]) == \
                 (PAIRS[1], PAIRS[2], _waves(PAIRS), 256), info
+
+
+@pytest.mark.parametrize("density", [0.25, 0.5])
+def test_units_rotated_or_in_csr_order(monkeypatch, density):
+    """The plan rotates each persistent unit to start at its column group's
+    share of the block columns (two column groups at 4096^2 x 512); with
+    BSP_SPMM_ROTATE=0 the units run in CSR order.  Both orders are held to
+    the oracle and repeat bit for bit; they differ only in the fp32
+    summation order of a unit."""
+    w = W.workload_spmm_sweep(density)
+    outs = {}
+    for rot in ("1", "0"):
+        monkeypatch.setenv("BSP_SPMM_ROTATE", rot)
+        outs[rot] = _check(w["a"], w["b"], "f32", f"{density} rotate={rot}")  # oracle + repeat
+    assert not np.array_equal(outs["1"], outs["0"]), "the rotation changed no unit's order"
