@@ -596,6 +596,9 @@ int main() {
     check_spmm_stream(uniform(4096, 4096, 32, 32, 164, 3), 512, cus, 128, 2, "stream 4096^2 1%");
     check_spmm_stream(skewed(16384, 16384, 32, 32, 5243, 5), 1024, cus, 128, 2, "stream skewed, duplicates");
     check_spmm_stream(uniform(2048, 1024, 64, 128, 60, 7), 256, cus, 256, 1, "stream 64x128 blocks");
+    check_spmm_stream(uniform(4096, 4096, 32, 64, 1500, 11), 512, cus, 128, 2, "stream 32x64 blocks, 2 col groups");
+    check_spmm_stream(uniform(4096, 4096, 32, 128, 700, 12), 512, cus, 128, 2, "stream 32x128 blocks, 2 col groups");
+    check_spmm_stream(skewed(4096, 4096, 32, 32, 3000, 13), 512, cus, 128, 2, "stream unsorted+dups, 2 col groups");
     check_spmm_stream(uniform(1024, 1024, 32, 32, 0, 9), 256, cus, 128, 1, "stream empty");
     check_spmm_stream(uniform(1024, 1024, 32, 32, 30, 9), 128, 8, 128, 2, "stream 8 CUs");
     check_spmm_stream(uniform(4096, 4096, 32, 32, 4096, 1), 512, cus, 128, 1, "stream 25% two pipelines", 2);

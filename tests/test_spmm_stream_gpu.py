@@ -7,7 +7,7 @@ each launch, so an unwritten element fails."""
 import numpy as np
 import pytest
 
-from helpers import W, assert_parity, bsr_of, capi, golden_spmm, run_spmm, spmm_k_eff
+from helpers import W, assert_parity, bsr_of, capi, golden_spmm, run_spmm, spmm_k_eff, with_values
 
 pytestmark = pytest.mark.gpu
 
@@ -260,3 +260,36 @@ def test_units_rotated_or_in_csr_order(monkeypatch, density):
         monkeypatch.setenv("BSP_SPMM_ROTATE", rot)
         outs[rot] = _check(w["a"], w["b"], "f32", f"{density} rotate={rot}")  # oracle + repeat
     assert not np.array_equal(outs["1"], outs["0"]), "the rotation changed no unit's order"
+
+
+def _unsorted_with_duplicates(seed):
+    """4096^2 in 32x32 blocks, about 18% of the positions: every row's columns
+    shuffled and one column in five repeated (the reference's FILL_COL yields
+    such rows), so a rotation point falls inside unsorted runs."""
+    rng = np.random.default_rng(seed)
+    base = W.random_positions(4096, 4096, 32, 32, 3000, rng)
+    ptr, idx = [0], []
+    for i in range(base.nbrows):
+        cols = list(base.indices[base.indptr[i]:base.indptr[i + 1]])
+        cols += [c for c in cols if rng.random() < 0.2]
+        rng.shuffle(cols)
+        idx += cols
+        ptr.append(len(idx))
+    return W.BsrArrays(4096, 4096, 32, 32, np.array(ptr, np.int32), np.array(idx, np.int32))
+
+
+@pytest.mark.parametrize("name", ["R32_C64", "R32_C128", "unsorted_duplicates"])
+def test_rotated_units_multi_entry_blocks_and_unsorted_rows(monkeypatch, name):
+    """Rotation with two column groups (4096^2 x 512) where a block is several
+    32-column entries (C = 64, 128: the rotation starts at a block boundary)
+    and where rows hold unsorted and repeated columns; held to the oracle in
+    both orders."""
+    rng = np.random.default_rng(41)
+    a = {"R32_C64": lambda: W.random_positions(4096, 4096, 32, 64, 1500, rng),
+         "R32_C128": lambda: W.random_positions(4096, 4096, 32, 128, 700, rng),
+         "unsorted_duplicates": lambda: _unsorted_with_duplicates(43)}[name]()
+    a = with_values(a, "RAND", seed=44)
+    b = W.dense_content(a.W, 512, "RAND", np.random.default_rng(45))
+    for rot in ("1", "0"):
+        monkeypatch.setenv("BSP_SPMM_ROTATE", rot)
+        _check(a, b, "f32", f"{name} rotate={rot}")
