@@ -120,6 +120,23 @@ __device__ __forceinline__ int a_read_offset(int l32, int q) {
     return g * 512 + (8 * (q ^ (g & 1)) + (l32 & 7)) * 16;
 }
 
+// Row layout of a 32x32 A sub-block (the persistent kernel): row r at 64 r,
+// its 16-byte chunk c at slot c ^ ((r >> 2) & 3).  Load j (1 KB, rows
+// 16j .. 16j+15): lane L fills slot L % 4 of row 16j + L / 4, so each four
+// lanes fetch one row's 64 contiguous bytes.  Element offset of what lane L
+// fetches in load j:
+__device__ __forceinline__ int a_row_load_offset(int j, int lane, int lda) {
+    const int r = 16 * j + (lane >> 2);
+    return r * lda + 8 * ((lane & 3) ^ ((r >> 2) & 3));
+}
+// Byte offset of lane (l32, q)'s A operand of k-step s (chunk 2s + q of row
+// l32).  A 16-lane quarter reads one chunk of 16 consecutive rows: their
+// offsets modulo 256 bytes are 64 (r % 4) + 16 (chunk ^ ((r >> 2) & 3)), all
+// sixteen distinct, so the quarter covers the 64 banks once.
+__device__ __forceinline__ int a_row_read_offset(int l32, int q, int s) {
+    return 64 * l32 + 16 * ((2 * s + q) ^ ((l32 >> 2) & 3));
+}
+
 // Direct global->LDS load of 16 bytes per lane: lane L's bytes land at
 // lds_wave_base + 16*L (lds_wave_base is wave-uniform).  Issued as inline asm
 // so that the compiler does not track it: its own bookkeeping would otherwise
@@ -1109,11 +1126,11 @@ __global__ __launch_bounds__(64 * (4 * SR + 1 + NBW) * PIPES) void spmm_stream_k
     };
 
     if (wave == MW + NBW) {
-        // A loader: load j (1 KB) covers segments 2j and 2j+1 of the 32x32
-        // sub-block (lanes 0-31 and 32-63), in the layout of a_load_offset.
+        // A loader: load j (1 KB) covers rows 16j .. 16j+15 of the 32x32
+        // sub-block, in the row layout of a_row_load_offset.
         uint32_t a_voff[2];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) a_voff[j] = 2 * a_load_offset(2 * j + (lane >> 5), lane, p.lda);
+        for (int j = 0; j < 2; ++j) a_voff[j] = 2 * a_row_load_offset(j, lane, p.lda);
         if constexpr (SR == 2) {
             // Stripe pairs: both halves of the stage; a half whose stripe has no
             // block here gets two 16-byte loads by lane 0 (from the other
@@ -1180,7 +1197,8 @@ __global__ __launch_bounds__(64 * (4 * SR + 1 + NBW) * PIPES) void spmm_stream_k
     const int l32 = lane & 31, q = lane >> 5;
     const int half = wave >> 2, wc = wave & 3;
     const BReads<TN, NTW> brd(lane, wc * NTW * 32, false);
-    const int a_rd = a_read_offset(l32, q) + half * kA_BYTES;
+    const int a_rd0 = a_row_read_offset(l32, q, 0) + half * kA_BYTES;
+    const int a_rd1 = a_row_read_offset(l32, q, 1) + half * kA_BYTES;
     f32x16 acc[NTW];
 #pragma unroll
     for (int i = 0; i < NTW; ++i)
@@ -1269,8 +1287,8 @@ __global__ __launch_bounds__(64 * (4 * SR + 1 + NBW) * PIPES) void spmm_stream_k
     };
     auto read = [&](int k, Operands& o) {
         const uint8_t* as = psmem + (k % SA) * A_STAGE;
-        o.a[0] = *(const u32x4*)(as + a_rd);
-        o.a[1] = *(const u32x4*)(as + 256 + a_rd);
+        o.a[0] = *(const u32x4*)(as + a_rd0);
+        o.a[1] = *(const u32x4*)(as + a_rd1);
         if constexpr (SR > 1) o.w = *(const uint32_t*)(psmem + FLAGS + (k % SA) * 8 + half * 4);
         brd.read(psmem + A_RING + (k % SB) * Loader::BYTES, o.b);
     };
