@@ -174,12 +174,11 @@ constexpr int64_t kPairMaxRows = 1024;
 // off): a unit of column group g starts at its first entry whose block column
 // is at least spmm_stream_rotation_column(block columns of A, g, col_groups)
 // and wraps around to its first entry (no rotation when there is none).  The
-// col_groups XCDs that read a stripe's A blocks for different column groups
-// then read each block about 1/col_groups of the stripe apart in time, and
-// the workgroups no longer all open on the lowest block columns of B at
-// once.  Only the summation order of a unit changes (a stripe pair rotates
-// at the same column as its two stripes, so pairs stay bit-identical to
-// single stripes).
+// column groups then sweep the block columns 1/col_groups apart, the units
+// of one column group (which read the same rows of B) still together; in CSR
+// order every workgroup opens on the lowest block columns at once.  Only the
+// summation order of a unit changes (a stripe pair rotates at the same column
+// as its two stripes, so pairs stay bit-identical to single stripes).
 // (4096^2 x 512, f32 C, graph replay: 25% 13.2-13.4 -> 12.3-12.4 us, 50%
 // 21.8-22.3 -> 20.8-21.6 us, 1%, 5% and the skewed workload unchanged.)
 inline int64_t spmm_stream_rotation_column(int64_t block_cols, int64_t group, int64_t col_groups) {
