@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define BSP_ABI_VERSION 5
+#define BSP_ABI_VERSION 6
 
 typedef enum bsp_status {
     BSP_OK = 0,
@@ -121,6 +121,10 @@ typedef struct bsp_plan_info {
                             stripe pairs that share one B slice per shared
                             block column; n_items then counts pair x tile
                             units); 1 otherwise; 0 for other kinds */
+    int32_t units_rotated; /* SpMM persistent: 1 when each unit's entries start
+                            at its column group's share of the block columns
+                            (the default; BSP_SPMM_ROTATE=0 at plan creation
+                            keeps them in CSR order), 0 otherwise */
 } bsp_plan_info;
 
 /* ---- library ------------------------------------------------------------- */

@@ -16,7 +16,7 @@ import numpy as np
 PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = PKG_DIR / "libbsparse.so"
 
-ABI_VERSION = 5  # BSP_ABI_VERSION of include/bsparse.h
+ABI_VERSION = 6  # BSP_ABI_VERSION of include/bsparse.h
 BSP_OK = 0
 BSP_ERR_INVALID_ARGUMENT = 1
 BSP_ERR_BAD_STRUCTURE = 2
@@ -65,6 +65,7 @@ class PlanInfo(ctypes.Structure):
         ("a_stages", c_int32),
         ("step_entries", c_int32),
         ("stripes_per_unit", c_int32),
+        ("units_rotated", c_int32),
     ]
 
     def as_dict(self) -> dict:

@@ -388,6 +388,7 @@ int make_spmm_stream_plan(bsp_plan** out, const bsp_bsr_desc* a, int64_t N, int 
     in.a_stages = sv.sa;
     in.step_entries = sv.eps;
     in.stripes_per_unit = sv.sr;
+    in.units_rotated = ss.rotated;
     hipError_t e = upload((bsp::SpmmStreamHead**)&p->d_wgs, ss.heads);
     if (e == hipSuccess) e = upload(&p->d_units, ss.units);
     if (e == hipSuccess) e = upload(&p->d_ent_off, ss.bw);

@@ -42,7 +42,7 @@ def test_library_links_hip_and_has_gfx950_code():
 
 def test_abi_version_and_status_strings():
     lib = capi.load()
-    assert lib.bsp_abi_version() == capi.ABI_VERSION == 5
+    assert lib.bsp_abi_version() == capi.ABI_VERSION == 6
     for code, text in [(0, b"ok"), (2, b"malformed BSR structure"), (3, b"unsupported")]:
         assert lib.bsp_status_string(code) == text
 

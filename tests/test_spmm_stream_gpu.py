@@ -258,6 +258,9 @@ def test_units_rotated_or_in_csr_order(monkeypatch, density):
     outs = {}
     for rot in ("1", "0"):
         monkeypatch.setenv("BSP_SPMM_ROTATE", rot)
+        plan = capi.SpmmPlan(bsr_of(w["a"]), 512, "f32")
+        assert plan.info()["units_rotated"] == int(rot), plan.info()
+        plan.close()
         outs[rot] = _check(w["a"], w["b"], "f32", f"{density} rotate={rot}")  # oracle + repeat
     assert not np.array_equal(outs["1"], outs["0"]), "the rotation changed no unit's order"
 
