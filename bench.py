@@ -1,12 +1,15 @@
 """Benchmark: effective TFLOP/s of block-sparse SpMM on one MI355X.
 
-Workload of the headline line: C = A*B with A 4096x4096 in 32x32 bf16 blocks
-at 25% uniform-random block density, B 4096x512 bf16, fp32 accumulation and
-fp32 output.  The same run reports every benchmark configuration as a section:
+Workload of the headline (`value`): the skewed SpMM, the largest single-GPU
+configuration: C = A*B with A 16384x16384 in 32x32 bf16 blocks, Zipf(1.2)
+blocks per block row capped at 512 and rescaled to 2% mean density (5243
+blocks), B 16384x1024 bf16, fp32 accumulation and fp32 output.  It is
+HBM-bound (99 FLOP per algorithmic byte), so its roofline is the HBM one.
+The same run measures every benchmark configuration as a section:
   c1         A 1024x1024, 10%, N=256 (the reference's CPU-golden case)
   sweep      A 4096x4096, densities 1/5/25/50%, N=512, fp32 and bf16 C
   sddmm      mask 4096x4096 10%, X 4096x256, Y 256x4096
-  skewed     A 16384x16384, Zipf(1.2) rows, 2% mean, N=1024
+  skewed     the headline workload
   attention  seq 8192, d 128: SDDMM then SpMM, and the fused pair
   spgemm     8192x8192 x 8192x8192, 32x32 blocks, 5% x 5%
   large      the reference's 8192^3 configuration (256x256 blocks, 25%) and
@@ -14,6 +17,12 @@ fp32 output.  The same run reports every benchmark configuration as a section:
   patterns   the reference's pattern families (Row, Col, Multi-diag, Random,
              tril, triu) at 8192^3 with 256x256 blocks
   host       the blocking host-buffer entry point (PCIe included; never `value`)
+  ablation   load balancing on and off (the reference's `_no_lb` operators) and
+             the per-workgroup timeline of the instrumented library (only when
+             asked for with --only ablation)
+The last stdout line is one compact JSON object: the headline fields, its
+roofline and CPU baseline, and a `summary` row per configuration.  The full
+per-section records are written to --sections-out.
 
 A step is one launch over the whole workload.  Inputs are resident in HBM:
 the timed launches cycle through enough copies of the operands and outputs
@@ -69,8 +78,10 @@ def parse_args():
     p.add_argument("--copy-calibration", action="store_true",
                    help="first run a 256 MiB device copy and a 256 MiB elementwise multiply (kernels of known traffic, "
                         "for scaling FETCH_SIZE / WRITE_SIZE counters)")
-    p.add_argument("--only", default="", help="comma list of sections (head = the 25%% fp32 sweep point only): "
+    p.add_argument("--only", default="", help="comma list of sections (head = the skewed headline workload only): "
                    + ", ".join(("head",) + SECTIONS))
+    p.add_argument("--sections-out", default=str(REPO / "gpurun_out" / "bench_sections.json"),
+                   help="file for the full per-section records (the last stdout line carries the summary)")
     return p.parse_args()
 
 
@@ -159,7 +170,8 @@ def summarize(t, flops, nbytes):
 
 
 def plan_summary(info):
-    keys = ("tile_n", "stages", "group", "grid", "waves", "persistent", "a_stages", "step_entries", "n_split_rows")
+    keys = ("tile_n", "stages", "group", "grid", "waves", "persistent", "a_stages", "step_entries", "n_split_rows",
+            "n_entries", "n_items")
     return {k: info[k] for k in keys if k in info}
 
 
@@ -635,7 +647,6 @@ def main():
         del src, dst
 
     out = {}
-    head = None
 
     def spmm_section(w, od, label, rotate=True, cpu=True):
         t, fl, nb, info, ncopy = bench_spmm(torch, capi, W, w["a"], w["b"], od, timer, warmup, rotate=rotate)
@@ -653,18 +664,13 @@ def main():
         rec["input_sha256"] = W.workload_digest(w)
         out["c1"] = rec
 
-    if run("sweep") or run("head"):
-        head_only = "head" in only and "sweep" not in only
+    if run("sweep"):
         sweep = []
         for d in W.SPMM_SWEEP_DENSITIES:
-            if head_only and d != 0.25:
-                continue
             w = W.workload_spmm_sweep(d)
             digest = W.workload_digest(w)
             cpu_rec = None
             for od in ("f32", "bf16"):
-                if head_only and od != "f32":
-                    continue
                 rec, t, fl, nb, info = spmm_section(
                     w, od, f"SpMM A 4096x4096, 32x32 blocks, {int(d * 100)}%, B 4096x512, {od} C",
                     cpu=cpu_rec is None)
@@ -676,10 +682,6 @@ def main():
                                       if isinstance(v, dict) else v) for k, v in cpu_rec.items()}
                 rec.update({"density": d, "input_sha256": digest})
                 sweep.append(rec)
-                if d == 0.25 and od == "f32":
-                    head = (t, fl, nb, rec, info)
-            if head_only:
-                continue
             # warm (cache-resident) figure for the same launch, for reference
             t, fl, nb, info, _ = bench_spmm(torch, capi, W, w["a"], w["b"], "f32", timer, warmup, rotate=False)
             sweep.append({"density": d, "out": "f32", "warm_cache": True, **summarize(t, fl, nb)})
@@ -697,7 +699,7 @@ def main():
             rec["cpu"] = cpu_sddmm(orc, W, m, s["x"], s["y"], cores, rec["tflops"])
         out["sddmm"] = rec
 
-    if run("skewed"):
+    if run("skewed") or run("head"):
         w = W.workload_spmm_skewed()
         rec, *_ = spmm_section(w, "f32", "SpMM A 16384x16384 Zipf(1.2) rows, 2% mean density, B 16384x1024, fp32 C")
         rec["input_sha256"] = W.workload_digest(w)
@@ -815,55 +817,155 @@ def main():
         out["host_entry"] = {"workload": "25% SpMM through bsp_host_spmm (host buffers, blocking)",
                              "ms_per_call": round(t_host * 1e3, 3), "tflops": round(fl / t_host / 1e12, 4)}
 
-    if head is None:
-        print(json.dumps(out))
-        return
-    t, fl, nbytes, row, info = head
-    us = t["launch_ms"] * 1e3
     roofs = measure_roofs(torch)
-    tr = row.get("traffic", {}).get("bytes_per_launch")
-    rl = roofline(fl, nbytes, us, tr, next(iter(row.get("kernels", {})), None) if row.get("kernels") else None)
-    rl["on_chip"] = on_chip_roof(info, us, roofs)
-    rl["hbm_stream_tbs"] = roofs["hbm_stream_tbs"]
     big = dense_gemm(torch, 8192, 8192, 8192)
-    rl["mfma_attainable"] = {"dense_gemm_tflops": big["tflops"], "frac_of_peak": round(big["tflops"] / PEAK_BF16_TFLOPS, 4),
-                             "note": "torch.matmul bf16 8192^3 (hipBLASLt), graph replay, operands resident: the MFMA "
-                                     "rate a tuned dense kernel sustains on this GPU"}
-    rl["dense_gemm"] = row.get("dense_gemm")
-    if row.get("kernel_us"):
-        rl["kernel_us"] = row["kernel_us"]
+    sections_path = Path(args.sections_out)
+    sections_path.parent.mkdir(parents=True, exist_ok=True)
+    sections_path.write_text(json.dumps({"roofs": roofs, "dense_gemm_8192": big, **out}, indent=1))
+    if "skewed" not in out:
+        print(json.dumps({"sections": os.path.relpath(sections_path, REPO), "summary": summary_rows(out, roofs)}))
+        return
+    shown = os.path.relpath(sections_path, REPO) if sections_path.is_absolute() else str(sections_path)
+    line = build_headline(out, roofs, big, steps, warmup, shown)
+    print(json.dumps(line, separators=(",", ":")))
+
+
+# ---------------------------------------------------------------------------
+# The result line.  Full per-section records go to a side file; the last
+# stdout line carries the headline (the largest single-GPU configuration, the
+# skewed 16384^2 SpMM) and one compact row per configuration.
+HEADLINE_MAX_BYTES = 8192
+
+
+def floor_us(flops, nbytes, roofs):
+    """Attainable time of one launch: the empty launch (graph replay of an
+    empty kernel, same run) plus the longer of the algorithmic bytes at the
+    measured HBM stream rate and the FLOPs at the MFMA peak."""
+    t_hbm = nbytes / (roofs["hbm_stream_tbs"] * 1e12) * 1e6
+    t_mfma = flops / (PEAK_BF16_TFLOPS * 1e12) * 1e6
+    return round(roofs["empty_launch_us"] + max(t_hbm, t_mfma), 3)
+
+
+def _row(rec, roofs):
+    us = rec["us_per_launch"]
+    r = {"us": us, "kernel_us": rec.get("kernel_us"), "tflops": round(rec["tflops"], 1),
+         "mfma": round(rec["frac_mfma_peak"], 4), "hbm": round(rec["frac_hbm_peak"], 4)}
+    if rec.get("kernel_us"):
+        r["kernel_hbm"] = round(rec["kernel_frac_hbm_peak"], 4)
+    tr = rec.get("traffic")
+    if tr:
+        r["traffic_x"] = tr["ratio_to_algorithmic"]
+    if roofs:
+        f = floor_us(rec["flops"], rec["bytes"], roofs)
+        r["floor_us"] = f
+        r["frac_of_floor"] = round(f / us, 3)
+    cpu = rec.get("cpu")
+    if cpu and "single" in cpu:
+        r["cpu_x"] = [cpu["single"].get("gpu_speedup"), cpu["all"].get("gpu_speedup")]
+    return r
+
+
+def summary_rows(out, roofs):
+    """One compact row per configuration: replay us, kernel us, TFLOP/s,
+    fractions of the MFMA and HBM peaks, measured traffic over algorithmic
+    bytes, the attainable floor and the fraction of it reached, and the GPU
+    speedup over the one-thread and all-core CPU oracle."""
+    rows = {}
+    if "c1" in out:
+        rows["c1"] = _row(out["c1"], roofs)
+    for rec in out.get("sweep", []):
+        if rec.get("warm_cache"):
+            continue
+        r = _row(rec, roofs)
+        if rec["density"] == 0.25 and rec["out"] == "f32" and "plan" in rec and "n_entries" in rec["plan"]:
+            r["on_chip_frac"] = on_chip_roof(rec["plan"], rec["us_per_launch"], roofs)["frac"]
+        rows[f"c2_{int(round(rec['density'] * 100))}_{rec['out']}"] = r
+    if "sddmm" in out:
+        rows["c3"] = _row(out["sddmm"], roofs)
+    if "skewed" in out:
+        rows["c4"] = _row(out["skewed"], roofs)
+    if "attention" in out:
+        at = out["attention"]
+        rows["c5_sddmm"] = _row(at["sddmm"], roofs)
+        rows["c5_spmm"] = _row(at["spmm"], roofs)
+        rows["c5_fused"] = _row(dict(at["fused"], cpu=at.get("cpu")), roofs)
+    if "spgemm" in out:
+        for r in out["spgemm"]["runs"]:
+            rows[f"spgemm_{r['out']}"] = _row(r, roofs)
+    if "large_blocks" in out:
+        for r in out["large_blocks"]["runs"]:
+            rows[f"8192c_256_{r['out']}"] = _row(r, roofs)
+    if "block_sizes" in out:
+        for r in out["block_sizes"]["runs"]:
+            rows[f"8192c_{r['R']}_f32"] = _row(r, roofs)
+    if "patterns" in out:
+        for r in out["patterns"]["runs"]:
+            key = f"pat_{r['pattern']}" + ("" if r["pattern"] in ("tril", "triu") else f"_{int(round(r['density'] * 100))}")
+            rows[key] = {"tflops": round(r["tflops"], 1), "mfma": round(r["frac_mfma_peak"], 4),
+                         "n150_dda_tflops": r.get("reference_dda_tflops_n150")}
+    if "ablation" in out:
+        rows["ablation"] = out["ablation"].get("summary")
+    if "host_entry" in out:
+        rows["host_ms"] = out["host_entry"]["ms_per_call"]
+    return rows
+
+
+def build_headline(out, roofs, big, steps, warmup, sections_path):
+    """The result line: the skewed 16384^2 SpMM (the largest single-GPU
+    configuration) as `value`, its HBM roofline (it is HBM-bound: 99 FLOP per
+    algorithmic byte) and CPU baseline, and the per-configuration summary."""
+    rec = out["skewed"]
+    us = rec["us_per_launch"]
+    kname = next(iter(rec.get("kernels") or {}), None)
+    tr = rec.get("traffic", {}).get("bytes_per_launch")
+    rl = roofline(rec["flops"], rec["bytes"], us, tr, kname)
+    for k in ("algorithmic_flop_per_launch", "algorithmic_bytes_per_launch"):
+        rl.pop(k, None)
+    rl.update({"bytes_per_launch": rec["bytes"], "flop_per_launch": rec["flops"],
+               "traffic_source": rec.get("traffic", {}).get("source"),
+               "floor_us": floor_us(rec["flops"], rec["bytes"], roofs),
+               "hbm_stream_tbs": roofs["hbm_stream_tbs"], "empty_launch_us": roofs["empty_launch_us"],
+               "mfma_attainable_tflops": big["tflops"]})
+    rl["frac_of_floor"] = round(rl["floor_us"] / us, 4)
+    if rec.get("kernel_us"):
+        rl["kernel_us"] = rec["kernel_us"]
+        rl["kernel_frac"] = round(rec["bytes"] / (rec["kernel_us"] * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)
     cpu = None
-    if "cpu" in row:
-        c = row["cpu"]
+    if "cpu" in rec:
+        c = rec["cpu"]
         cpu = {"value": c["all"]["tflops"], "unit": "TFLOP/s", "cores": c["all"]["cores"], "kind": "port",
-               "sample": f"{c['all']['sample']} of the 25% workload, OpenMP over block rows; median of 3 runs "
+               "sample": f"{c['all']['sample']} of the skewed workload, OpenMP over block rows; median of 3 runs "
                          f"after 1 warm-up: {c['all']['seconds']} s",
                "single_core": {"value": c["single"]["tflops"], "cores": 1,
-                               "sample": f"{c['single']['sample']}: {c['single']['seconds']} s"}}
-    result = {
+                               "sample": f"{c['single']['sample']}: {c['single']['seconds']} s"},
+               "gpu_speedup": [c["single"]["gpu_speedup"], c["all"]["gpu_speedup"]]}
+    return {
         "metric": "effective TFLOP/s on nonzero blocks (SpMM, SDDMM); % bf16 MFMA peak / % HBM BW",
-        "value": round(fl / (us * 1e-6) / 1e12, 3),
+        "value": round(rec["tflops"], 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": steps,
         "warmup": warmup,
-        "ms_per_step": round(t["launch_ms"], 6),
+        "ms_per_step": round(us * 1e-3, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded xoshiro256** uniform-random block positions, U[-1,1] bf16 values)",
-        "config": {"workload": "BSR SpMM C=A*B: A 4096x4096, 32x32 blocks, 25% block density (4096 blocks), "
-                               "B 4096x512 bf16, fp32 accumulate, fp32 C",
-                   "M": 4096, "K": 4096, "N": 512, "block": [32, 32], "density": 0.25,
-                   "input_sha256": row.get("input_sha256"),
+        "data": "synthetic (seeded xoshiro256**: Zipf(1.2) row counts, uniform block columns, U[-1,1] bf16 values)",
+        "config": {"workload": "skewed BSR SpMM C=A*B: A 16384x16384, 32x32 blocks, Zipf(1.2) blocks per block row "
+                               "capped at 512, 2% mean density (5243 blocks), B 16384x1024 bf16, fp32 accumulate, "
+                               "fp32 C",
+                   "M": 16384, "K": 16384, "N": 1024, "block": [32, 32], "nnzb": rec["nnzb"],
+                   "max_row_blocks": rec.get("max_row_blocks"), "input_sha256": rec.get("input_sha256"),
+                   "timing": "graph replay of `steps` launches between two HIP events on the launch stream; "
+                             "inputs rotated over > 512 MB of copies",
                    "peaks": {"bf16_mfma_tflops": PEAK_BF16_TFLOPS, "hbm_gbs": PEAK_HBM_GBS,
                              "source": "AMD Instinct MI355X published dense figures"}},
         "roofline": rl,
         "cpu_baseline": cpu,
+        "summary": summary_rows(out, roofs),
+        "sections": sections_path,
     }
-    result.update(out)
-    print(json.dumps(result))
 
 
 if __name__ == "__main__":

@@ -275,18 +275,30 @@ int bsp_host_spgemm(const bsp_bsr_desc* a, const uint16_t* a_vals, const bsp_bsr
 /* ---- SpMM without device allocation ------------------------------------------
  * No counterpart in the reference: an entry point for callers that cannot
  * allocate device memory (serving loops that must not touch the allocator,
- * harnesses that forbid hipMalloc).  C = A * B as bsp_spmm computes it (the
- * same persistent kernel and schedule a plan would use, except that a plan's
- * stripe pairs run as single stripes here, which gives the same bits),
- * without a plan: the schedule is built on the host and staged in a static
- * device array of
+ * harnesses that forbid hipMalloc).  C = A * B on the persistent SpMM kernel
+ * (the 32-row stripe kernel a plan takes for 32x32 blocks), without a plan:
+ * the schedule is built on the host and staged in a static device array of
  * BSP_NOALLOC_SCRATCH_BYTES that the library holds on every GPU it runs on
- * until the process ends.  It calls no hipMalloc or hipFree.  The call waits
- * for the schedule's copy on `stream` (and the stream's earlier work), then
- * launches asynchronously.  Calls on one GPU share the array: two calls that
- * overlap on one GPU race (order them on one stream, and let a launch finish
- * before the next call from another stream).  A schedule above the limit
- * returns BSP_ERR_UNSUPPORTED; so does N not a multiple of 128.
+ * until the process ends.  It calls no hipMalloc or hipFree.
+ *   Result: bit-identical to bsp_spmm with a plan that takes the persistent
+ *   kernel with single stripes (a plan's stripe pairs give the same bits).  A
+ *   plan that takes another kernel -- the row-group kernels some R >= 64
+ *   structures take, or a schedule changed by environment overrides at plan
+ *   creation -- may sum in another order; both stay within the oracle's
+ *   tolerance.
+ *   Synchronisation: the call copies the schedule on `stream` and then WAITS
+ *   ON THE HOST for `stream` (all of its earlier work and that copy) before
+ *   launching asynchronously.  It is therefore not asynchronous in the host's
+ *   sense, and it cannot be recorded into a HIP graph: on a stream under
+ *   capture it returns BSP_ERR_UNSUPPORTED without touching the stream.
+ *   Sharing: calls on one GPU share the array, which keeps the last call's
+ *   contents; two calls that overlap on one GPU race (order them on one
+ *   stream, and let a launch finish before the next call from another
+ *   stream).
+ *   Errors: the structure is validated first (as bsp_validate_bsr);
+ *   a schedule above the limit, N not a multiple of 128, or R, C not
+ *   multiples of 32 return BSP_ERR_UNSUPPORTED; no device, or a failed
+ *   compute-unit count query, BSP_ERR_DEVICE.
  * a: host BSR structure; a_vals, b, c: device pointers as for bsp_spmm. */
 #define BSP_NOALLOC_SCRATCH_BYTES (16 << 20)
 int bsp_spmm_noalloc(const bsp_bsr_desc* a, const uint16_t* a_vals, const uint16_t* b, int64_t N,

@@ -9,9 +9,12 @@
 // Set-up: the first call on a device takes the array's device address with
 // that device current (hipGetSymbolAddress) and keeps it per device; host code
 // passes that address, never the array's name, to the copy and the kernel.
-// Each call builds the schedule on the host, copies it into the array on the
-// caller's stream and waits for that copy (so the host staging buffer can be
-// reused), then launches asynchronously.  Nothing in the array needs to start
+// Each call validates the structure, builds the schedule on the host, copies
+// it into the array on the caller's stream and waits for that copy (so the
+// host staging buffer can be reused), then launches asynchronously.  The wait
+// blocks the host on the caller's stream, so the call cannot be recorded into
+// a HIP graph: on a stream under capture it returns BSP_ERR_UNSUPPORTED
+// before touching the stream.  Nothing in the array needs to start
 // at zero: every byte the kernel reads is written by the call's own copy.
 // Calls on one GPU share the array and keep the last call's contents, so two
 // calls that overlap on one GPU (different streams, or a launch still running
@@ -68,6 +71,16 @@ size_t put(std::vector<unsigned char>& buf, size_t off, const std::vector<T>& v)
 extern "C" int bsp_spmm_noalloc(const bsp_bsr_desc* a, const uint16_t* a_vals, const uint16_t* b, int64_t N,
                                 int64_t ldb, void* c, int64_t ldc, int out_dtype, int device, void* stream) {
     if (!a) return bsp::record_error(BSP_ERR_INVALID_ARGUMENT, "null BSR descriptor");
+    {
+        // The structure first: the variant choice and the schedule builder
+        // below index host arrays by indptr and indices.
+        std::string vmsg;
+        const int vst = bsp::validate_bsr(a, vmsg);
+        if (vst != BSP_OK) return bsp::record_error(vst, vmsg);
+    }
+    if (N <= 0) return bsp::record_error(BSP_ERR_INVALID_ARGUMENT, "N must be positive");
+    if (a->C % 32 != 0 || a->R % 32 != 0)
+        return bsp::record_error(BSP_ERR_UNSUPPORTED, "R and C must be multiples of 32");
     if (out_dtype != BSP_DTYPE_F32 && out_dtype != BSP_DTYPE_BF16)
         return bsp::record_error(BSP_ERR_INVALID_ARGUMENT, "out_dtype must be BSP_DTYPE_F32 or BSP_DTYPE_BF16");
     if (!b || !c || (a->nblocks > 0 && !a_vals)) return bsp::record_error(BSP_ERR_INVALID_ARGUMENT, "null device pointer");
@@ -82,18 +95,46 @@ extern "C" int bsp_spmm_noalloc(const bsp_bsr_desc* a, const uint16_t* a_vals, c
     if (N % 128 != 0)
         return bsp::record_error(BSP_ERR_UNSUPPORTED, "bsp_spmm_noalloc needs N a multiple of 128 (the persistent "
                                                       "kernel's tile); use a plan for other N");
+    {
+        // A lower bound of the schedule, checked before any device query: its
+        // entry words alone (an int64 B word and a uint32 A word per 32x32
+        // sub-block product and column tile), at the widest tile (256).
+        const int64_t min_bytes = 12 * a->nblocks * (a->R / 32) * (a->C / 32) * (N / 256);
+        if (min_bytes > (int64_t)BSP_NOALLOC_SCRATCH_BYTES)
+            return bsp::record_error(BSP_ERR_UNSUPPORTED,
+                                     "the schedule needs at least " + std::to_string((long long)min_bytes) +
+                                         " bytes, above the " + std::to_string((long long)BSP_NOALLOC_SCRATCH_BYTES) +
+                                         " bytes of the no-allocation scratch; use a plan");
+    }
 
+    // The device: present, not capturing on `stream` (the copy below waits on
+    // the host), and its compute-unit count, for which the schedule is built.
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0 || device >= count)
+        return bsp::record_error(BSP_ERR_DEVICE, "no HIP device " + std::to_string(device));
+    int cus = 0;
+    hipError_t qe = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (qe != hipSuccess || cus <= 0)
+        return bsp::record_error(BSP_ERR_DEVICE, std::string("compute-unit count of device ") + std::to_string(device) +
+                                                     ": " + hipGetErrorString(qe));
+    {
+        int prev = -1;
+        hipError_t ce = hipGetDevice(&prev);
+        if (ce == hipSuccess && prev != device) ce = hipSetDevice(device);
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        if (ce == hipSuccess) ce = hipStreamIsCapturing((hipStream_t)stream, &cap);
+        if (prev >= 0 && prev != device) (void)hipSetDevice(prev);
+        if (ce != hipSuccess)
+            return bsp::record_error(BSP_ERR_DEVICE, std::string("hipStreamIsCapturing: ") + hipGetErrorString(ce));
+        if (cap != hipStreamCaptureStatusNone)
+            return bsp::record_error(BSP_ERR_UNSUPPORTED, "bsp_spmm_noalloc waits for its schedule copy on the host and "
+                                                          "cannot be captured in a HIP graph; use a plan (bsp_spmm)");
+    }
     // The schedule, built on the host as a plan builds it (same variant
     // choice, but one pipeline per workgroup and one stripe per unit: a plan
     // that would take stripe pairs runs the default variant here, with the
-    // same per-stripe summation order), for 256 compute units per 8 XCDs
-    // unless the device says otherwise.
-    int cus = 256;
-    int count = 0;
-    if (hipGetDeviceCount(&count) == hipSuccess && device < count) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && n > 0) cus = n;
-    }
+    // same per-stripe summation order).  Blocks of R >= 64, which a plan may
+    // run on the row-group kernels, run the persistent kernel here.
     bsp::SpmmStreamVariant sv = bsp::kSpmmStreamDefault;
     int wpc = 2;
     if (!bsp::choose_spmm_stream(a, N, cus, &sv, &wpc) || sv.pipes != 1 || sv.sr != 1) {
@@ -113,7 +154,6 @@ extern "C" int bsp_spmm_noalloc(const bsp_bsr_desc* a, const uint16_t* a_vals, c
                                  "the schedule needs " + std::to_string(total) + " bytes, above the " +
                                      std::to_string((long long)BSP_NOALLOC_SCRATCH_BYTES) +
                                      " bytes of the no-allocation scratch; use a plan");
-    if (count <= 0 || device >= count) return bsp::record_error(BSP_ERR_DEVICE, "no HIP device " + std::to_string(device));
 
     unsigned char* base = nullptr;
     st = scratch_on(device, &base);

@@ -99,6 +99,27 @@ def run_spmm(a, b: np.ndarray, out_dtype="f32", plan=None, poison=True) -> np.nd
     return W.bf16_to_f32(out.view(np.uint16))
 
 
+def strided_run(a, b, out_dtype, ldb, ldc, call):
+    """Runs `call(da, b_view, c_view)` with B and C as the first N columns of
+    wider tensors (row strides ldb and ldc), their padding poisoned with NaN.
+    Returns (C as fp32, C's padding as raw bits, the padding's poison bits)."""
+    import torch
+    K, N, M = a.W, b.shape[1], a.H
+    da = torch.from_numpy(np.ascontiguousarray(a.data).view(np.int16)).cuda()
+    bw = torch.full((K, ldb), 0x7FC0, dtype=torch.int16, device="cuda")
+    bw[:, :N] = torch.from_numpy(np.ascontiguousarray(b).view(np.int16)).cuda()
+    if out_dtype == "f32":
+        cw = torch.full((M, ldc), float("nan"), dtype=torch.float32, device="cuda")
+    else:
+        cw = torch.full((M, ldc), 0x7FC0, dtype=torch.int16, device="cuda")
+    pad0 = cw[:, N:].cpu().numpy().copy()
+    call(da, bw[:, :N], cw[:, :N])
+    torch.cuda.synchronize()
+    out = cw.cpu().numpy()
+    got = out[:, :N] if out_dtype == "f32" else W.bf16_to_f32(out[:, :N].view(np.uint16))
+    return np.ascontiguousarray(got), out[:, N:], pad0
+
+
 def run_sddmm(mask, x: np.ndarray, y: np.ndarray, out_dtype="f32", y_layout=None, plan=None,
               poison=True) -> np.ndarray:
     """mask (.) (X*Y) block values on the GPU; y is passed as given (K x N for

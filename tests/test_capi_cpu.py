@@ -410,21 +410,54 @@ def test_library_first_then_torch_shares_one_hip_runtime():
 
 def test_noalloc_rejects_a_schedule_above_its_scratch_before_any_device_work():
     """bsp_spmm_noalloc checks its schedule against BSP_NOALLOC_SCRATCH_BYTES
-    (and N against its tile) before it touches a device: 1M blocks times two
-    tiles need about 24 MB of entry words."""
+    (and N against its tile) before it touches a device: 1M blocks times four
+    128-column tiles need about 48 MB of entry words (24 MB at the widest
+    tile)."""
     nbr = 1024
     indptr = np.arange(nbr + 1, dtype=np.int32) * 1024
     indices = np.tile(np.arange(1024, dtype=np.int32), nbr)
     d = capi.Bsr(nbr * 32, 1024 * 32, 32, 32, indptr, indices).desc()
     lib = capi.load()
     buf = ctypes.c_void_p(16)  # never dereferenced: the call fails before any device work
-    st = lib.bsp_spmm_noalloc(ctypes.byref(d), buf, buf, 256, 256, buf, 256, capi.DTYPE_F32, 0, None)
+    st = lib.bsp_spmm_noalloc(ctypes.byref(d), buf, buf, 512, 512, buf, 512, capi.DTYPE_F32, 0, None)
     assert st == capi.BSP_ERR_UNSUPPORTED
     assert "no-allocation scratch" in capi.last_error()
     small = capi.Bsr(64, 64, 32, 32, np.array([0, 1, 1], np.int32), np.array([0], np.int32)).desc()
     st = lib.bsp_spmm_noalloc(ctypes.byref(small), buf, buf, 96, 96, buf, 96, capi.DTYPE_F32, 0, None)
     assert st == capi.BSP_ERR_UNSUPPORTED and "multiple of 128" in capi.last_error()
     assert capi.NOALLOC_SCRATCH_BYTES == 16 << 20
+
+
+def test_noalloc_validates_the_structure_before_using_it():
+    """A column index out of range or a null indptr is rejected as by
+    bsp_validate_bsr, before the schedule builder reads the arrays (an
+    out-of-range column would otherwise index host tables out of bounds)."""
+    lib = capi.load()
+    buf = ctypes.c_void_p(16)  # never dereferenced: the call fails before any device work
+    nbr = 64
+    indptr = np.arange(nbr + 1, dtype=np.int32) * 4
+    indices = np.tile(np.array([0, 5, 9, 70], np.int32), nbr)  # 70 >= 64 block columns
+    bsr = capi.Bsr(nbr * 32, 64 * 32, 32, 32, indptr, indices)
+    d = bsr.desc()
+    assert lib.bsp_validate_bsr(ctypes.byref(d)) == capi.BSP_ERR_BAD_STRUCTURE
+    st = lib.bsp_spmm_noalloc(ctypes.byref(d), buf, buf, 4096, 4096, buf, 4096, capi.DTYPE_F32, 0, None)
+    assert st == capi.BSP_ERR_BAD_STRUCTURE and "indices[" in capi.last_error()
+    d.indptr = None
+    st = lib.bsp_spmm_noalloc(ctypes.byref(d), buf, buf, 4096, 4096, buf, 4096, capi.DTYPE_F32, 0, None)
+    assert st == capi.BSP_ERR_INVALID_ARGUMENT and "indptr is null" in capi.last_error()
+
+
+def test_noalloc_reports_a_missing_device_as_an_error():
+    """A valid call with no GPU visible returns BSP_ERR_DEVICE (never a
+    silent default compute-unit count)."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    lib = capi.load()
+    buf = ctypes.c_void_p(16)
+    small = capi.Bsr(64, 64, 32, 32, np.array([0, 1, 1], np.int32), np.array([0], np.int32)).desc()
+    st = lib.bsp_spmm_noalloc(ctypes.byref(small), buf, buf, 128, 128, buf, 128, capi.DTYPE_F32, 0, None)
+    assert st == capi.BSP_ERR_DEVICE
 
 
 class _OnGpu:

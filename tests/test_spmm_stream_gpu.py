@@ -7,7 +7,7 @@ each launch, so an unwritten element fails."""
 import numpy as np
 import pytest
 
-from helpers import W, assert_parity, bsr_of, capi, golden_spmm, run_spmm, spmm_k_eff, with_values
+from helpers import W, assert_parity, bsr_of, capi, golden_spmm, run_spmm, spmm_k_eff, strided_run, with_values
 
 pytestmark = pytest.mark.gpu
 
@@ -296,3 +296,28 @@ def test_rotated_units_multi_entry_blocks_and_unsorted_rows(monkeypatch, name):
     for rot in ("1", "0"):
         monkeypatch.setenv("BSP_SPMM_ROTATE", rot)
         _check(a, b, "f32", f"{name} rotate={rot}")
+
+
+
+@pytest.mark.parametrize("out_dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("v", [DEFAULT, PAIRS, (128, 6, 12, 2, 2, 1, 1)])
+def test_strided_b_and_c(monkeypatch, v, out_dtype):
+    """B and C as column slices of wider tensors (ldb = N + 64, ldc = N + 128)
+    with NaN-poisoned padding: the result equals the contiguous run bit for
+    bit, is held to the oracle, and the padding columns stay untouched."""
+    import torch
+    _stream_env(monkeypatch, v)
+    w = W.spmm_workload(2048, 2048, 512, 32, 32, 0.1, seed=91)
+    a, b = w["a"], w["b"]
+    N = b.shape[1]
+    plan = capi.SpmmPlan(bsr_of(a), N, out_dtype)
+    assert plan.info()["persistent"] >= 1
+    ref = run_spmm(a, b, out_dtype, plan=plan)
+
+    def call(da, bv, cv):
+        plan.run(da, bv, cv, stream=torch.cuda.current_stream().cuda_stream)
+    got, pad, pad0 = strided_run(a, b, out_dtype, N + 64, N + 128, call)
+    plan.close()
+    np.testing.assert_array_equal(got, ref, err_msg=f"strided {v} {out_dtype}")
+    np.testing.assert_array_equal(pad.view(np.uint8), pad0.view(np.uint8), err_msg="padding of C was written")
+    assert_parity(got, golden_spmm(a, b), spmm_k_eff(a), f"strided {v} {out_dtype}")
