@@ -65,7 +65,7 @@ sys.path.insert(0, str(REPO))
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (AMD Instinct MI355X datasheet)
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 ROTATE_BYTES = 600 << 20   # > 2 x the 256 MB Infinity Cache
-SECTIONS = ("c1", "sweep", "sddmm", "skewed", "attention", "spgemm", "large", "patterns", "host")
+SECTIONS = ("c1", "sweep", "sddmm", "skewed", "attention", "spgemm", "large", "patterns", "host", "ablation")
 
 
 def parse_args():
@@ -630,6 +630,8 @@ def main():
     def run(section):
         if only and section not in only:
             return False
+        if not only and section == "ablation":  # its own run: bench.py --only ablation
+            return False
         print(f"[bench] {section}", file=sys.stderr, flush=True)  # progress, one line per section
         return True
     steps, warmup = args.steps, args.warmup
@@ -817,6 +819,9 @@ def main():
         out["host_entry"] = {"workload": "25% SpMM through bsp_host_spmm (host buffers, blocking)",
                              "ms_per_call": round(t_host * 1e3, 3), "tflops": round(fl / t_host / 1e12, 4)}
 
+    if run("ablation"):
+        out["ablation"] = ablation(torch, capi, W, timer, warmup)
+
     roofs = measure_roofs(torch)
     big = dense_gemm(torch, 8192, 8192, 8192)
     sections_path = Path(args.sections_out)
@@ -828,6 +833,205 @@ def main():
     shown = os.path.relpath(sections_path, REPO) if sections_path.is_absolute() else str(sections_path)
     line = build_headline(out, roofs, big, steps, warmup, shown)
     print(json.dumps(line, separators=(",", ":")))
+
+
+# ---------------------------------------------------------------------------
+# Ablation: load balancing on and off, and the per-workgroup timeline.
+#
+# The reference prices its kernels' parts with profiling variants of its
+# operators (block_spmm/inc/host_code.hpp:86-161, registered in
+# HostCodeRegistryProfiling, :195-222; block_sddmm/PROFILING_PLAN.md).  Two of
+# its comparisons are rebuilt here on committed code:
+#   - load balancing on and off (its `_no_lb` operators; the published table
+#     block_spmm/scripts/figures/load_imbalance_table.csv): plans built with
+#     BSP_SPMM_BALANCE=0 keep rows whole and place work in natural order, in
+#     contiguous ranges;
+#   - where a launch's time goes: libbsparse_timeline.so (the same sources,
+#     plus per-workgroup wall-clock stamps, include/bsparse_timeline.h) gives
+#     each workgroup's start, first landing, progress and end.
+# Variants that skip part of the work are not built into committed code; the
+# timeline takes their place.
+class plan_env:
+    """Environment variables set while plans are created (the library reads
+    its schedule overrides at plan creation)."""
+
+    def __init__(self, env):
+        self.env = dict(env or {})
+
+    def __enter__(self):
+        self.saved = {k: os.environ.get(k) for k in self.env}
+        os.environ.update({k: str(v) for k, v in self.env.items()})
+
+    def __exit__(self, *exc):
+        for k, v in self.saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+def timeline_stats(stamps, khz, kind):
+    """Per-workgroup phases from a (grid x 64) stamp array: start offset from
+    the first workgroup's start, first landing after its own start, work end
+    after the first start, and (persistent SpMM) the time per unit."""
+    s = stamps.astype(np.int64)
+    ok = s[:, 0] > 0
+    s = s[ok]
+    if not len(s):
+        return {"workgroups": 0}
+    t0 = s[:, 0].min()
+    to_us = 1000.0 / khz
+    q = lambda v: {"p10": round(float(np.percentile(v, 10)), 3), "p50": round(float(np.median(v)), 3),
+                   "p90": round(float(np.percentile(v, 90)), 3), "max": round(float(np.max(v)), 3)}
+    start = (s[:, 0] - t0) * to_us
+    end = (s[:, 63] - t0) * to_us
+    landed = s[:, 1] > 0
+    rec = {"workgroups": int(len(s)), "clock_khz": khz,
+           "start_offset_us": q(start),
+           "first_landing_us": q((s[landed, 1] - s[landed, 0]) * to_us) if landed.any() else None,
+           "end_us": q(end), "span_us": round(float(end.max()), 3),
+           "busy_us": q(end - start)}
+    if kind == "persistent":
+        # unit ends in slots 2.. (each unit with entries); the time between
+        # consecutive ends, and the first unit's end after the first landing
+        per = []
+        for row in s:
+            u = row[2:63]
+            u = u[u > 0]
+            if len(u) > 1:
+                per.extend(np.diff(u) * to_us)
+        rec["unit_us"] = q(np.array(per)) if per else None
+    if kind == "sweep":
+        # progress stamps every 8 entries: time per 8 entries after the first landing
+        per = []
+        for row in s:
+            u = row[2:63]
+            u = u[u > 0]
+            if len(u) > 1:
+                per.extend(np.diff(u) * to_us)
+        rec["per_8_entries_us"] = q(np.array(per)) if per else None
+    if kind == "sddmm":
+        done = s[:, 2] > 0
+        rec["products_us"] = q((s[done, 2] - s[done, 1]) * to_us) if done.any() else None
+    return rec
+
+
+def _timeline_run(torch, capi, tl, launch, grid, reps=3):
+    """Launches through the timeline library `reps` times (cold operands:
+    each launch takes the next copy) and returns the last launch's stamps and
+    the stamp clock in kHz."""
+    stamps = torch.zeros((grid, capi.TIMELINE_SLOTS), dtype=torch.int64, device="cuda")
+    st = torch.cuda.current_stream()
+    capi.check(tl.bsp_timeline_attach(stamps.data_ptr(), grid, 0), tl)
+    try:
+        for i in range(reps):
+            stamps.zero_()
+            launch(i, st.cuda_stream)
+        torch.cuda.synchronize()
+    finally:
+        tl.bsp_timeline_attach(None, 0, 0)
+    khz = ctypes.c_int(0)
+    capi.check(tl.bsp_timeline_clock_khz(0, ctypes.byref(khz)), tl)
+    return stamps.cpu().numpy(), khz.value
+
+
+def timeline_spmm(torch, capi, W, a, b, out_dtype, env, kind):
+    tl = capi.load_timeline()
+    M, N = a.H, b.shape[1]
+    with plan_env(env):
+        plan = capi.SpmmPlan(capi.Bsr(a.H, a.W, a.R, a.C, a.indptr, a.indices), N, out_dtype, lib=tl)
+    info = plan.info()
+    out_bytes = 4 if out_dtype == "f32" else 2
+    per_copy = a.data.nbytes + b.nbytes + M * N * out_bytes
+    ncopy = max(1, -(-ROTATE_BYTES // per_copy))
+    da0, db0 = dev_u16(torch, a.data), dev_u16(torch, b)
+    copies = [(da0.clone(), db0.clone(),
+               torch.empty((M, N), dtype=torch.float32 if out_dtype == "f32" else torch.int16, device="cuda"))
+              for _ in range(ncopy)]
+
+    def launch(i, stream):
+        da, db, dc = copies[i % ncopy]
+        plan.run(da, db, dc, stream=stream)
+    stamps, khz = _timeline_run(torch, capi, tl, launch, info["grid"])
+    plan.close()
+    rec = timeline_stats(stamps, khz, kind)
+    rec["plan"] = plan_summary(info)
+    return rec
+
+
+def timeline_sddmm(torch, capi, W, m, x, y, out_dtype):
+    tl = capi.load_timeline()
+    K = x.shape[1]
+    plan = capi.SddmmPlan(capi.Bsr(m.H, m.W, m.R, m.C, m.indptr, m.indices), K, capi.ROW_MAJOR, out_dtype, lib=tl)
+    info = plan.info()
+    nv = m.nblocks * m.R * m.C
+    base = [dev_u16(torch, v) for v in (m.data, x, y)]
+    per_copy = m.data.nbytes + x.nbytes + y.nbytes + nv * 4
+    ncopy = max(1, -(-ROTATE_BYTES // per_copy))
+    copies = [[v.clone() for v in base] + [torch.empty(nv, dtype=torch.float32, device="cuda")]
+              for _ in range(ncopy)]
+
+    def launch(i, stream):
+        dm, dx, dy, do = copies[i % ncopy]
+        plan.run(dm, dx, dy, do, ldy=m.W, stream=stream)
+    stamps, khz = _timeline_run(torch, capi, tl, launch, info["grid"])
+    plan.close()
+    rec = timeline_stats(stamps, khz, "sddmm")
+    rec["plan"] = {"grid": info["grid"], "one_shot": info["stages"]}
+    return rec
+
+
+def ablation(torch, capi, W, timer, warmup):
+    """Load balancing on and off, and the per-workgroup timelines."""
+    rec = {"balance": [], "timeline": {}}
+    published = {"tril": (43.31, 29.5), "triu": (29.6, 24.88)}  # N150 DDA with / without LB, 8192, R=C=256
+    w = W.workload_spmm_skewed()
+    for label, env in (("skewed 16384^2, persistent kernel", {}),
+                       ("skewed 16384^2, per-item kernels", {"BSP_SPMM_STREAM": "0"})):
+        row = {"workload": label}
+        for lb in ("1", "0"):
+            with plan_env(dict(env, BSP_SPMM_BALANCE=lb)):
+                t, fl, nb, info, _ = bench_spmm(torch, capi, W, w["a"], w["b"], "f32", timer, warmup)
+            row["balanced" if lb == "1" else "unbalanced"] = {"us": round(t["launch_ms"] * 1e3, 3),
+                                                              "tflops": round(fl / (t["launch_ms"] * 1e-3) / 1e12, 1),
+                                                              "kernel_us": t.get("kernel_us") and round(t["kernel_us"], 3),
+                                                              "plan": plan_summary(info)}
+        row["speedup"] = round(row["unbalanced"]["us"] / row["balanced"]["us"], 3)
+        rec["balance"].append(row)
+    lt = Timer(torch, max(10, timer.steps // 10), trace=timer.trace)
+    b = pattern_b(W)
+    for pat in ("tril", "triu"):
+        a = pattern_workload(W, pat, 1.0)
+        row = {"workload": f"{pat} 8192^3, 256x256 blocks ({a.nblocks} blocks), bf16 C",
+               "reference_n150_dda_tflops": {"balanced": published[pat][0], "unbalanced": published[pat][1]}}
+        for lb in ("1", "0"):
+            with plan_env({"BSP_SPMM_BALANCE": lb}):
+                t, fl, nb, info, _ = bench_spmm(torch, capi, W, a, b, "bf16", lt, max(5, warmup // 2))
+            row["balanced" if lb == "1" else "unbalanced"] = {"us": round(t["launch_ms"] * 1e3, 3),
+                                                              "tflops": round(fl / (t["launch_ms"] * 1e-3) / 1e12, 1),
+                                                              "plan": plan_summary(info)}
+        row["speedup"] = round(row["unbalanced"]["us"] / row["balanced"]["us"], 3)
+        rec["balance"].append(row)
+        del a
+    del b
+    # timelines
+    w25 = W.workload_spmm_sweep(0.25)
+    rec["timeline"]["c2_25_f32"] = timeline_spmm(torch, capi, W, w25["a"], w25["b"], "f32", {}, "persistent")
+    rec["timeline"]["c4_persistent"] = timeline_spmm(torch, capi, W, w["a"], w["b"], "f32", {}, "persistent")
+    rec["timeline"]["c4_persistent_unbalanced"] = timeline_spmm(torch, capi, W, w["a"], w["b"], "f32",
+                                                                {"BSP_SPMM_BALANCE": "0"}, "persistent")
+    rec["timeline"]["c4_sweep"] = timeline_spmm(torch, capi, W, w["a"], w["b"], "f32", {"BSP_SPMM_SWEEP": "2"},
+                                                "sweep")
+    s3 = W.workload_sddmm()
+    rec["timeline"]["c3_sddmm"] = timeline_sddmm(torch, capi, W, s3["mask"], s3["x"], s3["y"], "f32")
+    rec["summary"] = {
+        "lb_speedup": {r["workload"].split(",")[0].split(" ")[0] + ("_items" if "per-item" in r["workload"] else ""):
+                       r["speedup"] for r in rec["balance"]},
+        "timeline_p50_us": {k: {"start": v["start_offset_us"]["p50"],
+                                "landing": v["first_landing_us"]["p50"] if v.get("first_landing_us") else None,
+                                "end": v["end_us"]["p50"], "span": v["span_us"]}
+                            for k, v in rec["timeline"].items() if v.get("workgroups")}}
+    return rec
 
 
 # ---------------------------------------------------------------------------

@@ -112,7 +112,9 @@ typedef struct bsp_plan_info {
                             persistent kernel with that many pipelines per
                             workgroup (each pipeline streams a list of stripe x
                             tile units; n_items counts the units, stages is the
-                            B ring depth) */
+                            B ring depth); 3 = sweep kernel (one workgroup per
+                            compute unit holding up to 16 units at once, see
+                            bsp_spmm_sweep_schedule) */
     int32_t a_stages;    /* SpMM persistent: depth of the A ring */
     int32_t step_entries;/* SpMM: entries per ring step, i.e. per workgroup
                             barrier (1, or 2 for the persistent kernel's
@@ -247,6 +249,26 @@ int bsp_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, bsp_plan_in
                       int32_t* items, int32_t* ent_row, int64_t* ent_off, int32_t* wgmap);
 int bsp_sddmm_schedule(const bsp_bsr_desc* mask, int64_t K, int num_cus, bsp_plan_info* info,
                        int32_t* items, int32_t* ent_row, int64_t* ent_off, int32_t* wgmap);
+
+/* SpMM sweep schedule (the sweep kernel a plan takes for large 32x32-block
+ * structures: one workgroup per compute unit holding up to 16 units -- 32-row
+ * stripe x 128 columns -- whose entries are merged by block column).  No
+ * counterpart in the reference: its load balancing is
+ * block_spmm/inc/host_code/bsr_spmm_multicore_load_balanced_new_DM.cpp
+ * :339-393, this is the MI355X schedule that replaces it for such shapes.
+ * col_groups: 0 = the plan's choice, else 1, 2, 4 or 8.  Sizes in *info:
+ * grid workgroups, n_slots sweep records, n_entries entries, group = column
+ * groups taken.
+ *   wgs     grid x 4 int32   {first entry, entries, first sweep, sweeps}
+ *   sweeps  n_slots x 33 int32 {entries, stripe of slots 0-15 (-1: unused),
+ *                               first column of slots 0-15}
+ *   bw      n_entries int64  first row of B | first column << 32 | slot << 56
+ *                            | skip << 60 (a skip entry pads a sweep to an
+ *                            even count and is not multiplied)
+ *   aw      n_entries uint32 element offset of the 32x32 A sub-block / 32 */
+int bsp_spmm_sweep_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, int col_groups,
+                            bsp_plan_info* info, int32_t* wgs, int32_t* sweeps, int64_t* bw,
+                            uint32_t* aw);
 
 /* ---- host-buffer, blocking entry points ------------------------------------
  * bsp_host_spmm: the HostCodeFunctionPtr shape (block_spmm/inc/host_code.hpp

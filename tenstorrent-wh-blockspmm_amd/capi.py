@@ -15,6 +15,7 @@ import numpy as np
 
 PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = PKG_DIR / "libbsparse.so"
+TIMELINE_PATH = PKG_DIR / "libbsparse_timeline.so"
 
 ABI_VERSION = 6  # BSP_ABI_VERSION of include/bsparse.h
 BSP_OK = 0
@@ -91,6 +92,8 @@ SIGNATURES = {
     "bsp_plan_destroy": (c_int, [c_void_p]),
     "bsp_spmm_schedule": (c_int, [_DESC_P, c_int64, c_int, _INFO_P, _I32P, _I32P, _I64P, _I32P]),
     "bsp_sddmm_schedule": (c_int, [_DESC_P, c_int64, c_int, _INFO_P, _I32P, _I32P, _I64P, _I32P]),
+    "bsp_spmm_sweep_schedule": (c_int, [_DESC_P, c_int64, c_int, c_int, _INFO_P, _I32P, _I32P, _I64P,
+                                        POINTER(ctypes.c_uint32)]),
     "bsp_host_spmm": (c_int, [_DESC_P, c_void_p, c_void_p, c_int64, c_void_p, c_int, c_int]),
     "bsp_host_sddmm": (c_int, [_DESC_P, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int, c_int]),
     "bsp_spgemm_symbolic": (c_int, [_DESC_P, _DESC_P, _I64P, _I32P, _I32P]),
@@ -145,13 +148,32 @@ def load(path: Optional[Path] = None, force_reload: bool = False) -> ctypes.CDLL
     return lib
 
 
-def last_error() -> str:
-    return load().bsp_last_error().decode()
+def last_error(lib: Optional[ctypes.CDLL] = None) -> str:
+    return (lib or load()).bsp_last_error().decode()
 
 
-def check(status: int) -> None:
+def check(status: int, lib: Optional[ctypes.CDLL] = None) -> None:
     if status != BSP_OK:
-        raise BsparseError(status, last_error())
+        raise BsparseError(status, last_error(lib))
+
+
+TIMELINE_SLOTS = 64  # BSP_TIMELINE_SLOTS of include/bsparse_timeline.h
+_timeline_lib: Optional[ctypes.CDLL] = None
+
+
+def load_timeline() -> ctypes.CDLL:
+    """libbsparse_timeline.so: every entry point of libbsparse.so (same
+    results), plus per-workgroup time stamps (include/bsparse_timeline.h).
+    Pass it as `lib` to the plan classes to run a plan through it."""
+    global _timeline_lib
+    if _timeline_lib is None:
+        lib = load(TIMELINE_PATH)
+        lib.bsp_timeline_attach.restype = c_int
+        lib.bsp_timeline_attach.argtypes = [c_void_p, c_int64, c_int]
+        lib.bsp_timeline_clock_khz.restype = c_int
+        lib.bsp_timeline_clock_khz.argtypes = [c_int, POINTER(c_int)]
+        _timeline_lib = lib
+    return _timeline_lib
 
 
 def _i32(a) -> np.ndarray:
@@ -252,8 +274,9 @@ def _dtype_code(out_dtype) -> int:
 
 
 class _Plan:
-    def __init__(self):
+    def __init__(self, lib: Optional[ctypes.CDLL] = None):
         self._h = c_void_p()
+        self._lib = lib or load()
 
     @property
     def handle(self) -> c_void_p:
@@ -263,12 +286,12 @@ class _Plan:
 
     def info(self) -> dict:
         inf = PlanInfo()
-        check(load().bsp_plan_info_get(self.handle, ctypes.byref(inf)))
+        check(self._lib.bsp_plan_info_get(self.handle, ctypes.byref(inf)), self._lib)
         return inf.as_dict()
 
     def close(self) -> None:
         if self._h:
-            load().bsp_plan_destroy(self._h)
+            self._lib.bsp_plan_destroy(self._h)
             self._h = c_void_p()
 
     def __del__(self):
@@ -281,12 +304,12 @@ class _Plan:
 class SpmmPlan(_Plan):
     """Plan for C[M x N] = A (BSR) * B[K x N] on one device."""
 
-    def __init__(self, bsr: Bsr, N: int, out_dtype="f32", device: int = 0):
-        super().__init__()
+    def __init__(self, bsr: Bsr, N: int, out_dtype="f32", device: int = 0, lib: Optional[ctypes.CDLL] = None):
+        super().__init__(lib)
         self.bsr, self.N, self.out_dtype, self.device = bsr, int(N), _dtype_code(out_dtype), device
         d = bsr.desc()
-        check(load().bsp_spmm_plan_create(ctypes.byref(self._h), ctypes.byref(d), self.N, ROW_MAJOR,
-                                          self.out_dtype, device))
+        check(self._lib.bsp_spmm_plan_create(ctypes.byref(self._h), ctypes.byref(d), self.N, ROW_MAJOR,
+                                          self.out_dtype, device), self._lib)
 
     def run(self, a_vals, b, c, ldb: Optional[int] = None, ldc: Optional[int] = None,
             stream: Optional[int] = None) -> None:
@@ -297,19 +320,19 @@ class SpmmPlan(_Plan):
         pa = _operand(a_vals, "a_vals", 2, 1, nv, nv, self.device)[0] if nv else _ptr(a_vals)
         pb, ldb = _operand(b, "b", 2, bs.W, self.N, ldb, self.device)
         pc, ldc = _operand(c, "c", 4 if self.out_dtype == DTYPE_F32 else 2, bs.H, self.N, ldc, self.device)
-        check(load().bsp_spmm(self.handle, pa, pb, ldb, pc, ldc, stream))
+        check(self._lib.bsp_spmm(self.handle, pa, pb, ldb, pc, ldc, stream), self._lib)
 
 
 class SddmmPlan(_Plan):
     """Plan for out = mask (.) (X[M x K] * Y[K x N]) at the mask's blocks."""
 
-    def __init__(self, mask: Bsr, K: int, y_layout: int = ROW_MAJOR, out_dtype="f32", device: int = 0):
-        super().__init__()
+    def __init__(self, mask: Bsr, K: int, y_layout: int = ROW_MAJOR, out_dtype="f32", device: int = 0, lib: Optional[ctypes.CDLL] = None):
+        super().__init__(lib)
         self.mask, self.K, self.y_layout, self.device = mask, int(K), int(y_layout), device
         self.out_dtype = _dtype_code(out_dtype)
         d = mask.desc()
-        check(load().bsp_sddmm_plan_create(ctypes.byref(self._h), ctypes.byref(d), self.K, self.y_layout,
-                                           self.out_dtype, device))
+        check(self._lib.bsp_sddmm_plan_create(ctypes.byref(self._h), ctypes.byref(d), self.K, self.y_layout,
+                                           self.out_dtype, device), self._lib)
 
     def run(self, mask_vals, x, y, out_vals, ldx: Optional[int] = None, ldy: Optional[int] = None,
             stream: Optional[int] = None) -> None:
@@ -319,26 +342,26 @@ class SddmmPlan(_Plan):
         m = self.mask
         nv = m.nblocks * m.R * m.C
         if nv == 0:
-            check(load().bsp_sddmm(self.handle, None, None, 0, None, 0, None, stream))
+            check(self._lib.bsp_sddmm(self.handle, None, None, 0, None, 0, None, stream), self._lib)
             return
         pm = _operand(mask_vals, "mask_vals", 2, 1, nv, nv, self.device)[0]
         px, ldx = _operand(x, "x", 2, m.H, self.K, ldx, self.device)
         yr, yc = (self.K, m.W) if self.y_layout == ROW_MAJOR else (m.W, self.K)
         py, ldy = _operand(y, "y", 2, yr, yc, ldy, self.device)
         po = _operand(out_vals, "out_vals", 4 if self.out_dtype == DTYPE_F32 else 2, 1, nv, nv, self.device)[0]
-        check(load().bsp_sddmm(self.handle, pm, px, ldx, py, ldy, po, stream))
+        check(self._lib.bsp_sddmm(self.handle, pm, px, ldx, py, ldy, po, stream), self._lib)
 
 
 class AttentionPlan(_Plan):
     """Plan for the fused pair O = bf16(mask (.) (Q * K^T)) * V on the mask's
     structure (queries x keys), head dimension 32, 64 or 128."""
 
-    def __init__(self, mask: Bsr, head_dim: int, out_dtype="f32", device: int = 0):
-        super().__init__()
+    def __init__(self, mask: Bsr, head_dim: int, out_dtype="f32", device: int = 0, lib: Optional[ctypes.CDLL] = None):
+        super().__init__(lib)
         self.mask, self.d, self.out_dtype, self.device = mask, int(head_dim), _dtype_code(out_dtype), device
         dsc = mask.desc()
-        check(load().bsp_attention_plan_create(ctypes.byref(self._h), ctypes.byref(dsc), self.d,
-                                               self.out_dtype, device))
+        check(self._lib.bsp_attention_plan_create(ctypes.byref(self._h), ctypes.byref(dsc), self.d,
+                                               self.out_dtype, device), self._lib)
 
     def run(self, mask_vals, q, k, v, out, ldq: Optional[int] = None, ldk: Optional[int] = None,
             ldv: Optional[int] = None, ldo: Optional[int] = None, stream: Optional[int] = None) -> None:
@@ -351,7 +374,7 @@ class AttentionPlan(_Plan):
         pk, ldk = _operand(k, "k", 2, m.W, d, ldk, self.device)
         pv, ldv = _operand(v, "v", 2, m.W, d, ldv, self.device)
         po, ldo = _operand(out, "out", 4 if self.out_dtype == DTYPE_F32 else 2, m.H, d, ldo, self.device)
-        check(load().bsp_attention(self.handle, pm, pq, ldq, pk, ldk, pv, ldv, po, ldo, stream))
+        check(self._lib.bsp_attention(self.handle, pm, pq, ldq, pk, ldk, pv, ldv, po, ldo, stream), self._lib)
 
 
 def _structure(fn, nbrows: int, *args):
@@ -376,13 +399,13 @@ def spgemm_symbolic(a: Bsr, b: Bsr) -> Bsr:
 class SpgemmPlan(_Plan):
     """Plan for C = A * B with A, B and C in BSR; `structure` is C's."""
 
-    def __init__(self, a: Bsr, b: Bsr, out_dtype="f32", device: int = 0):
-        super().__init__()
+    def __init__(self, a: Bsr, b: Bsr, out_dtype="f32", device: int = 0, lib: Optional[ctypes.CDLL] = None):
+        super().__init__(lib)
         self.a, self.b, self.out_dtype, self.device = a, b, _dtype_code(out_dtype), device
         da, db = a.desc(), b.desc()
-        check(load().bsp_spgemm_plan_create(ctypes.byref(self._h), ctypes.byref(da), ctypes.byref(db),
-                                            self.out_dtype, device))
-        indptr, indices = _structure(load().bsp_spgemm_structure, a.nbrows, self.handle)
+        check(self._lib.bsp_spgemm_plan_create(ctypes.byref(self._h), ctypes.byref(da), ctypes.byref(db),
+                                            self.out_dtype, device), self._lib)
+        indptr, indices = _structure(self._lib.bsp_spgemm_structure, a.nbrows, self.handle)
         self.structure = Bsr(a.H, b.W, a.R, b.C, indptr, indices)
 
     @property
@@ -397,7 +420,7 @@ class SpgemmPlan(_Plan):
         pb = _operand(b_vals, "b_vals", 2, 1, nb, nb, self.device)[0] if nb else _ptr(b_vals)
         po = _operand(out_vals, "out_vals", 4 if self.out_dtype == DTYPE_F32 else 2, 1, no, no, self.device)[0] \
             if no else _ptr(out_vals)
-        check(load().bsp_spgemm(self.handle, pa, pb, po, stream))
+        check(self._lib.bsp_spgemm(self.handle, pa, pb, po, stream), self._lib)
 
 
 def _schedule(fn_name: str, bsr: Bsr, n: int, num_cus: int) -> dict:
@@ -424,6 +447,28 @@ def _schedule(fn_name: str, bsr: Bsr, n: int, num_cus: int) -> dict:
 
 def spmm_schedule(bsr: Bsr, N: int, num_cus: int = 256) -> dict:
     return _schedule("bsp_spmm_schedule", bsr, N, num_cus)
+
+
+def spmm_sweep_schedule(bsr: Bsr, N: int, num_cus: int = 256, col_groups: int = 0) -> dict:
+    """The sweep kernel's schedule (host only): per-workgroup records
+    {first entry, entries, first sweep, sweeps}, sweep records {entries,
+    stripe of slots 0-15, first column of slots 0-15}, and the entry words."""
+    lib = load()
+    d = bsr.desc()
+    inf = PlanInfo()
+    null32, null64 = ctypes.cast(None, _I32P), ctypes.cast(None, _I64P)
+    nullu = ctypes.cast(None, POINTER(ctypes.c_uint32))
+    check(lib.bsp_spmm_sweep_schedule(ctypes.byref(d), N, num_cus, col_groups, ctypes.byref(inf), null32, null32,
+                                      null64, nullu))
+    wgs = np.zeros((max(inf.grid, 1), 4), np.int32)
+    sweeps = np.zeros((max(inf.n_slots, 1), 33), np.int32)
+    bw = np.zeros(max(inf.n_entries, 1), np.int64)
+    aw = np.zeros(max(inf.n_entries, 1), np.uint32)
+    check(lib.bsp_spmm_sweep_schedule(ctypes.byref(d), N, num_cus, col_groups, ctypes.byref(inf),
+                                      wgs.ctypes.data_as(_I32P), sweeps.ctypes.data_as(_I32P),
+                                      bw.ctypes.data_as(_I64P), aw.ctypes.data_as(POINTER(ctypes.c_uint32))))
+    return {"info": inf.as_dict(), "wgs": wgs[: inf.grid], "sweeps": sweeps[: inf.n_slots],
+            "bw": bw[: inf.n_entries], "aw": aw[: inf.n_entries]}
 
 
 def sddmm_schedule(mask: Bsr, K: int, num_cus: int = 256) -> dict:

@@ -38,6 +38,10 @@ struct bsp_plan {
     bsp::SpmmStreamUnit* d_units = nullptr;
     uint32_t* d_aw = nullptr;
     uint64_t* d_apw = nullptr;
+    // SpMM sweep kernel (info.persistent == 3): sweep records (heads in
+    // d_wgs, B words in d_ent_off, A words in d_aw).
+    bsp::SpmmSweepRec* d_sweeps = nullptr;
+    int sweep_ax4 = 0;
 };
 
 namespace {
@@ -87,6 +91,8 @@ void free_plan_buffers(bsp_plan* p) {
     if (p->d_units) (void)hipFree(p->d_units);
     if (p->d_aw) (void)hipFree(p->d_aw);
     if (p->d_apw) (void)hipFree(p->d_apw);
+    if (p->d_sweeps) (void)hipFree(p->d_sweeps);
+    p->d_sweeps = nullptr;
     p->d_units = nullptr;
     p->d_aw = nullptr;
     p->d_apw = nullptr;
@@ -213,6 +219,51 @@ int bsp_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, bsp_plan_in
     return BSP_OK;
 }
 
+int bsp_spmm_sweep_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, int col_groups, bsp_plan_info* info,
+                            int32_t* wgs, int32_t* sweeps, int64_t* bw, uint32_t* aw) {
+    if (!info) return fail(BSP_ERR_INVALID_ARGUMENT, "info is null");
+    bsp::SpmmSweep s;
+    std::string msg;
+    int st = bsp::build_spmm_sweep(a, N, num_cus, s, msg, col_groups);
+    if (st != BSP_OK) return fail(st, msg);
+    std::memset(info, 0, sizeof(*info));
+    info->kind = 1;
+    info->tile_n = bsp::kSweepTile;
+    info->n_tiles = s.n_tiles;
+    info->n_items = (int32_t)s.n_units;
+    info->n_entries = (int32_t)s.n_entries;
+    info->grid = (int32_t)s.wgs.size();
+    info->max_item_entries = s.max_wg_entries;
+    info->n_slots = (int32_t)(s.sweeps.size() - bsp::kStreamPad);
+    info->stages = bsp::kSweepStages;
+    info->group = s.col_groups;
+    info->waves = bsp::kSweepWaves;
+    info->persistent = 3;
+    info->a_stages = bsp::kSweepStages;
+    info->step_entries = 2;
+    info->stripes_per_unit = 1;
+    info->units_rotated = s.rotated;
+    if (wgs)
+        for (size_t g = 0; g < s.wgs.size(); ++g) {
+            const bsp::SpmmSweepWg& w = s.wgs[g];
+            int32_t* o = wgs + 4 * g;
+            o[0] = w.w_begin; o[1] = w.n; o[2] = w.s_begin; o[3] = w.n_sweeps;
+        }
+    if (sweeps)
+        for (int32_t r = 0; r < info->n_slots; ++r) {
+            const bsp::SpmmSweepRec& rec = s.sweeps[(size_t)r];
+            int32_t* o = sweeps + 33 * r;
+            o[0] = rec.count;
+            for (int j = 0; j < 16; ++j) {
+                o[1 + j] = rec.half[j / 8].row[j % 8];
+                o[17 + j] = rec.half[j / 8].n0[j % 8];
+            }
+        }
+    if (bw && s.n_entries) std::memcpy(bw, s.bw.data(), (size_t)s.n_entries * 8);
+    if (aw && s.n_entries) std::memcpy(aw, s.aw.data(), (size_t)s.n_entries * 4);
+    return BSP_OK;
+}
+
 int bsp_sddmm_schedule(const bsp_bsr_desc* m, int64_t K, int num_cus, bsp_plan_info* info,
                        int32_t* items, int32_t* ent_row, int64_t* ent_off, int32_t* wgmap) {
     if (!info) return fail(BSP_ERR_INVALID_ARGUMENT, "info is null");
@@ -248,6 +299,29 @@ int64_t env_int(const char* name, int64_t dflt) {
 }  // namespace
 
 namespace bsp {
+
+// Whether an SpMM plan takes the sweep kernel (see bsp_kernels.hpp).  It is
+// taken only when asked for (BSP_SPMM_SWEEP=2: whenever the shape allows; 1:
+// for 32x32 blocks, a structure the persistent kernel would run as single
+// stripes, at least 8 units per compute unit and B of at least 8 MB).  It
+// cuts the skewed 16384^2 x 1024 workload's HBM-side reads from 189 to 111 MB
+// but runs it in 69-88 us against the persistent kernel's 37, so no plan
+// takes it by default.
+bool choose_spmm_sweep(const bsp_bsr_desc* a, int64_t N, int cus) {
+    const int64_t mode = env_int("BSP_SPMM_SWEEP", 0);
+    if (mode == 0) return false;
+    if (a->R % bsp::kSub || a->C % bsp::kSub || N <= 0 || N % bsp::kSweepTile || N >= bsp::kSweepMaxN) return false;
+    if (a->nblocks * a->R * a->C / bsp::kSub > UINT32_MAX) return false;
+    if (mode == 2) return true;
+    if (std::getenv("BSP_SPMM_STREAM_VARIANT")) return false;  // a persistent variant was asked for
+    if (a->R != bsp::kSub || a->C != bsp::kSub) return false;
+    const int64_t units = (a->H / bsp::kSub) * (N / bsp::kSweepTile);
+    if (units < 8 * (int64_t)cus || a->W * N * 2 < (int64_t(8) << 20)) return false;
+    bsp::SpmmStreamVariant sv{};
+    int wpc = 1;
+    if (!choose_spmm_stream(a, N, cus, &sv, &wpc)) return false;
+    return sv.sr == 1;
+}
 
 // Whether an SpMM plan runs the persistent kernel, and which variant.  It
 // takes blocks whose stripes do not form row groups (row groups share each B
@@ -403,6 +477,59 @@ int make_spmm_stream_plan(bsp_plan** out, const bsp_bsr_desc* a, int64_t N, int 
     return BSP_OK;
 }
 
+// Plan of the sweep SpMM kernel: per-workgroup sweeps of up to 16 units and
+// their entries merged by first row of B.
+int make_spmm_sweep_plan(bsp_plan** out, const bsp_bsr_desc* a, int64_t N, int out_dtype, int device, int cus) {
+    std::string msg;
+    bsp::SpmmSweep sw;
+    const int cg = (int)env_int("BSP_SPMM_XCD_COLS", 0);
+    int st = bsp::build_spmm_sweep(a, N, cus, sw, msg, cg);
+    if (st != BSP_OK) return fail(st, msg);
+    DeviceGuard g(device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    bsp_plan* p = new bsp_plan();
+    p->kind = 1;
+    p->device = device;
+    p->out_dtype = out_dtype;
+    p->layout = BSP_ROW_MAJOR;
+    p->M = a->H;
+    p->K = a->W;
+    p->N = N;
+    p->R = a->R;
+    p->C = a->C;
+    p->nblocks = a->nblocks;
+    bsp_plan_info& in = p->info;
+    std::memset(&in, 0, sizeof(in));
+    in.kind = 1;
+    in.tile_n = bsp::kSweepTile;
+    in.n_tiles = sw.n_tiles;
+    in.n_items = (int32_t)sw.n_units;
+    in.n_entries = (int32_t)sw.n_entries;
+    in.grid = (int32_t)sw.wgs.size();
+    in.max_item_entries = sw.max_wg_entries;
+    in.stages = bsp::kSweepStages;
+    in.group = 1;
+    in.waves = bsp::kSweepWaves;
+    in.persistent = 3;
+    in.a_stages = bsp::kSweepStages;
+    in.step_entries = 2;
+    in.stripes_per_unit = 1;
+    in.units_rotated = sw.rotated;
+    p->sweep_ax4 = (int)env_int("BSP_SWEEP_AX4", 0);
+    hipError_t e = upload((bsp::SpmmSweepHead**)&p->d_wgs, sw.heads);
+    if (e == hipSuccess) e = upload(&p->d_sweeps, sw.sweeps);
+    if (e == hipSuccess) e = upload(&p->d_ent_off, sw.bw);
+    if (e == hipSuccess) e = upload(&p->d_aw, sw.aw);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        free_plan_buffers(p);
+        delete p;
+        return hip_fail(e, "SpMM plan upload");
+    }
+    *out = p;
+    return BSP_OK;
+}
+
 // Plan of an SpMM-shaped launch (SpMM, or the fused attention pair with the
 // mask as A and N = head dimension): schedule, upload, split-row scratch.
 int make_spmm_plan(bsp_plan** out, int kind, const bsp_bsr_desc* a, int64_t N, int out_dtype, int device,
@@ -416,6 +543,7 @@ int make_spmm_plan(bsp_plan** out, int kind, const bsp_bsr_desc* a, int64_t N, i
     st = device_cus(device, &cus);
     if (st != BSP_OK) return st;
     if (kind == 1) {
+        if (bsp::choose_spmm_sweep(a, N, cus)) return make_spmm_sweep_plan(out, a, N, out_dtype, device, cus);
         bsp::SpmmStreamVariant sv{};
         int wpc = 1;
         if (bsp::choose_spmm_stream(a, N, cus, &sv, &wpc)) return make_spmm_stream_plan(out, a, N, out_dtype, device, cus, sv, wpc);
@@ -511,7 +639,22 @@ int bsp_spmm(const bsp_plan* p, const uint16_t* a_vals, const uint16_t* b, int64
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     const bsp::SpmmArgs args = spmm_args(p, a_vals, b, ldb, c, ldc);
     hipError_t e;
-    if (p->info.persistent) {
+    if (p->info.persistent == 3) {
+        bsp::SpmmSweepArgs sa{};
+        sa.a = a_vals;
+        sa.b = b;
+        sa.c = c;
+        sa.heads = (const bsp::SpmmSweepHead*)p->d_wgs;
+        sa.sweeps = p->d_sweeps;
+        sa.bw = p->d_ent_off;
+        sa.aw = p->d_aw;
+        sa.ldb = ldb;
+        sa.ldc = ldc;
+        sa.lda = (int32_t)p->C;
+        sa.N = (int32_t)p->N;
+        e = bsp::launch_spmm_sweep(sa, p->out_dtype == BSP_DTYPE_BF16, p->sweep_ax4 != 0, p->info.grid,
+                                   (hipStream_t)stream);
+    } else if (p->info.persistent) {
         bsp::SpmmStreamArgs sa{};
         sa.a = a_vals;
         sa.b = b;

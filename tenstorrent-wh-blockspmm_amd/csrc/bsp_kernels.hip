@@ -19,8 +19,90 @@
 #include <cstdlib>
 
 #include "bsp_kernels.hpp"
+#ifdef BSP_TIMELINE
+#include "bsparse_timeline.h"
+#endif
 
 namespace bsp {
+
+// ---------------------------------------------------------------------------
+// Per-workgroup timeline (the instrumented build, BSP_TIMELINE; the slots are
+// listed in bsparse_timeline.h).  Lane 0 of wave 0 writes the wall clock
+// into a 64-word LDS log; when wave 0 ends, its lanes copy the log to the
+// attached buffer.  The log stays in LDS while the kernel runs so that no
+// stamp adds a global store, which would sit in the vector-memory queue of a
+// wave whose ring waits count its loads.
+#ifdef BSP_TIMELINE
+__device__ uint64_t* g_timeline_buf = nullptr;
+__device__ int64_t g_timeline_cap = 0;
+
+// The LDS log (allocated only in the kernels that use it).
+__device__ __forceinline__ uint64_t* timeline_lds() {
+    __shared__ uint64_t log[BSP_TIMELINE_SLOTS];
+    return log;
+}
+
+struct TimelineLog {
+    uint64_t* log;
+    __device__ __forceinline__ TimelineLog() : log(timeline_lds()) {
+        if (threadIdx.x < BSP_TIMELINE_SLOTS) log[threadIdx.x] = 0;
+        mark(0);
+    }
+    __device__ __forceinline__ void mark(int i) {
+        if (threadIdx.x == 0 && i >= 0 && i < BSP_TIMELINE_SLOTS) log[i] = wall_clock64();
+    }
+    // Wave 0 only (its lanes copy the log; other waves never call it).
+    __device__ __forceinline__ void flush() {
+        mark(BSP_TIMELINE_SLOTS - 1);
+        uint64_t* buf = g_timeline_buf;
+        if (threadIdx.x < BSP_TIMELINE_SLOTS && buf && (int64_t)blockIdx.x < g_timeline_cap)
+            buf[(int64_t)blockIdx.x * BSP_TIMELINE_SLOTS + threadIdx.x] = log[threadIdx.x];
+    }
+};
+// The same with slots 0, 1, 2 and 63 held in registers, for a kernel whose
+// LDS is sized to an exact occupancy (the one-shot SDDMM: two workgroups of
+// 80 KB per compute unit, which a 512-byte log would halve).
+struct TimelineRegs {
+    uint64_t t0 = 0, t1 = 0, t2 = 0;  // (scalars: a lane-indexed array would go to scratch)
+    __device__ __forceinline__ TimelineRegs() { t0 = wall_clock64(); }
+    __device__ __forceinline__ void mark(int i) {
+        if (i == 1) t1 = wall_clock64();
+        if (i == 2) t2 = wall_clock64();
+    }
+    __device__ __forceinline__ void flush() {
+        const uint64_t end = wall_clock64();
+        uint64_t* buf = g_timeline_buf;
+        const int l = threadIdx.x;
+        const uint64_t v = l == 0 ? t0 : l == 1 ? t1 : l == 2 ? t2 : l == BSP_TIMELINE_SLOTS - 1 ? end : 0;
+        if (l < BSP_TIMELINE_SLOTS && buf && (int64_t)blockIdx.x < g_timeline_cap)
+            buf[(int64_t)blockIdx.x * BSP_TIMELINE_SLOTS + l] = v;
+    }
+};
+// No log (kernels with no LDS to spare whose stamps sit in lambdas: the
+// two-pipeline persistent variants, which no plan takes by default).
+struct TimelineNone {
+    __device__ __forceinline__ void mark(int) {}
+    __device__ __forceinline__ void flush() {}
+};
+template <bool LDS_LOG>
+struct TimelinePick {
+    using type = TimelineNone;
+};
+template <>
+struct TimelinePick<true> {
+    using type = TimelineLog;
+};
+// LDS_LOG: the kernel has 512 bytes of LDS to spare.
+#define BSP_TL_DECL(LDS_LOG) typename TimelinePick<(LDS_LOG)>::type bsp_tl
+#define BSP_TL_DECL_REGS() TimelineRegs bsp_tl
+#define BSP_TL_MARK(i) bsp_tl.mark(i)
+#define BSP_TL_FLUSH() bsp_tl.flush()
+#else
+#define BSP_TL_DECL(LDS_LOG) ((void)0)
+#define BSP_TL_DECL_REGS() ((void)0)
+#define BSP_TL_MARK(i) ((void)0)
+#define BSP_TL_FLUSH() ((void)0)
+#endif
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -197,16 +279,29 @@ __device__ __forceinline__ void wait_vmcnt() {
     __asm__ volatile("" ::: "memory");
 }
 
-// Waits until at most PER*n vector loads of this wave are outstanding, n <= NMAX.
-template <int PER, int NMAX>
+// Waits until at most PER*n + EXTRA vector loads of this wave are
+// outstanding, n <= NMAX.
+template <int PER, int NMAX, int EXTRA = 0>
 __device__ __forceinline__ void wait_stages(int n) {
     if constexpr (NMAX >= 0) {
         if (n >= NMAX) {
-            wait_vmcnt<PER * NMAX>();
+            wait_vmcnt<PER * NMAX + EXTRA>();
             return;
         }
-        wait_stages<PER, NMAX - 1>(n);
+        wait_stages<PER, NMAX - 1, EXTRA>(n);
     }
+}
+
+// A pointer the compiler may hold in VGPRs made wave-uniform (SGPRs), for the
+// saddr operand of gl_lds16_s / gl_lds4_s, which must be an SGPR pair.  Only
+// for pointers that are uniform by construction (derived from plan words or
+// kernel arguments), where the compiler's divergence analysis loses that.
+template <typename T>
+__device__ __forceinline__ const T* uniform_ptr(const T* ptr) {
+    const uint64_t v = (uint64_t)(uintptr_t)ptr;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (const T*)(uintptr_t)(((uint64_t)hi << 32) | lo);
 }
 
 __device__ __forceinline__ u32x4 ld_tr_b16(const uint8_t* lds) {
@@ -1101,6 +1196,7 @@ __global__ __launch_bounds__(64 * (4 * SR + 1 + NBW) * PIPES) void spmm_stream_k
     constexpr int XCHG = PIPES > 1 ? 4 * NTW * 16 * 64 * 4 : 0;  // fp32 tile of the shared unit
     static_assert(PIPES == 1 || PIPES == 2, "pipelines");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[PIPES * PIPE_LDS + XCHG];
+    BSP_TL_DECL(PIPES * PIPE_LDS + XCHG + 8 * 64 <= 163840);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1244,6 +1340,7 @@ __global__ __launch_bounds__(64 * (4 * SR + 1 + NBW) * PIPES) void spmm_stream_k
     // Ends unit `cur`: store it, or (two pipelines) leave it in the exchange
     // buffer, or hold it for the exchange.
     auto finish_cur = [&] {
+        BSP_TL_MARK(2 + min(u, 60));
         if (PIPES > 1 && cur.aux == 1) {
 #pragma unroll
             for (int nt = 0; nt < NTW; ++nt)
@@ -1315,6 +1412,7 @@ __global__ __launch_bounds__(64 * (4 * SR + 1 + NBW) * PIPES) void spmm_stream_k
         Pair pa, pb;
         if (n > 0) {
             barrier_no_fence();  // step 0
+            BSP_TL_MARK(1);
             read(0, pa.e0);
             if (1 < n) read(1, pa.e1);
             lds_done();
@@ -1344,12 +1442,14 @@ __global__ __launch_bounds__(64 * (4 * SR + 1 + NBW) * PIPES) void spmm_stream_k
             multiply(pa.e0);  // entries k-2 and, if it exists, k-1
             if (k - 1 < n) multiply(pa.e1);
         }
+        if (wave_id == 0) BSP_TL_FLUSH();
         return;
     }
     Operands o0, o1;
     int k = 0;
     if (n > 0) {
         barrier_no_fence();  // X_0
+        BSP_TL_MARK(1);
         read(0, o0);
         lds_done();
         k = 1;
@@ -1391,6 +1491,346 @@ __global__ __launch_bounds__(64 * (4 * SR + 1 + NBW) * PIPES) void spmm_stream_k
             store_unit(held);
         }
     }
+    if (wave_id == 0) BSP_TL_FLUSH();
+}
+
+// ---------------------------------------------------------------------------
+// Sweep SpMM: one workgroup per compute unit holds the accumulators of every
+// unit of a sweep (up to 16 units of one 32-row stripe x 128 columns) and
+// streams their entries merged in ascending first row of B, so that all
+// workgroups of an XCD walk K together: a 32-row slice of B is fetched from
+// HBM by the first unit that needs it and served from the XCD's L2 to the
+// others shortly after, where a unit-by-unit walk spreads a slice's uses over
+// the whole launch and the A and C streams evict it in between.  Every L2
+// miss, whether the Infinity Cache or HBM serves it, costs the same on
+// MI355X (an L2-missing stream of a 64-256 MB region runs at 7.5 TB/s, one of
+// 1 GB at 7.4), so the misses are what the launch pays for.
+//   - 8 waves, two groups of four; group g owns slots 8g .. 8g+7, and wave
+//     4g + w owns columns 32w .. 32w+31 of each of them: 8 x 16 fp32
+//     accumulator registers per lane for the group's units;
+//   - every wave also loads: 1 KB of each entry's 8 KB B slice (the B slice
+//     layout of BSlice) and 256 bytes of its 2 KB A sub-block (the row layout
+//     of a_row_load_offset), into a ring of S stages of 10 KB;
+//   - step k (k = 0, 2, 4, ...) has one barrier: each wave waits for its own
+//     loads of entries k and k+1, passes the barrier, refills the stages of
+//     entries k-2 and k-1 with entries k+S-2 and k+S-1, then reads the
+//     operands of entries k and k+1 and multiplies them (only the four waves
+//     of each entry's group).  The operands are not double-buffered: the 128
+//     accumulator registers leave no room for a second set, and the launch is
+//     bound by its L2 misses, not by the LDS read latency this exposes;
+//   - when the last entry of a sweep is multiplied, each wave stores its
+//     columns of the sweep's units and clears its accumulators.
+// The entry's slot rides in its B word (bits 56-59, bit 60 marking the skip
+// entry that pads a sweep to an even count: loaded, never multiplied); each
+// wave keeps the slots of the entries in flight in a 64-bit shift register,
+// four bits each, pushed at issue and read S-1 and S-2 issues later.
+template <int S, bool OUT_BF16, bool AX4>
+__global__ __launch_bounds__(512, 1) void spmm_sweep_kernel(SpmmSweepArgs p) {
+    using namespace spmm_detail;
+    static_assert(S % 2 == 0 && S >= 6 && S <= 16, "two entries per step: an even ring of 6 to 16 stages");
+    static_assert(2 * (S - 2) + 2 < 64, "vmcnt budget");
+    constexpr int TN = kSweepTile;
+    using Loader = BSliceLoader<TN, 8>;  // one 1 KB piece per wave
+    constexpr int B_BYTES = Loader::BYTES;
+    constexpr int A_RING = S * kA_BYTES;
+    constexpr int WORDS = A_RING + S * B_BYTES;  // per wave: two word chunks
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[WORDS + 8 * 2 * kSweepWordChunk];
+    BSP_TL_DECL(true);
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const SpmmSweepHead* head = p.heads + blockIdx.x;
+    const SpmmSweepWg wg = load_const(&head->wg);
+    const int n = wg.n;
+    const uint32_t lds0 = lds_address(smem);
+
+    // ---- loads: B piece `wave` and A bytes 256*wave .. 256*wave+255 of the
+    // stage (row r = x / 64 of the row layout, slot (x % 64) / 16 holding
+    // chunk slot ^ ((r >> 2) & 3)).
+    const Loader ld(wave, lane, p.ldb);
+    uint32_t a_voff;
+    if constexpr (AX4) {
+        // Waves 0 and 1 load rows 16w .. 16w+15 of the A sub-block (1 KB each,
+        // a_row_load_offset): two loads per entry for them, one for the
+        // others (their waits count accordingly).
+        a_voff = wave < 2 ? (uint32_t)(2 * a_row_load_offset(wave, lane, p.lda)) : 0u;
+    } else {
+        const int x = 256 * wave + 4 * lane;
+        const int r = x >> 6, c = ((x & 63) >> 4) ^ ((r >> 2) & 3);
+        a_voff = (uint32_t)(2 * (r * p.lda + 8 * c) + (x & 15));
+    }
+    auto issue = [&](int e, int64_t bwd, uint32_t awd) __attribute__((always_inline)) {
+        const uint32_t st = (uint32_t)(e % S);
+        const uint16_t* bpan = uniform_ptr(p.b + (int64_t)(uint32_t)bwd * p.ldb + (int32_t)((bwd >> 32) & 0xffffff));
+        gl_lds16_s(ld.voff[0], bpan, lds0 + A_RING + st * B_BYTES + wave * 1024);
+        if constexpr (AX4) {
+            if (wave < 2)
+                gl_lds16_s(a_voff, uniform_ptr(p.a + (int64_t)awd * 32), lds0 + st * kA_BYTES + wave * 1024);
+        } else {
+            gl_lds4_s(a_voff, uniform_ptr(p.a + (int64_t)awd * 32), lds0 + st * kA_BYTES + wave * 256);
+        }
+    };
+    // ---- products.
+    const int l32 = lane & 31, q = lane >> 5;
+    const int group = wave >> 2, wc = wave & 3;
+    const BReads<TN, 1> brd(lane, wc * 32, false);
+    const int a_rd0 = a_row_read_offset(l32, q, 0);
+    const int a_rd1 = a_row_read_offset(l32, q, 1);
+    // (The lambdas are forced inline: one left out of line would take acc by
+    // address and move it to scratch memory.)
+    f32x16 acc[8];
+    auto zero_acc = [&] () __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[j][v] = 0.0f;
+    };
+    zero_acc();
+    const SpmmSweepRec* sweeps = p.sweeps + wg.s_begin;
+    int sw = 0, left = 0;
+    auto store_sweep = [&](int si) __attribute__((always_inline)) {
+        // Wait states between the last product (asm, unseen by the
+        // compiler's hazard checks) and the reads of its result: more than a
+        // 16-pass product's 18.
+        __asm__ volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+        const SpmmSweepHalf h = load_const(&sweeps[si].half[group]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (h.row[j] < 0) continue;
+            const int64_t row0 = (int64_t)h.row[j] * 32;
+            const int64_t col = h.n0[j] + wc * 32 + l32;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int64_t row = row0 + 8 * (v >> 2) + 4 * q + (v & 3);
+                if (OUT_BF16)
+                    store_out(&((uint16_t*)p.c)[row * p.ldc + col], f32_to_bf16_rne(acc[j][v]));
+                else
+                    store_out(&((float*)p.c)[row * p.ldc + col], acc[j][v]);
+            }
+        }
+    };
+    // Moves to the next sweep with entries, storing the zero tiles of sweeps
+    // without any on the way.
+    auto open = [&] () __attribute__((always_inline)) {
+        while (sw < wg.n_sweeps) {
+            const int cnt = load_const(&sweeps[sw].count);
+            if (cnt > 0) {
+                left = cnt;
+                return;
+            }
+            store_sweep(sw);
+            ++sw;
+        }
+        left = 0;
+    };
+    open();
+
+    struct Ops {
+        u32x4 a[2];
+        u32x4 b[2][1];
+        int slot;  // accumulator of this wave (0-7), or -1: another group's entry or a skip entry
+    };
+    auto read = [&](int k, uint32_t code, Ops& o) __attribute__((always_inline)) {
+        o.slot = (code & 16u) == 0 && (int)((code >> 3) & 1u) == group ? (int)(code & 7u) : -1;
+        if (o.slot >= 0) {
+            const uint8_t* as = smem + (k % S) * kA_BYTES;
+            o.a[0] = *(const u32x4*)(as + a_rd0);
+            o.a[1] = *(const u32x4*)(as + a_rd1);
+            brd.read(smem + A_RING + (k % S) * B_BYTES, o.b);
+        }
+    };
+    // The products of one entry on the accumulator of its slot, as a single
+    // asm block that holds the dispatch (compare and branch on the slot) and
+    // takes all eight accumulators as in-out operands.  Any dispatch the
+    // compiler sees -- a switch, or a chain of ifs, on builtin or asm
+    // products -- leaves it a join where each accumulator is either updated
+    // or not, and it resolves those joins by copying accumulators between two
+    // register sets: hundreds of v_mov per step, which set the kernel's pace.
+    // Here every acc[j] keeps one register, updated in place (the accumulate
+    // form: destination = source C).  The compiler's hazard checks do not see
+    // into the block: the products need two wait states after a vector ALU
+    // write of source C (the zeroing after a sweep: s_nop 1 at the block's
+    // start), none between products on one accumulator (source C exactly
+    // overlapping the previous destination), and the stores that read the
+    // results are preceded by explicit wait states (store_sweep).
+    auto multiply = [&](const Ops& o) __attribute__((always_inline)) {
+        const int slot = __builtin_amdgcn_readfirstlane(o.slot);
+        __asm__ volatile(
+            "s_nop 1\n\t"
+            "s_cmp_eq_u32 %12, 0\n\ts_cbranch_scc1 .Lsw0_%=\n\t"
+            "s_cmp_eq_u32 %12, 1\n\ts_cbranch_scc1 .Lsw1_%=\n\t"
+            "s_cmp_eq_u32 %12, 2\n\ts_cbranch_scc1 .Lsw2_%=\n\t"
+            "s_cmp_eq_u32 %12, 3\n\ts_cbranch_scc1 .Lsw3_%=\n\t"
+            "s_cmp_eq_u32 %12, 4\n\ts_cbranch_scc1 .Lsw4_%=\n\t"
+            "s_cmp_eq_u32 %12, 5\n\ts_cbranch_scc1 .Lsw5_%=\n\t"
+            "s_cmp_eq_u32 %12, 6\n\ts_cbranch_scc1 .Lsw6_%=\n\t"
+            "s_cmp_eq_u32 %12, 7\n\ts_cbranch_scc1 .Lsw7_%=\n\t"
+            "s_branch .Lswd_%=\n"
+#define BSP_SWEEP_CASE(J)                                              \
+            ".Lsw" #J "_%=:\n\t"                                      \
+            "v_mfma_f32_32x32x16_bf16 %" #J ", %8, %10, %" #J "\n\t"   \
+            "v_mfma_f32_32x32x16_bf16 %" #J ", %9, %11, %" #J "\n\t"   \
+            "s_branch .Lswd_%=\n"
+            BSP_SWEEP_CASE(0) BSP_SWEEP_CASE(1) BSP_SWEEP_CASE(2) BSP_SWEEP_CASE(3)
+            BSP_SWEEP_CASE(4) BSP_SWEEP_CASE(5) BSP_SWEEP_CASE(6) BSP_SWEEP_CASE(7)
+#undef BSP_SWEEP_CASE
+            ".Lswd_%=:"
+            : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), "+v"(acc[4]), "+v"(acc[5]),
+              "+v"(acc[6]), "+v"(acc[7])
+            : "v"(o.a[0]), "v"(o.a[1]), "v"(o.b[0][0]), "v"(o.b[1][0]), "s"(slot)
+            : "scc");
+    };
+    auto fence_sched = [] { __builtin_amdgcn_sched_barrier(0); };
+
+    // ---- the ring.  Entry words reach each wave through its own LDS copy,
+    // loaded by DMA 64 entries (a chunk) at a time into two buffers: the
+    // next chunk is fetched when the issue position enters a chunk, and the
+    // words of a step's refills are read from LDS one step earlier.  No
+    // scalar load is in flight while the ring runs: every wave reads LDS in
+    // every step, and the wait for those reads (s_waitcnt lgkmcnt) would also
+    // wait for a scalar load, putting a memory round trip on every refill of
+    // a scalar word chunk (the reason the loader waves of spmm_stream_kernel
+    // read no LDS).  A chunk's two loads, issued at step kc after the step's
+    // refills, are younger than the entries steps kc+2 .. kc+S-2 wait for, so
+    // those waits allow two more loads in flight.  The first S entries' words
+    // come from the head.  Every sweep has an even number of entries (the plan
+    // pads an odd one with a skip entry), so n is even and a step's two
+    // entries belong to one sweep.
+    const uint32_t wbuf = lds0 + WORDS + wave * 2 * kSweepWordChunk;
+    auto fetch_chunk = [&](int c) __attribute__((always_inline)) {
+        // B words (512 bytes: lanes 0-31, 16 each) at +0, A words (256 bytes)
+        // at +512 of buffer c & 1.  In bounds: a chunk is fetched only if it
+        // holds entries of this stream, and the arrays are padded by 64 words.
+        const uint32_t dst = wbuf + (uint32_t)(c & 1) * kSweepWordChunk;
+        const int64_t* bsrc = uniform_ptr(p.bw + wg.w_begin + 64 * c);
+        const uint32_t* asrc = uniform_ptr(p.aw + wg.w_begin + 64 * c);
+        if (lane < 32) gl_lds16_s((uint32_t)lane * 16, bsrc, dst);
+        gl_lds4_s((uint32_t)lane * 4, asrc, dst + 512);
+    };
+    // Words of entry e, from its chunk's buffer.
+    auto words_at = [&](int e, int64_t& bwd, uint32_t& awd) __attribute__((always_inline)) {
+        const uint8_t* buf = smem + (WORDS + wave * 2 * kSweepWordChunk) + ((e >> 6) & 1) * kSweepWordChunk;
+        const uint64_t b64 = *(const uint64_t*)(buf + 8 * (e & 63));
+        const uint32_t a32 = *(const uint32_t*)(buf + 512 + 4 * (e & 63));
+        bwd = (int64_t)(((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(b64 >> 32)) << 32) |
+                        __builtin_amdgcn_readfirstlane((uint32_t)b64));
+        awd = __builtin_amdgcn_readfirstlane(a32);
+    };
+    // The entries in flight: their slots (4 bits each, the last issued in
+    // bits 0-3) and skip flags (the last issued in bit 0).
+    uint64_t slots = 0;
+    uint32_t skips = 0;
+    auto push = [&](bool live, int64_t bwd) __attribute__((always_inline)) {
+        const uint64_t code = (uint64_t)bwd >> kSweepSlotShift;
+        slots = (slots << 4) | (live ? code & 15u : 0u);
+        skips = (skips << 1) | (live ? (uint32_t)(code >> 4) & 1u : 1u);
+    };
+    // Slot and skip flag of the entry issued `age` issues ago, as read()'s code.
+    auto code_at = [&](int age) __attribute__((always_inline)) {
+        return (uint32_t)((slots >> (4 * age)) & 15u) | (((skips >> age) & 1u) << 4);
+    };
+    // Chunks 0 and 1 first: older than every entry load, so the first wait
+    // covers them.
+    if (n > 0) fetch_chunk(0);
+    if (n > 64) fetch_chunk(1);
+    {
+        const int64_t* hb = head->bw;
+        const uint32_t* ha = head->aw;
+        struct W8B {
+            int64_t w[8];
+        };
+        struct W8A {
+            uint32_t w[8];
+        };
+        const W8B b0 = load_const((const W8B*)hb), b1 = load_const((const W8B*)hb + 1);
+        const W8A a0 = load_const((const W8A*)ha), a1 = load_const((const W8A*)ha + 1);
+#pragma unroll
+        for (int e = 0; e < S; ++e) {
+            const int64_t bwd = e < 8 ? b0.w[e] : b1.w[e - 8];
+            const uint32_t awd = e < 8 ? a0.w[e] : a1.w[e - 8];
+            if (e < n) issue(e, bwd, awd);
+            push(e < n, bwd);
+        }
+    }
+    // After the issues of step k the entries k .. k+S-1 are the last S issued:
+    // entry k is S-1 issues old, entry k+1 S-2.  The words of the next step's
+    // refills (entries k+S, k+S+1) are read with the operands.
+    int64_t nb0 = 0, nb1 = 0;
+    uint32_t na0 = 0, na1 = 0;
+    auto run_pair = [&](int k) __attribute__((always_inline)) {
+        Ops o0, o1;
+        if (k + S < n) words_at(k + S, nb0, na0);
+        if (k + S + 1 < n) words_at(k + S + 1, nb1, na1);
+        read(k, code_at(S - 1), o0);
+        read(k + 1, code_at(S - 2), o1);
+        fence_sched();
+        multiply(o0);
+        multiply(o1);
+        fence_sched();
+        left -= 2;
+        if (left == 0) {
+            store_sweep(sw);
+            zero_acc();
+            ++sw;
+            open();
+        }
+    };
+    // Loads per entry of this wave: 2 (B piece and A piece; with AX4 only
+    // waves 0 and 1 load A), else 1.
+    const bool two = !AX4 || wave < 2;
+    if (n > 0) {
+        if (two)
+            wait_stages<2, S - 2>(max(0, min(S, n) - 2));  // entries 0 and 1 (and chunks 0, 1) landed
+        else
+            wait_stages<1, S - 2>(max(0, min(S, n) - 2));
+        barrier_no_fence();
+        BSP_TL_MARK(1);
+        run_pair(0);
+    }
+    int kc = -2 * S;  // step of the last chunk fetch
+    for (int k = 2; k < n; k += 2) {
+        const int e = k + S - 2;
+        const bool chunk_young = k - kc <= S - 2;
+        if (e + 1 < n) {
+            if (two) {
+                if (chunk_young)
+                    wait_vmcnt<2 * (S - 4) + 2>();  // entries k, k+1 landed
+                else
+                    wait_vmcnt<2 * (S - 4)>();
+            } else {
+                if (chunk_young)
+                    wait_vmcnt<(S - 4) + 2>();
+                else
+                    wait_vmcnt<S - 4>();
+            }
+            barrier_no_fence();
+            issue(e, nb0, na0);
+            issue(e + 1, nb1, na1);
+            if ((e & 63) == 0 && e + 64 < n) {  // entering chunk e/64: fetch the next
+                fetch_chunk((e >> 6) + 1);
+                kc = k;
+            }
+        } else {
+            const int m = max(0, min(n, e) - (k + 2));
+            if (two) {
+                if (chunk_young)
+                    wait_stages<2, S - 4, 2>(m);
+                else
+                    wait_stages<2, S - 4>(m);
+            } else {
+                if (chunk_young)
+                    wait_stages<1, S - 4, 2>(m);
+                else
+                    wait_stages<1, S - 4>(m);
+            }
+            barrier_no_fence();
+        }
+        push(e < n, nb0);
+        push(e + 1 < n, nb1);
+        run_pair(k);
+        if ((k & 7) == 0 && k < 8 * 60) BSP_TL_MARK(2 + (k >> 3));
+    }
+    if (wave == 0) BSP_TL_FLUSH();
 }
 
 // ---------------------------------------------------------------------------
@@ -1824,6 +2264,7 @@ __global__ __launch_bounds__(256, 2) void sddmm_shot_kernel(SddmmArgs p) {
     using namespace spmm_detail;
     using L = sddmm_shot::Layout<K>;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[L::LDS];
+    BSP_TL_DECL_REGS();
     const SddmmItem it = load_const(p.wgs + blockIdx.x);
     if (it.e_end <= it.e_begin) return;  // idle workgroup (uniform)
     const int lane = threadIdx.x & 63;
@@ -1889,6 +2330,7 @@ __global__ __launch_bounds__(256, 2) void sddmm_shot_kernel(SddmmArgs p) {
     }
     wait_vmcnt<0>();
     barrier_no_fence();
+    BSP_TL_MARK(1);
     if (!has) return;
 
     const uint8_t* xs = smem;
@@ -1919,6 +2361,7 @@ __global__ __launch_bounds__(256, 2) void sddmm_shot_kernel(SddmmArgs p) {
             }
             acc = mfma32(a, b, acc);
         }
+    BSP_TL_MARK(2);
     if constexpr (MASK16) {
         // The products have consumed this wave's Y panel: stage the mask
         // sub-block there (row-major, 64-byte rows) and read back rows
@@ -1946,6 +2389,7 @@ __global__ __launch_bounds__(256, 2) void sddmm_shot_kernel(SddmmArgs p) {
         else
             store_out(&((float*)p.out)[idx], val);
     }
+    if (wave == 0) BSP_TL_FLUSH();
 }
 
 // ---------------------------------------------------------------------------
@@ -2196,6 +2640,18 @@ hipError_t launch_spmm_stream(const SpmmStreamArgs& a, const SpmmStreamVariant& 
     return hipErrorInvalidValue;
 }
 
+hipError_t launch_spmm_sweep(const SpmmSweepArgs& a, bool out_bf16, bool ax4, int grid, hipStream_t stream) {
+    if (grid <= 0) return hipSuccess;
+#define BSP_SWEEP_LAUNCH(OB, AX)                                                                                   \
+    hipLaunchKernelGGL((spmm_sweep_kernel<kSweepStages, OB, AX>), dim3(grid), dim3(64 * kSweepWaves), 0, stream, a)
+    if (out_bf16 && ax4) BSP_SWEEP_LAUNCH(true, true);
+    else if (out_bf16) BSP_SWEEP_LAUNCH(true, false);
+    else if (ax4) BSP_SWEEP_LAUNCH(false, true);
+    else BSP_SWEEP_LAUNCH(false, false);
+#undef BSP_SWEEP_LAUNCH
+    return hipGetLastError();
+}
+
 template <int DK>
 static void launch_attention_t(const AttentionArgs& a, bool out_bf16, int grid, int n_split, hipStream_t stream) {
     if (out_bf16)
@@ -2301,3 +2757,23 @@ hipError_t launch_spgemm(const SpgemmArgs& a, int stages, bool out_bf16, int gri
 }
 
 }  // namespace bsp
+
+#ifdef BSP_TIMELINE
+extern "C" int bsp_timeline_attach(void* buffer, int64_t capacity, int device) {
+    if (capacity < 0 || (buffer == nullptr) != (capacity == 0)) return BSP_ERR_INVALID_ARGUMENT;
+    int prev = -1;
+    hipError_t e = hipGetDevice(&prev);
+    if (e == hipSuccess && prev != device) e = hipSetDevice(device);
+    uint64_t* ptr = (uint64_t*)buffer;
+    if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(bsp::g_timeline_buf), &ptr, sizeof(ptr));
+    if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(bsp::g_timeline_cap), &capacity, sizeof(capacity));
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (prev >= 0 && prev != device) (void)hipSetDevice(prev);
+    return e == hipSuccess ? BSP_OK : BSP_ERR_DEVICE;
+}
+
+extern "C" int bsp_timeline_clock_khz(int device, int* khz) {
+    if (!khz) return BSP_ERR_INVALID_ARGUMENT;
+    return hipDeviceGetAttribute(khz, hipDeviceAttributeWallClockRate, device) == hipSuccess ? BSP_OK : BSP_ERR_DEVICE;
+}
+#endif

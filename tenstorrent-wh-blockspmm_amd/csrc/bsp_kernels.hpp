@@ -43,6 +43,38 @@ struct SpmmStreamArgs {
     int32_t N;
 };
 
+// Sweep SpMM (spmm_sweep_kernel): one workgroup per compute unit holds a
+// sweep's units (up to 16) and streams their entries merged by first row of B.
+struct SpmmSweepArgs {
+    const uint16_t* a;             // A block values (bf16)
+    const uint16_t* b;             // B (bf16), row-major K x N, leading dim ldb
+    void* c;                       // C (fp32 or bf16), row-major M x N, leading dim ldc
+    const SpmmSweepHead* heads;    // one per workgroup
+    const SpmmSweepRec* sweeps;    // sweep records (padded)
+    const int64_t* bw;             // per entry: first row of B | first column << 32 | slot << 56 (padded)
+    const uint32_t* aw;            // per entry: A sub-block offset / 32 (padded)
+    int64_t ldb;
+    int64_t ldc;
+    int32_t lda;                   // row stride inside an A block (= C)
+    int32_t N;
+};
+
+// Ring stages of the sweep kernel: 14 stages of 10 KB (2 KB of A, 8 KB of
+// B), and per wave two 768-byte chunks of entry words (64 B words and 64 A
+// words each): 152 KB of a compute unit's 160 KB of LDS.
+constexpr int kSweepStages = 14;
+constexpr int kSweepWordChunk = 768;
+constexpr int kSweepWaves = 8;
+
+hipError_t launch_spmm_sweep(const SpmmSweepArgs& a, bool out_bf16, bool ax4, int grid, hipStream_t stream);
+
+// Whether an SpMM plan takes the sweep kernel: 32x32-multiple blocks, N a
+// multiple of 128, at least 8 units (stripe x 128 columns) per compute unit
+// and a B of at least 8 MB (below that the whole of B stays in the L2s and
+// the persistent kernel's two workgroups per compute unit do better).
+// BSP_SPMM_SWEEP=0 turns it off, 2 takes it whenever the shape allows.
+bool choose_spmm_sweep(const bsp_bsr_desc* a, int64_t N, int cus);
+
 // Compiled persistent SpMM variants: tile width, B ring depth, A ring depth,
 // B loader waves, pipelines per workgroup, entries per ring step, stripes per
 // unit.  A pipeline has 4 MFMA waves (each 32*tile/128 columns), the B loader

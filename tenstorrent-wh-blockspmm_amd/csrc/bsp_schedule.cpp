@@ -12,6 +12,7 @@
 #include "bsp_schedule.hpp"
 
 #include <algorithm>
+#include <cmath>
 #include <cstdlib>
 #include <numeric>
 #include <queue>
@@ -27,6 +28,16 @@ int64_t env_int(const char* name, int64_t dflt) {
     long long x = std::strtoll(v, &end, 10);
     return (end && *end == 0) ? (int64_t)x : dflt;
 }
+
+// Load balancing of the SpMM schedules (BSP_SPMM_BALANCE, read when a
+// schedule is built): 1 (default) = the nnz-cost split of long rows and the
+// longest-first placement; 0 = neither: rows whole and work in its natural
+// order, in contiguous ranges -- the counterpart of the reference's operators
+// without load balancing (bsr_spmm_multicore_load_balanced_new_DM_no_lb and
+// its SnF / CDA siblings, block_spmm/inc/host_code.hpp:113-124, :158-161,
+// which deal contiguous row ranges to cores,
+// bsr_spmm_multicore_load_balanced_new_DM.cpp:339-344).
+bool load_balance() { return env_int("BSP_SPMM_BALANCE", 1) != 0; }
 
 }  // namespace
 
@@ -278,6 +289,7 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
     const int64_t mean = nonempty ? (gtotal + nonempty - 1) / nonempty : 0;
     const int64_t fair = (gtotal * s.n_tiles + num_cus - 1) / num_cus;
     int64_t L = std::max<int64_t>({32, 2 * mean, fair});
+    if (!load_balance()) L = INT32_MAX;  // rows whole
     L = env_int("BSP_SPMM_SPLIT", L);
     if (L < 1) L = 1;
     if (a->C % 64 == 0 && L < 2) L = 2;  // pieces hold whole entry pairs (below)
@@ -354,6 +366,12 @@ int build_spmm_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSched
     // entries each (at about one entry per row the store dominates and the
     // plain longest-first order measured faster).
     const int pair_cus = (int)env_int("BSP_SPMM_PAIR_CUS", mean >= 4 ? num_cus / kNumXcd : 0);
+    if (!load_balance()) {
+        // Natural order: workgroup g takes item g / n_tiles, tile g % n_tiles.
+        s.wgmap.resize(s.items.size() * (size_t)s.n_tiles);
+        std::iota(s.wgmap.begin(), s.wgmap.end(), 0);
+        return BSP_OK;
+    }
     s.wgmap = xcd_tile_map(cost, s.n_tiles, (int)cg, pair_cus, false);
     // Rows in contiguous bands per XCD instead (a banded structure, whose
     // nearby rows read nearby rows of B): kept when the busiest XCD then
@@ -521,7 +539,12 @@ int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n,
     const bool rotate = pipes == 1 && env_int("BSP_SPMM_ROTATE", 1) != 0;
     s.rotated = rotate ? 1 : 0;
 
-    // Stripe entry counts; a unit costs its entries plus the store.
+    // Stripe entry counts; a unit costs its entries plus the store.  (A
+    // cost fitted to per-unit times measured on the skewed workload,
+    // 0.1114 c + 0.3324 sqrt(c) us, which long units' faster streaming
+    // suggested, measured 0.5-1.5 us slower there: the spread of the
+    // workgroups' busy times comes from the memory system more than from
+    // the units' sizes.)
     constexpr int64_t kStoreCost = 2;
     // A pair's entries: the union of its two block rows' columns, merged in
     // column order (each row's own blocks keep their CSR order); emit(col,
@@ -551,13 +574,16 @@ int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n,
             cnt[sr] = (int64_t)(a->indptr[i + 1] - a->indptr[i]) * CS;
         }
     }
-    // Stripes onto row groups, longest first onto the least-loaded group.
+    // Stripes onto row groups, longest first onto the least-loaded group
+    // (without load balancing: contiguous ranges in stripe order).
+    const bool balance = load_balance();
     std::vector<int32_t> order(nsr);
     std::iota(order.begin(), order.end(), 0);
-    std::stable_sort(order.begin(), order.end(), [&](int32_t x, int32_t y) { return cnt[x] > cnt[y]; });
+    if (balance)
+        std::stable_sort(order.begin(), order.end(), [&](int32_t x, int32_t y) { return cnt[x] > cnt[y]; });
     std::vector<std::vector<int32_t>> rows(rg_count);
     using Load = std::pair<int64_t, int>;
-    {
+    if (balance) {
         std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
         for (int g = 0; g < rg_count; ++g) heap.push({0, g});
         for (int32_t sr : order) {
@@ -566,6 +592,8 @@ int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n,
             rows[l.second].push_back(sr);
             heap.push({l.first + cnt[sr] + kStoreCost, l.second});
         }
+    } else {
+        for (int64_t i = 0; i < nsr; ++i) rows[i * rg_count / nsr].push_back((int32_t)i);
     }
     // Inside each XCD: units longest first onto the least-loaded compute
     // unit, then each compute unit's units longest first onto the
@@ -577,8 +605,12 @@ int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n,
     const int cus_per_xcd = std::max(1, num_cus / kNumXcd);
     const int bins = cus_per_xcd * wg_per_cu;
     std::vector<std::vector<SpmmStreamUnit>> wg_units((size_t)bins * kNumXcd);
-    auto lpt = [](const std::vector<SpmmStreamUnit>& us, int nb, std::vector<std::vector<SpmmStreamUnit>>& out) {
+    auto lpt = [balance](const std::vector<SpmmStreamUnit>& us, int nb, std::vector<std::vector<SpmmStreamUnit>>& out) {
         out.assign(nb, {});
+        if (!balance) {  // contiguous ranges in order
+            for (size_t i = 0; i < us.size(); ++i) out[i * nb / us.size()].push_back(us[i]);
+            return;
+        }
         std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
         for (int b = 0; b < nb; ++b) heap.push({0, b});
         for (const SpmmStreamUnit& u : us) {  // longest first
@@ -725,6 +757,223 @@ int build_spmm_stream(const bsp_bsr_desc* a, int64_t N, int num_cus, int tile_n,
                 h.apw[j] = s.apw[(size_t)w.w_begin + j];
             else
                 h.aw[j] = s.aw[(size_t)w.w_begin + j];
+        }
+    }
+    return BSP_OK;
+}
+
+namespace {
+
+// Entries (32x32 sub-block products) of each 32-row stripe.
+std::vector<int64_t> stripe_entries(const bsp_bsr_desc* a) {
+    const int64_t RS = a->R / kSub, CS = a->C / kSub, nsr = a->H / kSub;
+    std::vector<int64_t> cnt(nsr);
+    for (int64_t sr = 0; sr < nsr; ++sr) {
+        const int64_t i = sr / RS;
+        cnt[sr] = (int64_t)(a->indptr[i + 1] - a->indptr[i]) * CS;
+    }
+    return cnt;
+}
+
+// Stripes onto `groups` row groups, longest first onto the least-loaded
+// (load: entries plus a store); each group's list longest first.
+std::vector<std::vector<int32_t>> stripe_row_groups(const std::vector<int64_t>& cnt, int64_t groups) {
+    constexpr int64_t kStoreCost = 2;
+    std::vector<int32_t> order(cnt.size());
+    std::iota(order.begin(), order.end(), 0);
+    std::stable_sort(order.begin(), order.end(), [&](int32_t x, int32_t y) { return cnt[x] > cnt[y]; });
+    std::vector<std::vector<int32_t>> rows(groups);
+    using Load = std::pair<int64_t, int64_t>;
+    std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
+    for (int64_t g = 0; g < groups; ++g) heap.push({0, g});
+    for (int32_t sr : order) {
+        Load l = heap.top();
+        heap.pop();
+        rows[l.second].push_back(sr);
+        heap.push({l.first + cnt[sr] + kStoreCost, l.second});
+    }
+    return rows;
+}
+
+}  // namespace
+
+int64_t spmm_sweep_read_estimate(const bsp_bsr_desc* a, int64_t N, int col_groups) {
+    if (col_groups < 1 || kNumXcd % col_groups) return INT64_MAX;
+    const std::vector<int64_t> cnt = stripe_entries(a);
+    const auto rows = stripe_row_groups(cnt, kNumXcd / col_groups);
+    const int64_t RS = a->R / kSub, nbc = a->W / a->C;
+    std::vector<int32_t> seen(nbc, -1);
+    int64_t b_bytes = 0;
+    for (size_t g = 0; g < rows.size(); ++g) {
+        int64_t distinct = 0;
+        for (int32_t sr : rows[g]) {
+            const int64_t i = sr / RS;
+            for (int64_t blk = a->indptr[i]; blk < a->indptr[i + 1]; ++blk)
+                if (seen[a->indices[blk]] != (int32_t)g) {
+                    seen[a->indices[blk]] = (int32_t)g;
+                    ++distinct;
+                }
+        }
+        b_bytes += distinct * a->C * N * 2;
+    }
+    return col_groups * a->nblocks * a->R * a->C * 2 + b_bytes;
+}
+
+int build_spmm_sweep(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSweep& s, std::string& msg,
+                     int col_groups) {
+    int st = validate_bsr(a, msg);
+    if (st != BSP_OK) return st;
+    if (a->R % kSub || a->C % kSub) {
+        msg = "R and C must be multiples of 32";
+        return BSP_ERR_UNSUPPORTED;
+    }
+    if (N <= 0 || N % kSweepTile != 0 || N >= kSweepMaxN) {
+        msg = "the sweep kernel needs N a positive multiple of 128 below 2^24";
+        return BSP_ERR_UNSUPPORTED;
+    }
+    const int64_t RS = a->R / kSub, CS = a->C / kSub, nsr = a->H / kSub;
+    if (a->nblocks * a->R * a->C / kSub > UINT32_MAX || a->nblocks * RS * CS * (N / kSweepTile) > INT32_MAX - kStreamPad ||
+        a->W > INT32_MAX) {
+        msg = "problem too large for the sweep schedule";
+        return BSP_ERR_UNSUPPORTED;
+    }
+    if (num_cus <= 0) num_cus = 256;
+    const int64_t n_tiles = N / kSweepTile;
+    int64_t cg = col_groups;
+    if (cg <= 0) {
+        int64_t best = INT64_MAX;
+        for (int64_t c = 1; c <= kNumXcd; c *= 2) {
+            if (n_tiles % c) continue;
+            const int64_t est = spmm_sweep_read_estimate(a, N, (int)c);
+            if (est < best) {
+                best = est;
+                cg = c;
+            }
+        }
+    }
+    if (cg < 1 || kNumXcd % cg || n_tiles % cg) cg = 1;
+    const std::vector<int64_t> cnt = stripe_entries(a);
+    const bool balance = load_balance();
+    std::vector<std::vector<int32_t>> rows;
+    if (balance) {
+        rows = stripe_row_groups(cnt, kNumXcd / cg);
+    } else {  // contiguous ranges in stripe order
+        rows.assign(kNumXcd / cg, {});
+        for (int64_t i = 0; i < nsr; ++i) rows[i * (kNumXcd / cg) / nsr].push_back((int32_t)i);
+    }
+    const int64_t tpg = n_tiles / cg;
+    const int cus_per_xcd = std::max(1, num_cus / kNumXcd);
+    const bool rotate = env_int("BSP_SWEEP_ROTATE", 0) != 0;
+    constexpr int64_t kStoreCost = 2;
+
+    s = SpmmSweep{};
+    s.n_tiles = (int32_t)n_tiles;
+    s.col_groups = (int32_t)cg;
+    s.rotated = rotate ? 1 : 0;
+    s.wgs.assign((size_t)cus_per_xcd * kNumXcd, SpmmSweepWg{});
+    struct Unit {
+        int32_t row, n0;
+        int64_t count;
+    };
+    struct Entry {
+        int64_t brow;
+        uint32_t aw;
+        int32_t slot;
+        int32_t n0;
+    };
+    for (int64_t r = 0; r < kNumXcd / cg; ++r)
+        for (int64_t c = 0; c < cg; ++c) {
+            const int x = (int)(r * cg + c);
+            std::vector<Unit> us;
+            for (int32_t sr : rows[r])  // longest first
+                for (int64_t t = c * tpg; t < (c + 1) * tpg; ++t) us.push_back({sr, (int32_t)(t * kSweepTile), cnt[sr]});
+            // Units onto the XCD's workgroups, longest first onto the
+            // least-loaded one that has a free slot.
+            const int64_t n_sw = std::max<int64_t>(1, ((int64_t)us.size() + (int64_t)cus_per_xcd * kSweepSlots - 1) /
+                                                          ((int64_t)cus_per_xcd * kSweepSlots));
+            const int64_t cap = n_sw * kSweepSlots;
+            std::vector<std::vector<Unit>> per(cus_per_xcd);
+            using Load = std::pair<int64_t, int>;
+            if (balance) {
+                std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
+                for (int w = 0; w < cus_per_xcd; ++w) heap.push({0, w});
+                for (const Unit& u : us) {
+                    Load l = heap.top();
+                    heap.pop();
+                    per[l.second].push_back(u);
+                    if ((int64_t)per[l.second].size() < cap) heap.push({l.first + u.count + kStoreCost, l.second});
+                }
+            } else if (!us.empty()) {  // contiguous ranges in order (at most cap each)
+                for (size_t i = 0; i < us.size(); ++i) per[i * cus_per_xcd / us.size()].push_back(us[i]);
+            }
+            // Each workgroup's units into n_sw sweeps (unit i -> sweep i % n_sw,
+            // longest first), its entries merged by first row of B.
+            const int64_t stagger = env_int("BSP_SWEEP_STAGGER", 0);
+            for (int w = 0; w < cus_per_xcd; ++w) {
+                const int64_t kcol = ((rotate ? spmm_stream_rotation_column(a->W / a->C, c, cg) : 0) + stagger * w) %
+                                     (a->W / a->C) * a->C;
+                SpmmSweepWg& rec = s.wgs[(size_t)w * kNumXcd + x];
+                rec.w_begin = (int32_t)s.bw.size();
+                rec.s_begin = (int32_t)s.sweeps.size();
+                const std::vector<Unit>& mine = per[w];
+                for (int64_t sw = 0; sw < n_sw; ++sw) {
+                    SpmmSweepRec sr{};
+                    for (int g = 0; g < 2; ++g)
+                        for (int j = 0; j < 8; ++j) {
+                            sr.half[g].row[j] = -1;
+                            sr.half[g].n0[j] = 0;
+                        }
+                    std::vector<Entry> es;
+                    int slot = 0;
+                    for (size_t ui = (size_t)sw; ui < mine.size(); ui += (size_t)n_sw, ++slot) {
+                        const Unit& u = mine[ui];
+                        sr.half[slot / 8].row[slot % 8] = u.row;
+                        sr.half[slot / 8].n0[slot % 8] = u.n0;
+                        const int64_t i = u.row / RS, sub = u.row % RS;
+                        for (int64_t blk = a->indptr[i]; blk < a->indptr[i + 1]; ++blk)
+                            for (int64_t t = 0; t < CS; ++t)
+                                es.push_back({(int64_t)a->indices[blk] * a->C + kSub * t,
+                                              (uint32_t)((blk * a->R * a->C + kSub * sub * a->C + kSub * t) / kSub),
+                                              slot, u.n0});
+                    }
+                    if (slot == 0) continue;  // no units left for this sweep
+                    std::stable_sort(es.begin(), es.end(), [](const Entry& p, const Entry& q) { return p.brow < q.brow; });
+                    size_t off = 0;
+                    if (kcol > 0) {
+                        while (off < es.size() && es[off].brow < kcol) ++off;
+                        if (off == es.size()) off = 0;
+                        std::rotate(es.begin(), es.begin() + off, es.end());
+                    }
+                    for (const Entry& e : es) {
+                        s.bw.push_back(e.brow | ((int64_t)e.n0 << 32) | ((int64_t)e.slot << kSweepSlotShift));
+                        s.aw.push_back(e.aw);
+                    }
+                    if (es.size() % 2) {  // pad to an even count
+                        s.bw.push_back(s.bw.back() | kSweepSkip);
+                        s.aw.push_back(s.aw.back());
+                    }
+                    sr.count = (int32_t)(es.size() + es.size() % 2);
+                    s.sweeps.push_back(sr);
+                    ++rec.n_sweeps;
+                }
+                rec.n = (int32_t)(s.bw.size() - rec.w_begin);
+                s.max_wg_entries = std::max(s.max_wg_entries, rec.n);
+                s.max_sweeps = std::max(s.max_sweeps, rec.n_sweeps);
+                s.n_units += (int64_t)mine.size();
+            }
+        }
+    s.n_entries = (int64_t)s.bw.size();
+    s.bw.resize(s.bw.size() + kStreamPad, 0);
+    s.aw.resize(s.aw.size() + kStreamPad, 0);
+    SpmmSweepRec zero{};
+    s.sweeps.resize(s.sweeps.size() + kStreamPad, zero);
+    s.heads.assign(s.wgs.size(), SpmmSweepHead{});
+    for (size_t g = 0; g < s.wgs.size(); ++g) {
+        SpmmSweepHead& h = s.heads[g];
+        h.wg = s.wgs[g];
+        for (int j = 0; j < kHeadWords; ++j) {
+            h.bw[j] = s.bw[(size_t)h.wg.w_begin + j];
+            h.aw[j] = s.aw[(size_t)h.wg.w_begin + j];
         }
     }
     return BSP_OK;

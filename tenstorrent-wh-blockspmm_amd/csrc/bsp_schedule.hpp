@@ -193,6 +193,85 @@ std::vector<int64_t> spmm_packed_entries(const SpmmSchedule& s);
 // stripes: stripe s of a group piece p uses slot base + s * npieces + p).
 std::vector<SpmmSplit> spmm_splits(const SpmmSchedule& s);
 
+// ---- sweep SpMM (spmm_sweep_kernel) ------------------------------------------
+// One workgroup per compute unit holds the accumulators of up to
+// kSweepSlots units (32-row stripe x 128-column tile) at once -- a sweep --
+// and streams the entries of all of them merged in ascending first row of B
+// (block column), so that every workgroup of an XCD walks K in step with the
+// others and each 32-row slice of B is read from HBM once per XCD and reused
+// from the L2 by every unit that needs it, instead of being evicted between
+// uses by the A and C streams that pass through the same L2.  Slots 8g .. 8g+7
+// belong to wave group g (waves 4g .. 4g+3, each 32 columns of the tile).
+constexpr int kSweepSlots = 16;
+constexpr int kSweepTile = 128;
+
+struct SpmmSweepWg {
+    int32_t w_begin;   // first word of this workgroup's entry stream
+    int32_t n;         // entries in the stream (all sweeps)
+    int32_t s_begin;   // first sweep record
+    int32_t n_sweeps;
+};
+static_assert(sizeof(SpmmSweepWg) == 16, "SpmmSweepWg layout is shared with the kernels");
+
+// The units of one wave group in a sweep: stripe (-1: slot unused) and first
+// output column of each of its eight slots.
+struct SpmmSweepHalf {
+    int32_t row[8];
+    int32_t n0[8];
+};
+struct SpmmSweepRec {
+    int32_t count;     // entries of the sweep (0: its units are empty stripes, stored as zeros)
+    int32_t pad[3];
+    SpmmSweepHalf half[2];
+};
+static_assert(sizeof(SpmmSweepRec) == 144, "SpmmSweepRec layout is shared with the kernels");
+
+// What a workgroup reads first: its record and the first kHeadWords words
+// of its streams (copies; the arrays keep them too).
+struct SpmmSweepHead {
+    SpmmSweepWg wg;
+    int32_t pad[12];
+    int64_t bw[kHeadWords];
+    uint32_t aw[kHeadWords];
+    uint32_t pad2[16];
+};
+static_assert(sizeof(SpmmSweepHead) == 320, "SpmmSweepHead layout is shared with the kernels");
+
+// B word of a sweep entry: first row of B (bits 0-31) | first output column
+// (bits 32-55) | slot (bits 56-59) | skip (bit 60).  Every sweep has an even
+// number of entries: an odd one is padded with a skip entry (a copy of its
+// last entry's words with the skip bit, loaded and not multiplied).
+constexpr int kSweepSlotShift = 56;
+constexpr int64_t kSweepSkip = int64_t(1) << 60;
+constexpr int64_t kSweepMaxN = int64_t(1) << 24;
+
+struct SpmmSweep {
+    int32_t n_tiles = 0;
+    int32_t col_groups = 1;      // column groups of the XCD map
+    int32_t max_sweeps = 0;      // most sweeps of any workgroup
+    int32_t max_wg_entries = 0;  // longest workgroup stream
+    int32_t rotated = 0;         // 1: each XCD's sweeps start at its column group's share of K
+    int64_t n_entries = 0;
+    int64_t n_units = 0;
+    std::vector<SpmmSweepWg> wgs;      // one per workgroup (= compute unit); workgroup g on XCD g % kNumXcd
+    std::vector<SpmmSweepHead> heads;  // one per workgroup
+    std::vector<SpmmSweepRec> sweeps;  // (+ kStreamPad zero records)
+    std::vector<int64_t> bw;           // per entry (+ pad)
+    std::vector<uint32_t> aw;          // per entry: A sub-block element offset / 32 (+ pad)
+};
+
+// Estimated HBM-side reads (bytes) of a sweep plan with col_groups column
+// groups: A read once per column group, and each row group's touched 32-row
+// slices of B read once per XCD.
+int64_t spmm_sweep_read_estimate(const bsp_bsr_desc* a, int64_t N, int col_groups);
+
+// Builds the sweep schedule for num_cus compute units (one workgroup each).
+// col_groups = 0 picks the count (1, 2, 4, 8 dividing the tile count) of
+// least estimated reads.  R and C multiples of 32, N a multiple of 128 below
+// 2^24.
+int build_spmm_sweep(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSweep& s, std::string& msg,
+                     int col_groups = 0);
+
 // One unit of SDDMM work: a run of output sub-blocks that share 32 rows of X.
 struct SddmmItem {
     int32_t x_row0;

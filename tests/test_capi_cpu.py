@@ -9,7 +9,7 @@ import subprocess
 import numpy as np
 import pytest
 
-from helpers import REPO, W, capi
+from helpers import REPO, W, bsr_of, capi
 
 HEADER = REPO / "include" / "bsparse.h"
 
@@ -30,6 +30,20 @@ def test_every_declared_symbol_is_exported():
     nm = subprocess.run(["nm", "-D", "--defined-only", str(capi.LIB_PATH)], capture_output=True, text=True)
     exported = set(re.findall(r"\bT (bsp_\w+)", nm.stdout))
     assert set(names) <= exported
+
+
+def test_timeline_library_exports_the_same_entry_points_and_its_own():
+    """libbsparse_timeline.so (the profiling build) exports every function of
+    bsparse.h and the two of bsparse_timeline.h."""
+    lib = capi.load_timeline()
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+    text = re.sub(r"/\*.*?\*/", "", (REPO / "include" / "bsparse_timeline.h").read_text(), flags=re.S)
+    own = sorted(set(re.findall(r"\b(bsp_[a-z_0-9]+)\s*\(", text)))
+    assert own == ["bsp_timeline_attach", "bsp_timeline_clock_khz"]
+    for name in own:
+        assert hasattr(lib, name)
+    assert lib.bsp_timeline_attach(None, 5, 0) == capi.BSP_ERR_INVALID_ARGUMENT
 
 
 def test_library_links_hip_and_has_gfx950_code():
@@ -510,3 +524,19 @@ def test_binding_refuses_host_memory_and_mismatched_tensors():
     t = torch.zeros((4, 24), dtype=torch.int16)
     addr, ld = op(_OnGpu(t[:, :16]), "b", 2, 4, 16, None, 0)
     assert ld == 24 and addr == t.data_ptr()
+
+
+def test_spmm_schedule_without_load_balancing(monkeypatch):
+    """BSP_SPMM_BALANCE=0 (the reference's _no_lb operators): the skewed
+    workload's rows stay whole, work items map to workgroups in natural
+    order, and the products are still each scheduled once."""
+    a = W.workload_spmm_skewed()["a"]
+    bal = capi.spmm_schedule(bsr_of(a), 1024, 256)
+    assert bal["info"]["n_split_rows"] >= 0
+    monkeypatch.setenv("BSP_SPMM_BALANCE", "0")
+    s = capi.spmm_schedule(bsr_of(a), 1024, 256)
+    assert s["info"]["n_split_rows"] == 0
+    assert np.array_equal(s["wgmap"], np.arange(len(s["wgmap"])))
+    items = s["items"]
+    assert np.all(items[:, 3] == -1)
+    assert (items[:, 2] - items[:, 1]).sum() == a.nblocks

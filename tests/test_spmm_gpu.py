@@ -125,23 +125,31 @@ def test_many_empty_rows_R256():
     assert np.all(got[256:] == 0.0)
 
 
-# --- skewed rows: the persistent kernel, and the per-item kernels with split
-# rows (the reduce kernel adds the pieces)
-@pytest.mark.parametrize("kernel,split", [("persistent", None), ("items", None), ("items", 40)])
+# --- skewed rows: the persistent kernel (the plan's choice), the sweep
+# kernel, and the per-item kernels with split rows (the reduce kernel adds
+# the pieces)
+@pytest.mark.parametrize("kernel,split", [("sweep", None), ("persistent", None), ("items", None), ("items", 40)])
 def test_skewed_workload_full_size(monkeypatch, kernel, split):
-    """The skewed workload as planned (the persistent kernel), on the per-item
-    kernels with every row whole, and with the rows over 40 entries cut into
-    pieces: held to the oracle, and the same bits on a second run."""
+    """The skewed workload as planned (the persistent kernel), on the sweep
+    kernel (its shape qualifies for the sweep kernel's automatic choice), on
+    the per-item kernels with every row whole, and with the rows over 40
+    entries cut into pieces: held to the oracle, and the same bits on a second
+    run."""
     if kernel == "items":
         monkeypatch.setenv("BSP_SPMM_STREAM", "0")
+    if kernel == "sweep":
+        monkeypatch.setenv("BSP_SPMM_SWEEP", "1")
     if split:
         monkeypatch.setenv("BSP_SPMM_SPLIT", str(split))
     w = W.workload_spmm_skewed()
     a = w["a"]
     plan = capi.SpmmPlan(capi.Bsr(a.H, a.W, 32, 32, a.indptr, a.indices), w["N"], "f32")
     info = plan.info()
-    assert info["persistent"] == (kernel == "persistent")
+    assert info["persistent"] == {"sweep": 3, "persistent": 1, "items": 0}[kernel], info
     assert (info["n_split_rows"] > 0) == bool(split)
+    if kernel == "sweep":
+        # one workgroup per compute unit, 16 units each, one sweep
+        assert (info["grid"], info["waves"], info["stages"], info["n_items"]) == (256, 8, 14, 4096), info
     if kernel == "persistent":
         # eight units per workgroup, the longest (101 entries) above a
         # workgroup's share: one workgroup per compute unit, four B loaders,
