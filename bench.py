@@ -204,10 +204,11 @@ def attach_traffic(rec, key):
 
 # ---------------------------------------------------------------------------
 # Sections
-def bench_spmm(torch, capi, W, a, b, out_dtype, timer, warmup, rotate=True):
-    """Times SpMM on (a, b); returns (timings, flops, bytes, plan info, copies)."""
+def bench_spmm(torch, capi, W, a, b, out_dtype, timer, warmup, rotate=True, lib=None):
+    """Times SpMM on (a, b) (through `lib`, default libbsparse.so); returns
+    (timings, flops, bytes, plan info, copies)."""
     M, N = a.H, b.shape[1]
-    plan = capi.SpmmPlan(capi.Bsr(a.H, a.W, a.R, a.C, a.indptr, a.indices), N, out_dtype)
+    plan = capi.SpmmPlan(capi.Bsr(a.H, a.W, a.R, a.C, a.indptr, a.indices), N, out_dtype, lib=lib)
     out_bytes = 4 if out_dtype == "f32" else 2
     per_copy = a.data.nbytes + b.nbytes + M * N * out_bytes
     ncopy = max(1, -(-ROTATE_BYTES // per_copy)) if rotate else 1
@@ -228,10 +229,10 @@ def bench_spmm(torch, capi, W, a, b, out_dtype, timer, warmup, rotate=True):
     return t, W.spmm_flops(a.nblocks, a.R, a.C, N), W.spmm_bytes(a, N, out_bytes), info, ncopy
 
 
-def bench_sddmm(torch, capi, W, mask, x, y, y_layout, out_dtype, timer, warmup):
+def bench_sddmm(torch, capi, W, mask, x, y, y_layout, out_dtype, timer, warmup, lib=None):
     K = x.shape[1]
     plan = capi.SddmmPlan(capi.Bsr(mask.H, mask.W, mask.R, mask.C, mask.indptr, mask.indices), K,
-                          y_layout, out_dtype)
+                          y_layout, out_dtype, lib=lib)
     nv = mask.nblocks * mask.R * mask.C
     out_bytes = 4 if out_dtype == "f32" else 2
     per_copy = mask.data.nbytes + x.nbytes + y.nbytes + nv * out_bytes
@@ -836,21 +837,25 @@ def main():
 
 
 # ---------------------------------------------------------------------------
-# Ablation: load balancing on and off, and the per-workgroup timeline.
+# Ablation: the cost decomposition, load balancing on and off, and the
+# per-workgroup timeline.
 #
 # The reference prices its kernels' parts with profiling variants of its
 # operators (block_spmm/inc/host_code.hpp:86-161, registered in
-# HostCodeRegistryProfiling, :195-222; block_sddmm/PROFILING_PLAN.md).  Two of
-# its comparisons are rebuilt here on committed code:
+# HostCodeRegistryProfiling, :195-222; block_sddmm/inc/host_code.hpp:71-153;
+# block_sddmm/PROFILING_PLAN.md).  Its comparisons are rebuilt here on
+# committed code, all through libbsparse_timeline.so (the same sources as
+# libbsparse.so, plus the switches and stamps of include/bsparse_timeline.h):
+#   - the decomposition: each workload timed whole and with one part left
+#     out (its _no_a_read, _no_b_read, _no_compute and _no_write variants;
+#     SDDMM's _no_b/c/d_read), and with everything left out (the launch and
+#     the schedule's own walk);
 #   - load balancing on and off (its `_no_lb` operators; the published table
 #     block_spmm/scripts/figures/load_imbalance_table.csv): plans built with
 #     BSP_SPMM_BALANCE=0 keep rows whole and place work in natural order, in
 #     contiguous ranges;
-#   - where a launch's time goes: libbsparse_timeline.so (the same sources,
-#     plus per-workgroup wall-clock stamps, include/bsparse_timeline.h) gives
-#     each workgroup's start, first landing, progress and end.
-# Variants that skip part of the work are not built into committed code; the
-# timeline takes their place.
+#   - where a launch's time goes: each workgroup's start, first landing,
+#     progress and end.
 class plan_env:
     """Environment variables set while plans are created (the library reads
     its schedule overrides at plan creation)."""
@@ -981,9 +986,74 @@ def timeline_sddmm(torch, capi, W, m, x, y, out_dtype):
     return rec
 
 
+SPMM_PARTS = (("full", 0), ("no_a_read", 1), ("no_b_read", 2), ("no_compute", 8), ("no_write", 16),
+              ("nothing", 1 | 2 | 8 | 16))
+SDDMM_PARTS = (("full", 0), ("no_mask_read", 1), ("no_x_read", 2), ("no_y_read", 4), ("no_compute", 8),
+               ("no_write", 16), ("nothing", 1 | 2 | 4 | 8 | 16))
+
+
+def decompose(torch, capi, tl, parts, time_one):
+    """Times one workload with each set of parts left out (graph replay,
+    cold operands); returns {part: us} and the time each part adds (full
+    minus the time without it)."""
+    rec = {}
+    try:
+        for name, flags in parts:
+            capi.check(tl.bsp_timeline_skip(flags), tl)
+            rec[name] = time_one()
+    finally:
+        tl.bsp_timeline_skip(0)
+    rec["saved_us"] = {name: round(rec["full"] - rec[name], 3) for name, _ in parts if name != "full"}
+    return rec
+
+
+def decomposition(torch, capi, W, warmup):
+    """The cost decomposition of the headline kernels: 4096^2 25% and 50%
+    (fp32 C), the skewed 16384^2, the reference's own 8192^3 configuration
+    (256x256 blocks, random 50%, bf16 C), and the 10% SDDMM."""
+    tl = capi.load_timeline()
+    timer = Timer(torch, 50, trace=False)
+    out = {}
+
+    def spmm(label, a, b, od, env=None):
+        plan_kind = {}
+
+        def one():
+            with plan_env(env):
+                t, fl, nb, info, _ = bench_spmm(torch, capi, W, a, b, od, timer, warmup, lib=tl)
+            plan_kind.update(plan_summary(info))
+            return round(t["launch_ms"] * 1e3, 3)
+        r = decompose(torch, capi, tl, SPMM_PARTS, one)
+        r["plan"] = plan_kind
+        out[label] = r
+        print(f"[bench] ablation {label}: " + json.dumps({k: r[k] for k, _ in SPMM_PARTS}), file=sys.stderr,
+              flush=True)
+
+    for d in (0.25, 0.5):
+        w = W.workload_spmm_sweep(d)
+        spmm(f"c2_{int(d * 100)}_f32", w["a"], w["b"], "f32")
+    w = W.workload_spmm_skewed()
+    spmm("c4", w["a"], w["b"], "f32")
+    spmm("c4_sweep_kernel", w["a"], w["b"], "f32", {"BSP_SPMM_SWEEP": "2"})
+    del w
+    a, b = pattern_workload(W, "random", 0.5), pattern_b(W)
+    spmm("8192c_256_random50_bf16", a, b, "bf16")
+    del a, b
+    s3 = W.workload_sddmm()
+
+    def one_sddmm():
+        t, fl, nb, info = bench_sddmm(torch, capi, W, s3["mask"], s3["x"], s3["y"], capi.ROW_MAJOR, "f32", timer,
+                                      warmup, lib=tl)
+        return round(t["launch_ms"] * 1e3, 3)
+    out["c3_sddmm"] = decompose(torch, capi, tl, SDDMM_PARTS, one_sddmm)
+    return out
+
+
 def ablation(torch, capi, W, timer, warmup):
-    """Load balancing on and off, and the per-workgroup timelines."""
+    """The cost decomposition, load balancing on and off, and the
+    per-workgroup timelines."""
     rec = {"balance": [], "timeline": {}}
+    rec["decomposition"] = decomposition(torch, capi, W, warmup)
     published = {"tril": (43.31, 29.5), "triu": (29.6, 24.88)}  # N150 DDA with / without LB, 8192, R=C=256
     w = W.workload_spmm_skewed()
     for label, env in (("skewed 16384^2, persistent kernel", {}),
@@ -1025,6 +1095,8 @@ def ablation(torch, capi, W, timer, warmup):
     s3 = W.workload_sddmm()
     rec["timeline"]["c3_sddmm"] = timeline_sddmm(torch, capi, W, s3["mask"], s3["x"], s3["y"], "f32")
     rec["summary"] = {
+        "decomposition_us": {k: {p: v[p] for p, _ in (SDDMM_PARTS if k.startswith("c3") else SPMM_PARTS)}
+                             for k, v in rec["decomposition"].items()},
         "lb_speedup": {r["workload"].split(",")[0].split(" ")[0] + ("_items" if "per-item" in r["workload"] else ""):
                        r["speedup"] for r in rec["balance"]},
         "timeline_p50_us": {k: {"start": v["start_offset_us"]["p50"],

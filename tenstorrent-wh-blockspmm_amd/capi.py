@@ -158,13 +158,20 @@ def check(status: int, lib: Optional[ctypes.CDLL] = None) -> None:
 
 
 TIMELINE_SLOTS = 64  # BSP_TIMELINE_SLOTS of include/bsparse_timeline.h
+# Skip switches of the instrumented build (BSP_SKIP_* of include/bsparse_timeline.h).
+SKIP_SPARSE_READ = 1   # A of SpMM, the mask values of SDDMM
+SKIP_DENSE_READ = 2    # B of SpMM, X of SDDMM
+SKIP_DENSE2_READ = 4   # Y of SDDMM
+SKIP_COMPUTE = 8
+SKIP_WRITE = 16
 _timeline_lib: Optional[ctypes.CDLL] = None
 
 
 def load_timeline() -> ctypes.CDLL:
     """libbsparse_timeline.so: every entry point of libbsparse.so (same
-    results), plus per-workgroup time stamps (include/bsparse_timeline.h).
-    Pass it as `lib` to the plan classes to run a plan through it."""
+    results), plus per-workgroup time stamps and the skip switches
+    (include/bsparse_timeline.h).  Pass it as `lib` to the plan classes to
+    run a plan through it."""
     global _timeline_lib
     if _timeline_lib is None:
         lib = load(TIMELINE_PATH)
@@ -172,6 +179,8 @@ def load_timeline() -> ctypes.CDLL:
         lib.bsp_timeline_attach.argtypes = [c_void_p, c_int64, c_int]
         lib.bsp_timeline_clock_khz.restype = c_int
         lib.bsp_timeline_clock_khz.argtypes = [c_int, POINTER(c_int)]
+        lib.bsp_timeline_skip.restype = c_int
+        lib.bsp_timeline_skip.argtypes = [c_int]
         _timeline_lib = lib
     return _timeline_lib
 

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -12,6 +13,13 @@
 #include "bsp_kernels.hpp"
 #include "bsp_schedule.hpp"
 #include "bsparse.h"
+#ifdef BSP_TIMELINE
+#include "bsparse_timeline.h"
+static_assert(BSP_SKIP_SPARSE_READ == bsp::kSkipSparseRead && BSP_SKIP_DENSE_READ == bsp::kSkipDenseRead &&
+                  BSP_SKIP_DENSE2_READ == bsp::kSkipDense2Read && BSP_SKIP_COMPUTE == bsp::kSkipCompute &&
+                  BSP_SKIP_WRITE == bsp::kSkipWrite,
+              "skip flags of bsparse_timeline.h and the kernels");
+#endif
 
 struct bsp_plan {
     int kind = 0;  // 1 SpMM, 2 SDDMM, 3 fused attention pair, 4 SpGEMM
@@ -47,6 +55,15 @@ struct bsp_plan {
 namespace {
 
 thread_local std::string g_last_error;
+
+// Work left out of every launch from now on (the instrumented build's
+// bsp_timeline_skip; always 0 in libbsparse.so).
+#ifdef BSP_TIMELINE
+std::atomic<int> g_skips{0};
+int launch_skips() { return g_skips.load(std::memory_order_relaxed); }
+#else
+constexpr int launch_skips() { return 0; }
+#endif
 
 int fail(int status, const std::string& msg) {
     g_last_error = msg;
@@ -603,6 +620,7 @@ bsp::SpmmArgs spmm_args(const bsp_plan* p, const uint16_t* a_vals, const uint16_
     args.lda = (int32_t)p->C;
     args.n_tiles = p->info.n_tiles;
     args.N = (int32_t)p->N;
+    args.skips = launch_skips();
     return args;
 }
 
@@ -638,6 +656,10 @@ int bsp_spmm(const bsp_plan* p, const uint16_t* a_vals, const uint16_t* b, int64
     DeviceGuard g(p->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     const bsp::SpmmArgs args = spmm_args(p, a_vals, b, ldb, c, ldc);
+    // Work can be left out (the instrumented build) of the persistent, sweep
+    // and 256-column row-group kernels only.
+    if (args.skips != 0 && !p->info.persistent && !(p->info.group > 1 && p->info.tile_n == 256))
+        return fail(BSP_ERR_UNSUPPORTED, "this plan's kernel has no switches to leave work out");
     hipError_t e;
     if (p->info.persistent == 3) {
         bsp::SpmmSweepArgs sa{};
@@ -652,6 +674,7 @@ int bsp_spmm(const bsp_plan* p, const uint16_t* a_vals, const uint16_t* b, int64
         sa.ldc = ldc;
         sa.lda = (int32_t)p->C;
         sa.N = (int32_t)p->N;
+        sa.skips = args.skips;
         e = bsp::launch_spmm_sweep(sa, p->out_dtype == BSP_DTYPE_BF16, p->sweep_ax4 != 0, p->info.grid,
                                    (hipStream_t)stream);
     } else if (p->info.persistent) {
@@ -668,6 +691,7 @@ int bsp_spmm(const bsp_plan* p, const uint16_t* a_vals, const uint16_t* b, int64
         sa.ldc = ldc;
         sa.lda = (int32_t)p->C;
         sa.N = (int32_t)p->N;
+        sa.skips = args.skips;
         e = bsp::launch_spmm_stream(sa, p->stream_variant, p->out_dtype == BSP_DTYPE_BF16, p->info.grid,
                                     (hipStream_t)stream);
     } else {
@@ -711,6 +735,7 @@ int bsp_attention(const bsp_plan* p, const uint16_t* mask_vals, const uint16_t* 
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     bsp::AttentionArgs args{};
     args.s = spmm_args(p, mask_vals, v, ldv, out, ldo);
+    if (args.s.skips != 0) return fail(BSP_ERR_UNSUPPORTED, "the attention kernel has no switches to leave work out");
     args.q = q;
     args.k = k;
     args.ldq = ldq;
@@ -801,6 +826,9 @@ int bsp_sddmm(const bsp_plan* p, const uint16_t* mask_vals, const uint16_t* x, i
     args.ldo = (int32_t)p->C;
     args.K = (int32_t)p->K;
     args.one_shot = p->sddmm_one_shot;
+    args.skips = launch_skips();
+    if (args.skips != 0 && !args.one_shot)
+        return fail(BSP_ERR_UNSUPPORTED, "this plan's kernel has no switches to leave work out");
     hipError_t e = bsp::launch_sddmm(args, p->layout == BSP_COL_MAJOR,
                                      p->out_dtype == BSP_DTYPE_BF16, p->info.grid,
                                      (hipStream_t)stream);
@@ -1062,3 +1090,12 @@ int bsp_host_spgemm(const bsp_bsr_desc* a, const uint16_t* a_vals, const bsp_bsr
 }
 
 }  // extern "C"
+
+#ifdef BSP_TIMELINE
+extern "C" int bsp_timeline_skip(int flags) {
+    const int all = BSP_SKIP_SPARSE_READ | BSP_SKIP_DENSE_READ | BSP_SKIP_DENSE2_READ | BSP_SKIP_COMPUTE | BSP_SKIP_WRITE;
+    if (flags & ~all) return fail(BSP_ERR_INVALID_ARGUMENT, "unknown skip flags");
+    g_skips.store(flags, std::memory_order_relaxed);
+    return BSP_OK;
+}
+#endif

@@ -97,11 +97,15 @@ struct TimelinePick<true> {
 #define BSP_TL_DECL_REGS() TimelineRegs bsp_tl
 #define BSP_TL_MARK(i) bsp_tl.mark(i)
 #define BSP_TL_FLUSH() bsp_tl.flush()
+// Whether the launch leaves out a part of the work (kSkip* bit of the
+// kernel arguments, a wave-uniform scalar).
+#define BSP_SKIP(p, bit) (((p).skips & (bit)) != 0)
 #else
 #define BSP_TL_DECL(LDS_LOG) ((void)0)
 #define BSP_TL_DECL_REGS() ((void)0)
 #define BSP_TL_MARK(i) ((void)0)
 #define BSP_TL_FLUSH() ((void)0)
+#define BSP_SKIP(p, bit) false
 #endif
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -930,9 +934,17 @@ __global__ __launch_bounds__(64 * NW, RW <= 4 && S == 3 ? 2 : 1) void spmm_group
     const uint32_t a_lds = lds0 + wave * (HALF ? 512 : AL * 1024);
     const uint32_t b_lds = lds0 + B_RING + wave * Slice::BI * 1024;
     EntryWords words(p.ents + it.e_begin, it.e_end - it.e_begin, lane);
+    // (An operand left out by the instrumented build is read, for every
+    // entry, where the item's first entry reads it -- an L2 hit after the
+    // first, a different line per workgroup: the waits count both operands'
+    // loads, so the loads stay.)
+    uint32_t bw_first = 0, aw_first = 0;
+    if (BSP_SKIP(p, kSkipSparseRead | kSkipDenseRead)) words.get(0, lane, bw_first, aw_first);
     auto issue = [&](int e, int stage) {
         uint32_t bw, aw;
         words.get(e, lane, bw, aw);
+        if (BSP_SKIP(p, kSkipSparseRead)) aw = aw_first;
+        if (BSP_SKIP(p, kSkipDenseRead)) bw = bw_first;
         const uint16_t* ablk = p.a + (int64_t)aw * 32;
         if constexpr (PAIR) {
             if ((e & 1) == 0) {
@@ -986,6 +998,7 @@ __global__ __launch_bounds__(64 * NW, RW <= 4 && S == 3 ? 2 : 1) void spmm_group
         brd.read_half(smem + B_RING + stage * Slice::BYTES, o.b, h);
     };
     auto mul_half = [&](const Operands& o, int h) {
+        if (BSP_SKIP(p, kSkipCompute)) return;
 #pragma unroll
         for (int i = 0; i < SR; ++i)
 #pragma unroll
@@ -993,6 +1006,7 @@ __global__ __launch_bounds__(64 * NW, RW <= 4 && S == 3 ? 2 : 1) void spmm_group
     };
     run_ring_halves<S, PER, EXTRA, SR * NT, Operands>(it.e_end - it.e_begin, issue, read_half, mul_half, [] {});
 
+    if (BSP_SKIP(p, kSkipWrite)) return;
 #pragma unroll
     for (int i = 0; i < SR; ++i) {
         const int st = wr * SR + i;  // stripe within the group
@@ -1236,9 +1250,15 @@ __global__ __launch_bounds__(64 * (4 * SR + 1 + NBW) * PIPES) void spmm_stream_k
             // (lanes 0 and 1, 4 bytes each) through the same DMA path, so the
             // loader's wait for the entry covers it too.
             const void* words = p.apw + wg.w_begin;
+            // (A left out by the instrumented build: every entry's loads read
+            // the A sub-blocks of the workgroup's first entry, an L2 hit after
+            // the first, so that the wave's five loads per entry stay.)
+            uint64_t apw_first = 0;
+            if (BSP_SKIP(p, kSkipSparseRead)) apw_first = load_const(&head->apw[0]);
             auto issue_pair = [&](int e, uint64_t w) {
                 const uint32_t st = (uint32_t)(e % SA);
-                const uint32_t w0 = (uint32_t)w, w1 = (uint32_t)(w >> 32);
+                const uint64_t wa = BSP_SKIP(p, kSkipSparseRead) ? apw_first : w;
+                const uint32_t w0 = (uint32_t)wa, w1 = (uint32_t)(wa >> 32);
                 const uint32_t any = w0 != kNoBlock ? w0 : w1;
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
@@ -1258,6 +1278,7 @@ __global__ __launch_bounds__(64 * (4 * SR + 1 + NBW) * PIPES) void spmm_stream_k
             return;
         }
         auto issue_a = [&](int e, uint32_t w) {
+            if (BSP_SKIP(p, kSkipSparseRead)) return;  // left out: the wave's waits pass at once
             const uint16_t* ablk = p.a + (int64_t)w * 32;
             const uint32_t dst = lds0 + (uint32_t)(e % SA) * A_STAGE;
             gl_lds16_s(a_voff[0], ablk, dst);
@@ -1275,6 +1296,7 @@ __global__ __launch_bounds__(64 * (4 * SR + 1 + NBW) * PIPES) void spmm_stream_k
         const Loader ld(wb, lane, p.ldb);
         const uint32_t b_lds = lds0 + A_RING + wb * Loader::BI * 1024;
         auto issue_b = [&](int e, int64_t w) {
+            if (BSP_SKIP(p, kSkipDenseRead)) return;  // left out: the wave's waits pass at once
             const uint16_t* bpan = p.b + (int64_t)(uint32_t)w * p.ldb + (int32_t)(w >> 32);
             const uint32_t dst = b_lds + (uint32_t)(e % SB) * Loader::BYTES;
 #pragma unroll
@@ -1314,6 +1336,7 @@ __global__ __launch_bounds__(64 * (4 * SR + 1 + NBW) * PIPES) void spmm_stream_k
     // Stores this wave's part of the unit's tile (with stripe pairs, of its
     // stripe; the second stripe of an odd one out is -1).
     auto store_unit = [&](const SpmmStreamUnit& un) {
+        if (BSP_SKIP(p, kSkipWrite)) return;
         const int32_t stripe = half == 0 ? un.row : un.aux;
         if (SR > 1 && stripe < 0) return;
         const int64_t row0 = (int64_t)stripe * 32;
@@ -1392,7 +1415,7 @@ __global__ __launch_bounds__(64 * (4 * SR + 1 + NBW) * PIPES) void spmm_stream_k
     auto multiply = [&](const Operands& o) {
         // With stripe pairs, a wave whose stripe has no block in the entry's
         // column skips its products (the word was read in an earlier step).
-        if (SR == 1 || __builtin_amdgcn_readfirstlane(o.w) != kNoBlock) {
+        if (!BSP_SKIP(p, kSkipCompute) && (SR == 1 || __builtin_amdgcn_readfirstlane(o.w) != kNoBlock)) {
 #pragma unroll
             for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
@@ -1559,15 +1582,27 @@ __global__ __launch_bounds__(512, 1) void spmm_sweep_kernel(SpmmSweepArgs p) {
         const int r = x >> 6, c = ((x & 63) >> 4) ^ ((r >> 2) & 3);
         a_voff = (uint32_t)(2 * (r * p.lda + 8 * c) + (x & 15));
     }
+    // (An operand left out by the instrumented build is read, for every
+    // entry, where the workgroup's first entry reads it -- an L2 hit after
+    // the first, and a different line per workgroup: the wave's waits count
+    // both operands' loads, so the loads stay.)
+    int64_t bw_first = 0;
+    uint32_t aw_first = 0;
+    if (BSP_SKIP(p, kSkipSparseRead | kSkipDenseRead)) {
+        bw_first = load_const(&head->bw[0]);
+        aw_first = load_const(&head->aw[0]);
+    }
     auto issue = [&](int e, int64_t bwd, uint32_t awd) __attribute__((always_inline)) {
         const uint32_t st = (uint32_t)(e % S);
+        if (BSP_SKIP(p, kSkipDenseRead)) bwd = bw_first;
+        if (BSP_SKIP(p, kSkipSparseRead)) awd = aw_first;
         const uint16_t* bpan = uniform_ptr(p.b + (int64_t)(uint32_t)bwd * p.ldb + (int32_t)((bwd >> 32) & 0xffffff));
+        const uint16_t* ablk = uniform_ptr(p.a + (int64_t)awd * 32);
         gl_lds16_s(ld.voff[0], bpan, lds0 + A_RING + st * B_BYTES + wave * 1024);
         if constexpr (AX4) {
-            if (wave < 2)
-                gl_lds16_s(a_voff, uniform_ptr(p.a + (int64_t)awd * 32), lds0 + st * kA_BYTES + wave * 1024);
+            if (wave < 2) gl_lds16_s(a_voff, ablk, lds0 + st * kA_BYTES + wave * 1024);
         } else {
-            gl_lds4_s(a_voff, uniform_ptr(p.a + (int64_t)awd * 32), lds0 + st * kA_BYTES + wave * 256);
+            gl_lds4_s(a_voff, ablk, lds0 + st * kA_BYTES + wave * 256);
         }
     };
     // ---- products.
@@ -1589,6 +1624,7 @@ __global__ __launch_bounds__(512, 1) void spmm_sweep_kernel(SpmmSweepArgs p) {
     const SpmmSweepRec* sweeps = p.sweeps + wg.s_begin;
     int sw = 0, left = 0;
     auto store_sweep = [&](int si) __attribute__((always_inline)) {
+        if (BSP_SKIP(p, kSkipWrite)) return;
         // Wait states between the last product (asm, unseen by the
         // compiler's hazard checks) and the reads of its result: more than a
         // 16-pass product's 18.
@@ -1654,6 +1690,7 @@ __global__ __launch_bounds__(512, 1) void spmm_sweep_kernel(SpmmSweepArgs p) {
     // overlapping the previous destination), and the stores that read the
     // results are preceded by explicit wait states (store_sweep).
     auto multiply = [&](const Ops& o) __attribute__((always_inline)) {
+        if (BSP_SKIP(p, kSkipCompute)) return;
         const int slot = __builtin_amdgcn_readfirstlane(o.slot);
         __asm__ volatile(
             "s_nop 1\n\t"
@@ -2284,13 +2321,17 @@ __global__ __launch_bounds__(256, 2) void sddmm_shot_kernel(SddmmArgs p) {
     uint32_t mk[16];
     u32x4 mraw[2];
     if (has) off = load_const(p.ent_off + e);
+    // (A read left out by the instrumented build is not issued: every wait
+    // here is for all of the workgroup's loads.)
     if constexpr (MASK16) {
-        if (has) {
+        if (has && !BSP_SKIP(p, kSkipSparseRead)) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const int c = lane + 64 * h;
                 mraw[h] = *(const u32x4*)(p.mask + off + (int64_t)(c >> 2) * p.ldo + 8 * (c & 3));
             }
+        } else {
+            mraw[0] = mraw[1] = u32x4{0u, 0u, 0u, 0u};
         }
     }
 
@@ -2305,9 +2346,9 @@ __global__ __launch_bounds__(256, 2) void sddmm_shot_kernel(SddmmArgs p) {
 #pragma unroll
     for (int j = 0; j < (L::XI + 3) / 4; ++j) {
         const int t = wave + 4 * j;
-        if (t < L::XI) rows_panel(p.x + (int64_t)it.x_row0 * p.ldx, p.ldx, t, lds0);
+        if (t < L::XI && !BSP_SKIP(p, kSkipDenseRead)) rows_panel(p.x + (int64_t)it.x_row0 * p.ldx, p.ldx, t, lds0);
     }
-    if (has) {
+    if (has && !BSP_SKIP(p, kSkipDense2Read)) {
         const int32_t col = load_const(p.ent_col + e);
         if (Y_COLMAJOR) {
 #pragma unroll
@@ -2322,10 +2363,13 @@ __global__ __launch_bounds__(256, 2) void sddmm_shot_kernel(SddmmArgs p) {
         }
     }
     if constexpr (!MASK16) {
-        if (has) {
+        if (has && !BSP_SKIP(p, kSkipSparseRead)) {
 #pragma unroll
             for (int v = 0; v < 16; ++v)
                 mk[v] = p.mask[off + (int64_t)(8 * (v >> 2) + 4 * q + (v & 3)) * p.ldo + l32];
+        } else {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) mk[v] = 0u;
         }
     }
     wait_vmcnt<0>();
@@ -2359,7 +2403,7 @@ __global__ __launch_bounds__(256, 2) void sddmm_shot_kernel(SddmmArgs p) {
                 const u32x4 hi = ld_tr_b16(ys + (r + 4) * 64 + cb);
                 b = u32x4{lo.x, lo.y, hi.x, hi.y};
             }
-            acc = mfma32(a, b, acc);
+            if (!BSP_SKIP(p, kSkipCompute)) acc = mfma32(a, b, acc);
         }
     BSP_TL_MARK(2);
     if constexpr (MASK16) {
@@ -2380,14 +2424,16 @@ __global__ __launch_bounds__(256, 2) void sddmm_shot_kernel(SddmmArgs p) {
             mk[4 * i + 3] = r.y >> 16;
         }
     }
+    if (!BSP_SKIP(p, kSkipWrite)) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const float val = acc[v] * bf16_to_f32((uint16_t)mk[v]);
-        const int64_t idx = off + (int64_t)(8 * (v >> 2) + 4 * q + (v & 3)) * p.ldo + l32;
-        if (OUT_BF16)
-            store_out(&((uint16_t*)p.out)[idx], f32_to_bf16_rne(val));
-        else
-            store_out(&((float*)p.out)[idx], val);
+        for (int v = 0; v < 16; ++v) {
+            const float val = acc[v] * bf16_to_f32((uint16_t)mk[v]);
+            const int64_t idx = off + (int64_t)(8 * (v >> 2) + 4 * q + (v & 3)) * p.ldo + l32;
+            if (OUT_BF16)
+                store_out(&((uint16_t*)p.out)[idx], f32_to_bf16_rne(val));
+            else
+                store_out(&((float*)p.out)[idx], val);
+        }
     }
     if (wave == 0) BSP_TL_FLUSH();
 }

@@ -10,6 +10,16 @@
 
 namespace bsp {
 
+// Work the instrumented build (libbsparse_timeline.so) can leave out of a
+// launch, for cost decompositions (the values of BSP_SKIP_* in
+// bsparse_timeline.h).  Sparse = A of SpMM, the mask values of SDDMM; dense
+// = B of SpMM, X of SDDMM; dense2 = Y of SDDMM.
+constexpr int kSkipSparseRead = 1;
+constexpr int kSkipDenseRead = 2;
+constexpr int kSkipDense2Read = 4;
+constexpr int kSkipCompute = 8;
+constexpr int kSkipWrite = 16;
+
 struct SpmmArgs {
     const uint16_t* a;        // A block values (bf16), nblocks*R*C
     const uint16_t* b;        // B (bf16), row-major K x N, leading dim ldb
@@ -23,7 +33,7 @@ struct SpmmArgs {
     int32_t lda;              // row stride inside an A block (= C)
     int32_t n_tiles;
     int32_t N;                // columns of B and C (the last tile may be partial)
-    int32_t pad;
+    int32_t skips;            // work the instrumented build leaves out (kSkip*; 0 in libbsparse.so)
 };
 
 // Persistent SpMM (spmm_stream_kernel): each workgroup streams the entries of
@@ -41,6 +51,8 @@ struct SpmmStreamArgs {
     int64_t ldc;
     int32_t lda;                   // row stride inside an A block (= C)
     int32_t N;
+    int32_t skips;                 // work the instrumented build leaves out (kSkip*; 0 in libbsparse.so)
+    int32_t pad;
 };
 
 // Sweep SpMM (spmm_sweep_kernel): one workgroup per compute unit holds a
@@ -57,6 +69,8 @@ struct SpmmSweepArgs {
     int64_t ldc;
     int32_t lda;                   // row stride inside an A block (= C)
     int32_t N;
+    int32_t skips;                 // work the instrumented build leaves out (kSkip*; 0 in libbsparse.so)
+    int32_t pad;
 };
 
 // Ring stages of the sweep kernel: 14 stages of 10 KB (2 KB of A, 8 KB of
@@ -162,7 +176,7 @@ struct SddmmArgs {
     int32_t ldo;              // row stride inside an output / mask block (= C)
     int32_t K;
     int32_t one_shot;         // 1: sddmm_shot_kernel (chosen at plan creation)
-    int32_t pad;
+    int32_t skips;            // work the instrumented build leaves out (kSkip*; 0 in libbsparse.so)
 };
 
 // The one-shot SDDMM kernel takes K of 32, 64, 128 or 256 and items of at

@@ -34,16 +34,27 @@ def test_every_declared_symbol_is_exported():
 
 def test_timeline_library_exports_the_same_entry_points_and_its_own():
     """libbsparse_timeline.so (the profiling build) exports every function of
-    bsparse.h and the two of bsparse_timeline.h."""
+    bsparse.h and the three of bsparse_timeline.h; the skip switches take
+    only the BSP_SKIP_* bits (set and cleared here without a device)."""
     lib = capi.load_timeline()
     for name in _declared_functions():
         assert hasattr(lib, name), name
     text = re.sub(r"/\*.*?\*/", "", (REPO / "include" / "bsparse_timeline.h").read_text(), flags=re.S)
     own = sorted(set(re.findall(r"\b(bsp_[a-z_0-9]+)\s*\(", text)))
-    assert own == ["bsp_timeline_attach", "bsp_timeline_clock_khz"]
+    assert own == ["bsp_timeline_attach", "bsp_timeline_clock_khz", "bsp_timeline_skip"]
     for name in own:
         assert hasattr(lib, name)
     assert lib.bsp_timeline_attach(None, 5, 0) == capi.BSP_ERR_INVALID_ARGUMENT
+    flags = dict(re.findall(r"#define (BSP_SKIP_\w+) (\d+)", text))
+    assert {k: int(v) for k, v in flags.items()} == {
+        "BSP_SKIP_SPARSE_READ": capi.SKIP_SPARSE_READ, "BSP_SKIP_DENSE_READ": capi.SKIP_DENSE_READ,
+        "BSP_SKIP_DENSE2_READ": capi.SKIP_DENSE2_READ, "BSP_SKIP_COMPUTE": capi.SKIP_COMPUTE,
+        "BSP_SKIP_WRITE": capi.SKIP_WRITE}
+    assert lib.bsp_timeline_skip(32) == capi.BSP_ERR_INVALID_ARGUMENT
+    assert lib.bsp_timeline_skip(-1) == capi.BSP_ERR_INVALID_ARGUMENT
+    assert lib.bsp_timeline_skip(31) == capi.BSP_OK
+    assert lib.bsp_timeline_skip(0) == capi.BSP_OK
+    assert not hasattr(capi.load(), "bsp_timeline_skip")  # the plain library has no switches
 
 
 def test_library_links_hip_and_has_gfx950_code():
