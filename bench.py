@@ -986,8 +986,8 @@ def timeline_sddmm(torch, capi, W, m, x, y, out_dtype):
     return rec
 
 
-SPMM_PARTS = (("full", 0), ("no_a_read", 1), ("no_b_read", 2), ("no_compute", 8), ("no_write", 16),
-              ("nothing", 1 | 2 | 8 | 16))
+SPMM_PARTS = (("full", 0), ("no_a_read", 1), ("no_b_read", 2), ("no_reads", 1 | 2), ("no_compute", 8),
+              ("no_write", 16), ("nothing", 1 | 2 | 8 | 16))
 SDDMM_PARTS = (("full", 0), ("no_mask_read", 1), ("no_x_read", 2), ("no_y_read", 4), ("no_compute", 8),
                ("no_write", 16), ("nothing", 1 | 2 | 4 | 8 | 16))
 
@@ -1025,8 +1025,11 @@ def decomposition(torch, capi, W, warmup):
             return round(t["launch_ms"] * 1e3, 3)
         r = decompose(torch, capi, tl, SPMM_PARTS, one)
         r["plan"] = plan_kind
+        with plan_env(env):  # the same launch through libbsparse.so, for the instrumented build's overhead
+            t, *_ = bench_spmm(torch, capi, W, a, b, od, timer, warmup)
+        r["plain_us"] = round(t["launch_ms"] * 1e3, 3)
         out[label] = r
-        print(f"[bench] ablation {label}: " + json.dumps({k: r[k] for k, _ in SPMM_PARTS}), file=sys.stderr,
+        print(f"[bench] ablation {label}: " + json.dumps(dict({k: r[k] for k, _ in SPMM_PARTS}, plain=r["plain_us"])), file=sys.stderr,
               flush=True)
 
     for d in (0.25, 0.5):
@@ -1046,6 +1049,8 @@ def decomposition(torch, capi, W, warmup):
                                       warmup, lib=tl)
         return round(t["launch_ms"] * 1e3, 3)
     out["c3_sddmm"] = decompose(torch, capi, tl, SDDMM_PARTS, one_sddmm)
+    t, *_ = bench_sddmm(torch, capi, W, s3["mask"], s3["x"], s3["y"], capi.ROW_MAJOR, "f32", timer, warmup)
+    out["c3_sddmm"]["plain_us"] = round(t["launch_ms"] * 1e3, 3)
     return out
 
 
@@ -1095,7 +1100,8 @@ def ablation(torch, capi, W, timer, warmup):
     s3 = W.workload_sddmm()
     rec["timeline"]["c3_sddmm"] = timeline_sddmm(torch, capi, W, s3["mask"], s3["x"], s3["y"], "f32")
     rec["summary"] = {
-        "decomposition_us": {k: {p: v[p] for p, _ in (SDDMM_PARTS if k.startswith("c3") else SPMM_PARTS)}
+        "decomposition_us": {k: dict({p: v[p] for p, _ in (SDDMM_PARTS if k.startswith("c3") else SPMM_PARTS)},
+                                     plain=v["plain_us"])
                              for k, v in rec["decomposition"].items()},
         "lb_speedup": {r["workload"].split(",")[0].split(" ")[0] + ("_items" if "per-item" in r["workload"] else ""):
                        r["speedup"] for r in rec["balance"]},

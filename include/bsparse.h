@@ -264,7 +264,8 @@ int bsp_sddmm_schedule(const bsp_bsr_desc* mask, int64_t K, int num_cus, bsp_pla
  *                               first column of slots 0-15}
  *   bw      n_entries int64  first row of B | first column << 32 | slot << 56
  *                            | skip << 60 (a skip entry pads a sweep to an
- *                            even count and is not multiplied)
+ *                            even count and is not multiplied) | last << 61
+ *                            (the last entry of its unit in stream order)
  *   aw      n_entries uint32 element offset of the 32x32 A sub-block / 32 */
 int bsp_spmm_sweep_schedule(const bsp_bsr_desc* a, int64_t N, int num_cus, int col_groups,
                             bsp_plan_info* info, int32_t* wgs, int32_t* sweeps, int64_t* bw,

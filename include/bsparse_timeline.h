@@ -14,9 +14,13 @@
  * plus:
  *   - time stamps: wave 0 of every workgroup of the persistent SpMM, sweep
  *     SpMM and one-shot SDDMM kernels records the 100 MHz wall clock
- *     (s_memrealtime) at fixed points of its work into an LDS log, flushed to
- *     a caller's buffer when the workgroup ends (the log costs a scalar clock
- *     read per stamp and one 512-byte store per workgroup);
+ *     (s_memrealtime) at fixed points of its work: the persistent SpMM
+ *     stores each stamp to the caller's buffer at once (its wave 0 waits for
+ *     none of its own memory operations, and its LDS is sized to two
+ *     workgroups per compute unit with no byte to spare); the sweep SpMM
+ *     keeps a log in LDS and the one-shot SDDMM in registers, flushed to the
+ *     buffer when the workgroup ends (a scalar clock read per stamp, one
+ *     512-byte store per workgroup);
  *   - skip switches (bsp_timeline_skip), off by default: with none set a
  *     launch does all of the work of the plain library's, bit for bit.
  *
@@ -28,8 +32,9 @@
  *       entries 0 .. k+1 multiplied, every 8th entry (slot 2 + k/8 for
  *       k % 8 == 0, k/8 < 60); one-shot SDDMM: slot 2 = products done
  *   63  wave 0 has issued its last store (the end of its work)
- * A workgroup that ends without work (an idle one-shot SDDMM workgroup)
- * leaves its slots untouched: clear the buffer before a launch.
+ * Slots a workgroup does not reach keep what the buffer held (the
+ * persistent SpMM writes only the slots it reaches; an idle one-shot SDDMM
+ * workgroup writes none): clear the buffer before each launch.
  */
 #ifndef BSPARSE_TIMELINE_H
 #define BSPARSE_TIMELINE_H
@@ -54,7 +59,8 @@ extern "C" {
  *     workgroup's first entry reads it instead -- an L2 hit after the
  *     first, on a line of its own per workgroup -- so that the operand
  *     moves no HBM or Infinity-Cache bytes while its requests and bytes
- *     into LDS stay;
+ *     into LDS stay; with both operands of such a kernel left out, no load
+ *     is issued at all;
  *   BSP_SKIP_COMPUTE: no matrix-core products (the operands are still read
  *     from LDS; the accumulators stay zero);
  *   BSP_SKIP_WRITE: no stores of the output.
@@ -67,9 +73,8 @@ extern "C" {
 
 /* Attaches a device buffer of `capacity` workgroups x BSP_TIMELINE_SLOTS
  * uint64 stamps on `device` (NULL detaches).  Launches from then on write the
- * stamps of workgroups below `capacity` (workgroup g at g*64 .. g*64+63) and
- * zero the slots they do not reach.  Calls that overlap on the device share
- * the buffer.  Returns a bsp_status. */
+ * stamps of workgroups below `capacity` (workgroup g at g*64 .. g*64+63).
+ * Calls that overlap on the device share the buffer.  Returns a bsp_status. */
 int bsp_timeline_attach(void* buffer, int64_t capacity, int device);
 
 /* Frequency of the stamps' clock in kHz (hipDeviceAttributeWallClockRate). */

@@ -49,7 +49,6 @@ struct bsp_plan {
     // SpMM sweep kernel (info.persistent == 3): sweep records (heads in
     // d_wgs, B words in d_ent_off, A words in d_aw).
     bsp::SpmmSweepRec* d_sweeps = nullptr;
-    int sweep_ax4 = 0;
 };
 
 namespace {
@@ -532,7 +531,6 @@ int make_spmm_sweep_plan(bsp_plan** out, const bsp_bsr_desc* a, int64_t N, int o
     in.step_entries = 2;
     in.stripes_per_unit = 1;
     in.units_rotated = sw.rotated;
-    p->sweep_ax4 = (int)env_int("BSP_SWEEP_AX4", 0);
     hipError_t e = upload((bsp::SpmmSweepHead**)&p->d_wgs, sw.heads);
     if (e == hipSuccess) e = upload(&p->d_sweeps, sw.sweeps);
     if (e == hipSuccess) e = upload(&p->d_ent_off, sw.bw);
@@ -675,8 +673,7 @@ int bsp_spmm(const bsp_plan* p, const uint16_t* a_vals, const uint16_t* b, int64
         sa.lda = (int32_t)p->C;
         sa.N = (int32_t)p->N;
         sa.skips = args.skips;
-        e = bsp::launch_spmm_sweep(sa, p->out_dtype == BSP_DTYPE_BF16, p->sweep_ax4 != 0, p->info.grid,
-                                   (hipStream_t)stream);
+        e = bsp::launch_spmm_sweep(sa, p->out_dtype == BSP_DTYPE_BF16, p->info.grid, (hipStream_t)stream);
     } else if (p->info.persistent) {
         bsp::SpmmStreamArgs sa{};
         sa.a = a_vals;

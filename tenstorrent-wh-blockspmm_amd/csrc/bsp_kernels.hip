@@ -78,6 +78,24 @@ struct TimelineRegs {
             buf[(int64_t)blockIdx.x * BSP_TIMELINE_SLOTS + l] = v;
     }
 };
+// Stamps stored straight to the attached buffer by lane 0 of wave 0, for a
+// kernel whose wave 0 waits for none of its own vector-memory operations
+// (the persistent SpMM, where wave 0 is an MFMA wave: it issues stores and no
+// loads, and waits only for its LDS reads) and whose LDS is sized to an exact
+// occupancy (two 80 KB workgroups per compute unit: an LDS log would leave
+// room for one).  Slots a workgroup does not reach keep what the buffer held.
+struct TimelineGlobal {
+    uint64_t* row = nullptr;
+    __device__ __forceinline__ TimelineGlobal() {
+        uint64_t* buf = g_timeline_buf;
+        if (buf && (int64_t)blockIdx.x < g_timeline_cap) row = buf + (int64_t)blockIdx.x * BSP_TIMELINE_SLOTS;
+        mark(0);
+    }
+    __device__ __forceinline__ void mark(int i) {
+        if (row && threadIdx.x == 0 && i >= 0 && i < BSP_TIMELINE_SLOTS) row[i] = wall_clock64();
+    }
+    __device__ __forceinline__ void flush() { mark(BSP_TIMELINE_SLOTS - 1); }
+};
 // No log (kernels with no LDS to spare whose stamps sit in lambdas: the
 // two-pipeline persistent variants, which no plan takes by default).
 struct TimelineNone {
@@ -95,6 +113,7 @@ struct TimelinePick<true> {
 // LDS_LOG: the kernel has 512 bytes of LDS to spare.
 #define BSP_TL_DECL(LDS_LOG) typename TimelinePick<(LDS_LOG)>::type bsp_tl
 #define BSP_TL_DECL_REGS() TimelineRegs bsp_tl
+#define BSP_TL_DECL_GLOBAL() TimelineGlobal bsp_tl
 #define BSP_TL_MARK(i) bsp_tl.mark(i)
 #define BSP_TL_FLUSH() bsp_tl.flush()
 // Whether the launch leaves out a part of the work (kSkip* bit of the
@@ -103,6 +122,7 @@ struct TimelinePick<true> {
 #else
 #define BSP_TL_DECL(LDS_LOG) ((void)0)
 #define BSP_TL_DECL_REGS() ((void)0)
+#define BSP_TL_DECL_GLOBAL() ((void)0)
 #define BSP_TL_MARK(i) ((void)0)
 #define BSP_TL_FLUSH() ((void)0)
 #define BSP_SKIP(p, bit) false
@@ -943,6 +963,8 @@ __global__ __launch_bounds__(64 * NW, RW <= 4 && S == 3 ? 2 : 1) void spmm_group
     auto issue = [&](int e, int stage) {
         uint32_t bw, aw;
         words.get(e, lane, bw, aw);
+        // Both operands left out: no loads at all (the waits then pass at once).
+        if (BSP_SKIP(p, kSkipSparseRead) && BSP_SKIP(p, kSkipDenseRead)) return;
         if (BSP_SKIP(p, kSkipSparseRead)) aw = aw_first;
         if (BSP_SKIP(p, kSkipDenseRead)) bw = bw_first;
         const uint16_t* ablk = p.a + (int64_t)aw * 32;
@@ -1210,7 +1232,7 @@ __global__ __launch_bounds__(64 * (4 * SR + 1 + NBW) * PIPES) void spmm_stream_k
     constexpr int XCHG = PIPES > 1 ? 4 * NTW * 16 * 64 * 4 : 0;  // fp32 tile of the shared unit
     static_assert(PIPES == 1 || PIPES == 2, "pipelines");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[PIPES * PIPE_LDS + XCHG];
-    BSP_TL_DECL(PIPES * PIPE_LDS + XCHG + 8 * 64 <= 163840);
+    BSP_TL_DECL_GLOBAL();
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1524,41 +1546,35 @@ __global__ __launch_bounds__(64 * (4 * SR + 1 + NBW) * PIPES) void spmm_stream_k
 // workgroups of an XCD walk K together: a 32-row slice of B is fetched from
 // HBM by the first unit that needs it and served from the XCD's L2 to the
 // others shortly after, where a unit-by-unit walk spreads a slice's uses over
-// the whole launch and the A and C streams evict it in between.  Every L2
-// miss, whether the Infinity Cache or HBM serves it, costs the same on
-// MI355X (an L2-missing stream of a 64-256 MB region runs at 7.5 TB/s, one of
-// 1 GB at 7.4), so the misses are what the launch pays for.
-//   - 8 waves, two groups of four; group g owns slots 8g .. 8g+7, and wave
-//     4g + w owns columns 32w .. 32w+31 of each of them: 8 x 16 fp32
-//     accumulator registers per lane for the group's units;
-//   - every wave also loads: 1 KB of each entry's 8 KB B slice (the B slice
-//     layout of BSlice) and 256 bytes of its 2 KB A sub-block (the row layout
-//     of a_row_load_offset), into a ring of S stages of 10 KB;
-//   - step k (k = 0, 2, 4, ...) has one barrier: each wave waits for its own
-//     loads of entries k and k+1, passes the barrier, refills the stages of
-//     entries k-2 and k-1 with entries k+S-2 and k+S-1, then reads the
-//     operands of entries k and k+1 and multiplies them (only the four waves
-//     of each entry's group).  The operands are not double-buffered: the 128
-//     accumulator registers leave no room for a second set, and the launch is
-//     bound by its L2 misses, not by the LDS read latency this exposes;
-//   - when the last entry of a sweep is multiplied, each wave stores its
-//     columns of the sweep's units and clears its accumulators.
-// The entry's slot rides in its B word (bits 56-59, bit 60 marking the skip
-// entry that pads a sweep to an even count: loaded, never multiplied); each
-// wave keeps the slots of the entries in flight in a 64-bit shift register,
-// four bits each, pushed at issue and read S-1 and S-2 issues later.
-template <int S, bool OUT_BF16, bool AX4>
-__global__ __launch_bounds__(512, 1) void spmm_sweep_kernel(SpmmSweepArgs p) {
+// the whole launch and the A and C streams evict it in between.
+//   - waves 0-7 (MFMA waves), two groups of four: group g owns slots
+//     8g .. 8g+7 and wave 4g + w columns 32w .. 32w+31 of each of them, 8 x 16
+//     fp32 accumulator registers per lane; they issue no loads;
+//   - wave 8 (A loader) and waves 9 .. 8+NBW (B loaders) run the persistent
+//     kernel's ring (stream_loader2: two entries per barrier, entry words by
+//     scalar loads two chunks ahead) over the workgroup's merged stream;
+//   - the MFMA waves read the same stream's B words by scalar loads (a
+//     step's two, one step ahead, in the scalar cache after the loaders'
+//     reads): the slot (bits 56-58 within the group) picks the accumulator,
+//     the skip bit (60) marks a padding entry (loaded, never multiplied);
+//   - right after the products of a unit's last entry (the last bit of its
+//     word, bit 61) the waves of its group store their columns of its tile,
+//     so that the output streams out while the walk goes on instead of in
+//     one burst at its end; units without entries are stored as zeros when
+//     their sweep opens, and the accumulators are cleared between sweeps.
+// A step reads and multiplies this group's entries among its two one after
+// the other, into one operand set (the 128 accumulators leave no registers
+// for a second); the plan gives the two groups alternate units, longest
+// first, so that their entry counts are alike.
+template <int SB, int SA, int NBW, bool OUT_BF16>
+__global__ __launch_bounds__(64 * (8 + 1 + NBW), 1) void spmm_sweep_kernel(SpmmSweepArgs p) {
     using namespace spmm_detail;
-    static_assert(S % 2 == 0 && S >= 6 && S <= 16, "two entries per step: an even ring of 6 to 16 stages");
-    static_assert(2 * (S - 2) + 2 < 64, "vmcnt budget");
+    static_assert(SB % 2 == 0 && SA % 2 == 0 && SB <= 16 && SA <= 16, "two entries per step");
     constexpr int TN = kSweepTile;
-    using Loader = BSliceLoader<TN, 8>;  // one 1 KB piece per wave
-    constexpr int B_BYTES = Loader::BYTES;
-    constexpr int A_RING = S * kA_BYTES;
-    constexpr int WORDS = A_RING + S * B_BYTES;  // per wave: two word chunks
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[WORDS + 8 * 2 * kSweepWordChunk];
-    BSP_TL_DECL(true);
+    using Loader = BSliceLoader<TN, NBW>;
+    constexpr int A_RING = SA * kA_BYTES;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[A_RING + SB * Loader::BYTES];
+    BSP_TL_DECL_GLOBAL();
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1567,45 +1583,38 @@ __global__ __launch_bounds__(512, 1) void spmm_sweep_kernel(SpmmSweepArgs p) {
     const int n = wg.n;
     const uint32_t lds0 = lds_address(smem);
 
-    // ---- loads: B piece `wave` and A bytes 256*wave .. 256*wave+255 of the
-    // stage (row r = x / 64 of the row layout, slot (x % 64) / 16 holding
-    // chunk slot ^ ((r >> 2) & 3)).
-    const Loader ld(wave, lane, p.ldb);
-    uint32_t a_voff;
-    if constexpr (AX4) {
-        // Waves 0 and 1 load rows 16w .. 16w+15 of the A sub-block (1 KB each,
-        // a_row_load_offset): two loads per entry for them, one for the
-        // others (their waits count accordingly).
-        a_voff = wave < 2 ? (uint32_t)(2 * a_row_load_offset(wave, lane, p.lda)) : 0u;
-    } else {
-        const int x = 256 * wave + 4 * lane;
-        const int r = x >> 6, c = ((x & 63) >> 4) ^ ((r >> 2) & 3);
-        a_voff = (uint32_t)(2 * (r * p.lda + 8 * c) + (x & 15));
+    if (wave == 8) {
+        // A loader: load j (1 KB) covers rows 16j .. 16j+15 of the sub-block
+        // (the row layout of a_row_load_offset).
+        uint32_t a_voff[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) a_voff[j] = 2 * a_row_load_offset(j, lane, p.lda);
+        auto issue_a = [&](int e, uint32_t w) {
+            if (BSP_SKIP(p, kSkipSparseRead)) return;  // left out: the wave's waits pass at once
+            const uint16_t* ablk = p.a + (int64_t)w * 32;
+            const uint32_t dst = lds0 + (uint32_t)(e % SA) * kA_BYTES;
+            gl_lds16_s(a_voff[0], ablk, dst);
+            gl_lds16_s(a_voff[1], ablk, dst + 1024);
+        };
+        stream_loader2<SA, 2>(n, head->aw, p.aw + wg.w_begin, issue_a);
+        return;
     }
-    // (An operand left out by the instrumented build is read, for every
-    // entry, where the workgroup's first entry reads it -- an L2 hit after
-    // the first, and a different line per workgroup: the wave's waits count
-    // both operands' loads, so the loads stay.)
-    int64_t bw_first = 0;
-    uint32_t aw_first = 0;
-    if (BSP_SKIP(p, kSkipSparseRead | kSkipDenseRead)) {
-        bw_first = load_const(&head->bw[0]);
-        aw_first = load_const(&head->aw[0]);
+    if (wave > 8) {
+        const int wb = wave - 9;
+        const Loader ld(wb, lane, p.ldb);
+        const uint32_t b_lds = lds0 + A_RING + wb * Loader::BI * 1024;
+        auto issue_b = [&](int e, int64_t w) {
+            if (BSP_SKIP(p, kSkipDenseRead)) return;  // left out: the wave's waits pass at once
+            const uint16_t* bpan = p.b + (int64_t)(uint32_t)w * p.ldb + (int32_t)((w >> 32) & 0xffffff);
+            const uint32_t dst = b_lds + (uint32_t)(e % SB) * Loader::BYTES;
+#pragma unroll
+            for (int j = 0; j < Loader::BI; ++j) gl_lds16_s(ld.voff[j], bpan, dst + j * 1024);
+        };
+        stream_loader2<SB, Loader::BI>(n, head->bw, p.bw + wg.w_begin, issue_b);
+        return;
     }
-    auto issue = [&](int e, int64_t bwd, uint32_t awd) __attribute__((always_inline)) {
-        const uint32_t st = (uint32_t)(e % S);
-        if (BSP_SKIP(p, kSkipDenseRead)) bwd = bw_first;
-        if (BSP_SKIP(p, kSkipSparseRead)) awd = aw_first;
-        const uint16_t* bpan = uniform_ptr(p.b + (int64_t)(uint32_t)bwd * p.ldb + (int32_t)((bwd >> 32) & 0xffffff));
-        const uint16_t* ablk = uniform_ptr(p.a + (int64_t)awd * 32);
-        gl_lds16_s(ld.voff[0], bpan, lds0 + A_RING + st * B_BYTES + wave * 1024);
-        if constexpr (AX4) {
-            if (wave < 2) gl_lds16_s(a_voff, ablk, lds0 + st * kA_BYTES + wave * 1024);
-        } else {
-            gl_lds4_s(a_voff, ablk, lds0 + st * kA_BYTES + wave * 256);
-        }
-    };
-    // ---- products.
+
+    // ---- MFMA waves.
     const int l32 = lane & 31, q = lane >> 5;
     const int group = wave >> 2, wc = wave & 3;
     const BReads<TN, 1> brd(lane, wc * 32, false);
@@ -1623,38 +1632,56 @@ __global__ __launch_bounds__(512, 1) void spmm_sweep_kernel(SpmmSweepArgs p) {
     zero_acc();
     const SpmmSweepRec* sweeps = p.sweeps + wg.s_begin;
     int sw = 0, left = 0;
-    auto store_sweep = [&](int si) __attribute__((always_inline)) {
-        if (BSP_SKIP(p, kSkipWrite)) return;
-        // Wait states between the last product (asm, unseen by the
-        // compiler's hazard checks) and the reads of its result: more than a
-        // 16-pass product's 18.
-        __asm__ volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
-        const SpmmSweepHalf h = load_const(&sweeps[si].half[group]);
+    SpmmSweepHalf h{};  // this group's units in the open sweep
+    // Stores this wave's columns of a unit's tile (t: its accumulator, or zeros).
+    auto store_tile = [&](const f32x16& t, int32_t stripe, int32_t n0) __attribute__((always_inline)) {
+        const int64_t row0 = (int64_t)stripe * 32;
+        const int64_t col = n0 + wc * 32 + l32;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            if (h.row[j] < 0) continue;
-            const int64_t row0 = (int64_t)h.row[j] * 32;
-            const int64_t col = h.n0[j] + wc * 32 + l32;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int64_t row = row0 + 8 * (v >> 2) + 4 * q + (v & 3);
-                if (OUT_BF16)
-                    store_out(&((uint16_t*)p.c)[row * p.ldc + col], f32_to_bf16_rne(acc[j][v]));
-                else
-                    store_out(&((float*)p.c)[row * p.ldc + col], acc[j][v]);
-            }
+        for (int v = 0; v < 16; ++v) {
+            const int64_t row = row0 + 8 * (v >> 2) + 4 * q + (v & 3);
+            if (OUT_BF16)
+                store_out(&((uint16_t*)p.c)[row * p.ldc + col], f32_to_bf16_rne(t[v]));
+            else
+                store_out(&((float*)p.c)[row * p.ldc + col], t[v]);
         }
     };
-    // Moves to the next sweep with entries, storing the zero tiles of sweeps
-    // without any on the way.
+    // Stores the tile of the unit in `slot` after its last entry's products.
+    auto store_slot = [&](int slot) __attribute__((always_inline)) {
+        if (BSP_SKIP(p, kSkipWrite)) return;
+        // Wait states between the products (asm, unseen by the compiler's
+        // hazard checks; twelve at the end of their block) and the reads of
+        // their result: more than a 16-pass product's 18.
+        __asm__ volatile("s_nop 7\n\ts_nop 7" ::: "memory");
+        switch (slot) {
+#define BSP_SWEEP_STORE(J) \
+            case J: store_tile(acc[J], h.row[J], h.n0[J]); break;
+            BSP_SWEEP_STORE(0) BSP_SWEEP_STORE(1) BSP_SWEEP_STORE(2) BSP_SWEEP_STORE(3)
+            BSP_SWEEP_STORE(4) BSP_SWEEP_STORE(5) BSP_SWEEP_STORE(6) BSP_SWEEP_STORE(7)
+#undef BSP_SWEEP_STORE
+            default: break;
+        }
+    };
+    // Opens the next sweep with entries: its units' records, and zero tiles
+    // for its units without entries (all of them in a sweep of none).
+    struct Head4 {
+        int32_t count, empty, pad[2];
+    };
     auto open = [&] () __attribute__((always_inline)) {
         while (sw < wg.n_sweeps) {
-            const int cnt = load_const(&sweeps[sw].count);
-            if (cnt > 0) {
-                left = cnt;
+            const Head4 r = load_const((const Head4*)&sweeps[sw]);
+            h = load_const(&sweeps[sw].half[group]);
+            const int empty = (r.empty >> (8 * group)) & 0xff;
+            if (empty != 0 && !BSP_SKIP(p, kSkipWrite)) {
+                const f32x16 zero = {};
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if ((empty >> j) & 1) store_tile(zero, h.row[j], h.n0[j]);
+            }
+            if (r.count > 0) {
+                left = r.count;
                 return;
             }
-            store_sweep(sw);
             ++sw;
         }
         left = 0;
@@ -1664,45 +1691,47 @@ __global__ __launch_bounds__(512, 1) void spmm_sweep_kernel(SpmmSweepArgs p) {
     struct Ops {
         u32x4 a[2];
         u32x4 b[2][1];
-        int slot;  // accumulator of this wave (0-7), or -1: another group's entry or a skip entry
     };
-    auto read = [&](int k, uint32_t code, Ops& o) __attribute__((always_inline)) {
-        o.slot = (code & 16u) == 0 && (int)((code >> 3) & 1u) == group ? (int)(code & 7u) : -1;
-        if (o.slot >= 0) {
-            const uint8_t* as = smem + (k % S) * kA_BYTES;
-            o.a[0] = *(const u32x4*)(as + a_rd0);
-            o.a[1] = *(const u32x4*)(as + a_rd1);
-            brd.read(smem + A_RING + (k % S) * B_BYTES, o.b);
-        }
+    auto read = [&](int k, Ops& o) __attribute__((always_inline)) {
+        const uint8_t* as = smem + (k % SA) * kA_BYTES;
+        o.a[0] = *(const u32x4*)(as + a_rd0);
+        o.a[1] = *(const u32x4*)(as + a_rd1);
+        brd.read(smem + A_RING + (k % SB) * Loader::BYTES, o.b);
     };
     // The products of one entry on the accumulator of its slot, as a single
-    // asm block that holds the dispatch (compare and branch on the slot) and
-    // takes all eight accumulators as in-out operands.  Any dispatch the
-    // compiler sees -- a switch, or a chain of ifs, on builtin or asm
+    // asm block that holds the dispatch (a three-level tree on the slot's
+    // bits) and takes all eight accumulators as in-out operands.  Any dispatch
+    // the compiler sees -- a switch, or a chain of ifs, on builtin or asm
     // products -- leaves it a join where each accumulator is either updated
     // or not, and it resolves those joins by copying accumulators between two
-    // register sets: hundreds of v_mov per step, which set the kernel's pace.
-    // Here every acc[j] keeps one register, updated in place (the accumulate
-    // form: destination = source C).  The compiler's hazard checks do not see
-    // into the block: the products need two wait states after a vector ALU
-    // write of source C (the zeroing after a sweep: s_nop 1 at the block's
-    // start), none between products on one accumulator (source C exactly
-    // overlapping the previous destination), and the stores that read the
-    // results are preceded by explicit wait states (store_sweep).
-    auto multiply = [&](const Ops& o) __attribute__((always_inline)) {
+    // register sets.  Here every acc[j] keeps one register, updated in place
+    // (the accumulate form: destination = source C).  The compiler's hazard
+    // checks do not see into the block: the products need two wait states
+    // after a vector ALU write of source C (the zeroing after a sweep: s_nop 1
+    // at the block's start), none between products on one accumulator (source
+    // C exactly overlapping the previous destination), and the stores that
+    // read the results are preceded by explicit wait states (store_sweep).
+    // The block ends with twelve wait states, so that the next LDS read into
+    // the same operand registers never overwrites a source the products may
+    // still be reading.
+    auto multiply = [&](const Ops& o, int slot) __attribute__((always_inline)) {
         if (BSP_SKIP(p, kSkipCompute)) return;
-        const int slot = __builtin_amdgcn_readfirstlane(o.slot);
         __asm__ volatile(
             "s_nop 1\n\t"
-            "s_cmp_eq_u32 %12, 0\n\ts_cbranch_scc1 .Lsw0_%=\n\t"
-            "s_cmp_eq_u32 %12, 1\n\ts_cbranch_scc1 .Lsw1_%=\n\t"
-            "s_cmp_eq_u32 %12, 2\n\ts_cbranch_scc1 .Lsw2_%=\n\t"
-            "s_cmp_eq_u32 %12, 3\n\ts_cbranch_scc1 .Lsw3_%=\n\t"
-            "s_cmp_eq_u32 %12, 4\n\ts_cbranch_scc1 .Lsw4_%=\n\t"
-            "s_cmp_eq_u32 %12, 5\n\ts_cbranch_scc1 .Lsw5_%=\n\t"
-            "s_cmp_eq_u32 %12, 6\n\ts_cbranch_scc1 .Lsw6_%=\n\t"
-            "s_cmp_eq_u32 %12, 7\n\ts_cbranch_scc1 .Lsw7_%=\n\t"
-            "s_branch .Lswd_%=\n"
+            "s_bitcmp1_b32 %12, 2\n\ts_cbranch_scc1 .Lsw4567_%=\n\t"
+            "s_bitcmp1_b32 %12, 1\n\ts_cbranch_scc1 .Lsw23_%=\n\t"
+            "s_bitcmp1_b32 %12, 0\n\ts_cbranch_scc1 .Lsw1_%=\n\t"
+            "s_branch .Lsw0_%=\n"
+            ".Lsw23_%=:\n\t"
+            "s_bitcmp1_b32 %12, 0\n\ts_cbranch_scc1 .Lsw3_%=\n\t"
+            "s_branch .Lsw2_%=\n"
+            ".Lsw4567_%=:\n\t"
+            "s_bitcmp1_b32 %12, 1\n\ts_cbranch_scc1 .Lsw67_%=\n\t"
+            "s_bitcmp1_b32 %12, 0\n\ts_cbranch_scc1 .Lsw5_%=\n\t"
+            "s_branch .Lsw4_%=\n"
+            ".Lsw67_%=:\n\t"
+            "s_bitcmp1_b32 %12, 0\n\ts_cbranch_scc1 .Lsw7_%=\n\t"
+            "s_branch .Lsw6_%=\n"
 #define BSP_SWEEP_CASE(J)                                              \
             ".Lsw" #J "_%=:\n\t"                                      \
             "v_mfma_f32_32x32x16_bf16 %" #J ", %8, %10, %" #J "\n\t"   \
@@ -1711,161 +1740,58 @@ __global__ __launch_bounds__(512, 1) void spmm_sweep_kernel(SpmmSweepArgs p) {
             BSP_SWEEP_CASE(0) BSP_SWEEP_CASE(1) BSP_SWEEP_CASE(2) BSP_SWEEP_CASE(3)
             BSP_SWEEP_CASE(4) BSP_SWEEP_CASE(5) BSP_SWEEP_CASE(6) BSP_SWEEP_CASE(7)
 #undef BSP_SWEEP_CASE
-            ".Lswd_%=:"
+            ".Lswd_%=:\n\t"
+            "s_nop 7\n\ts_nop 3"
             : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), "+v"(acc[4]), "+v"(acc[5]),
               "+v"(acc[6]), "+v"(acc[7])
             : "v"(o.a[0]), "v"(o.a[1]), "v"(o.b[0][0]), "v"(o.b[1][0]), "s"(slot)
             : "scc");
     };
-    auto fence_sched = [] { __builtin_amdgcn_sched_barrier(0); };
-
-    // ---- the ring.  Entry words reach each wave through its own LDS copy,
-    // loaded by DMA 64 entries (a chunk) at a time into two buffers: the
-    // next chunk is fetched when the issue position enters a chunk, and the
-    // words of a step's refills are read from LDS one step earlier.  No
-    // scalar load is in flight while the ring runs: every wave reads LDS in
-    // every step, and the wait for those reads (s_waitcnt lgkmcnt) would also
-    // wait for a scalar load, putting a memory round trip on every refill of
-    // a scalar word chunk (the reason the loader waves of spmm_stream_kernel
-    // read no LDS).  A chunk's two loads, issued at step kc after the step's
-    // refills, are younger than the entries steps kc+2 .. kc+S-2 wait for, so
-    // those waits allow two more loads in flight.  The first S entries' words
-    // come from the head.  Every sweep has an even number of entries (the plan
-    // pads an odd one with a skip entry), so n is even and a step's two
-    // entries belong to one sweep.
-    const uint32_t wbuf = lds0 + WORDS + wave * 2 * kSweepWordChunk;
-    auto fetch_chunk = [&](int c) __attribute__((always_inline)) {
-        // B words (512 bytes: lanes 0-31, 16 each) at +0, A words (256 bytes)
-        // at +512 of buffer c & 1.  In bounds: a chunk is fetched only if it
-        // holds entries of this stream, and the arrays are padded by 64 words.
-        const uint32_t dst = wbuf + (uint32_t)(c & 1) * kSweepWordChunk;
-        const int64_t* bsrc = uniform_ptr(p.bw + wg.w_begin + 64 * c);
-        const uint32_t* asrc = uniform_ptr(p.aw + wg.w_begin + 64 * c);
-        if (lane < 32) gl_lds16_s((uint32_t)lane * 16, bsrc, dst);
-        gl_lds4_s((uint32_t)lane * 4, asrc, dst + 512);
+    auto lds_done = [] { __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); };
+    // Step k (k = 0, 2, 4, ...; the loaders' barrier for entries k and k+1):
+    // read and multiply this group's entries among k and k+1.
+    // This group's entry among a step's two: its slot, or -1.
+    auto mine = [&](int64_t w) __attribute__((always_inline)) {
+        const uint32_t code = (uint32_t)((uint64_t)w >> kSweepSlotShift) & 31u;
+        return (code & 16u) == 0 && (int)(code >> 3) == group ? (int)(code & 7u) : -1;
     };
-    // Words of entry e, from its chunk's buffer.
-    auto words_at = [&](int e, int64_t& bwd, uint32_t& awd) __attribute__((always_inline)) {
-        const uint8_t* buf = smem + (WORDS + wave * 2 * kSweepWordChunk) + ((e >> 6) & 1) * kSweepWordChunk;
-        const uint64_t b64 = *(const uint64_t*)(buf + 8 * (e & 63));
-        const uint32_t a32 = *(const uint32_t*)(buf + 512 + 4 * (e & 63));
-        bwd = (int64_t)(((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(b64 >> 32)) << 32) |
-                        __builtin_amdgcn_readfirstlane((uint32_t)b64));
-        awd = __builtin_amdgcn_readfirstlane(a32);
-    };
-    // The entries in flight: their slots (4 bits each, the last issued in
-    // bits 0-3) and skip flags (the last issued in bit 0).
-    uint64_t slots = 0;
-    uint32_t skips = 0;
-    auto push = [&](bool live, int64_t bwd) __attribute__((always_inline)) {
-        const uint64_t code = (uint64_t)bwd >> kSweepSlotShift;
-        slots = (slots << 4) | (live ? code & 15u : 0u);
-        skips = (skips << 1) | (live ? (uint32_t)(code >> 4) & 1u : 1u);
-    };
-    // Slot and skip flag of the entry issued `age` issues ago, as read()'s code.
-    auto code_at = [&](int age) __attribute__((always_inline)) {
-        return (uint32_t)((slots >> (4 * age)) & 15u) | (((skips >> age) & 1u) << 4);
-    };
-    // Chunks 0 and 1 first: older than every entry load, so the first wait
-    // covers them.
-    if (n > 0) fetch_chunk(0);
-    if (n > 64) fetch_chunk(1);
-    {
-        const int64_t* hb = head->bw;
-        const uint32_t* ha = head->aw;
-        struct W8B {
-            int64_t w[8];
-        };
-        struct W8A {
-            uint32_t w[8];
-        };
-        const W8B b0 = load_const((const W8B*)hb), b1 = load_const((const W8B*)hb + 1);
-        const W8A a0 = load_const((const W8A*)ha), a1 = load_const((const W8A*)ha + 1);
-#pragma unroll
-        for (int e = 0; e < S; ++e) {
-            const int64_t bwd = e < 8 ? b0.w[e] : b1.w[e - 8];
-            const uint32_t awd = e < 8 ? a0.w[e] : a1.w[e - 8];
-            if (e < n) issue(e, bwd, awd);
-            push(e < n, bwd);
+    auto step = [&](int k, int64_t w0, int64_t w1) __attribute__((always_inline)) {
+        barrier_no_fence();
+        const int s0 = mine(w0), s1 = mine(w1);
+        Ops o;
+        if (s0 >= 0) {
+            read(k, o);
+            lds_done();
+            multiply(o, s0);
+            if (w0 & kSweepLast) store_slot(s0);  // the unit's last entry
         }
-    }
-    // After the issues of step k the entries k .. k+S-1 are the last S issued:
-    // entry k is S-1 issues old, entry k+1 S-2.  The words of the next step's
-    // refills (entries k+S, k+S+1) are read with the operands.
-    int64_t nb0 = 0, nb1 = 0;
-    uint32_t na0 = 0, na1 = 0;
-    auto run_pair = [&](int k) __attribute__((always_inline)) {
-        Ops o0, o1;
-        if (k + S < n) words_at(k + S, nb0, na0);
-        if (k + S + 1 < n) words_at(k + S + 1, nb1, na1);
-        read(k, code_at(S - 1), o0);
-        read(k + 1, code_at(S - 2), o1);
-        fence_sched();
-        multiply(o0);
-        multiply(o1);
-        fence_sched();
+        if (s1 >= 0) {
+            read(k + 1, o);
+            lds_done();
+            multiply(o, s1);
+            if (w1 & kSweepLast) store_slot(s1);
+        }
         left -= 2;
         if (left == 0) {
-            store_sweep(sw);
             zero_acc();
             ++sw;
             open();
         }
     };
-    // Loads per entry of this wave: 2 (B piece and A piece; with AX4 only
-    // waves 0 and 1 load A), else 1.
-    const bool two = !AX4 || wave < 2;
-    if (n > 0) {
-        if (two)
-            wait_stages<2, S - 2>(max(0, min(S, n) - 2));  // entries 0 and 1 (and chunks 0, 1) landed
-        else
-            wait_stages<1, S - 2>(max(0, min(S, n) - 2));
-        barrier_no_fence();
-        BSP_TL_MARK(1);
-        run_pair(0);
-    }
-    int kc = -2 * S;  // step of the last chunk fetch
-    for (int k = 2; k < n; k += 2) {
-        const int e = k + S - 2;
-        const bool chunk_young = k - kc <= S - 2;
-        if (e + 1 < n) {
-            if (two) {
-                if (chunk_young)
-                    wait_vmcnt<2 * (S - 4) + 2>();  // entries k, k+1 landed
-                else
-                    wait_vmcnt<2 * (S - 4)>();
-            } else {
-                if (chunk_young)
-                    wait_vmcnt<(S - 4) + 2>();
-                else
-                    wait_vmcnt<S - 4>();
-            }
-            barrier_no_fence();
-            issue(e, nb0, na0);
-            issue(e + 1, nb1, na1);
-            if ((e & 63) == 0 && e + 64 < n) {  // entering chunk e/64: fetch the next
-                fetch_chunk((e >> 6) + 1);
-                kc = k;
-            }
-        } else {
-            const int m = max(0, min(n, e) - (k + 2));
-            if (two) {
-                if (chunk_young)
-                    wait_stages<2, S - 4, 2>(m);
-                else
-                    wait_stages<2, S - 4>(m);
-            } else {
-                if (chunk_young)
-                    wait_stages<1, S - 4, 2>(m);
-                else
-                    wait_stages<1, S - 4>(m);
-            }
-            barrier_no_fence();
-        }
-        push(e < n, nb0);
-        push(e + 1 < n, nb1);
-        run_pair(k);
+    // The stream's B words, two (a step's) at a time by a scalar load one step
+    // ahead, waited for with the step's LDS reads (the arrays are padded past
+    // every stream's end).
+    struct W2 {
+        int64_t w[2];
+    };
+    const W2* wp = (const W2*)(p.bw + wg.w_begin);
+    W2 cur = load_const(wp);
+    for (int k = 0; k < n; k += 2) {
+        const W2 nxt = load_const(wp + k / 2 + 1);
+        step(k, cur.w[0], cur.w[1]);
+        if (k == 0) BSP_TL_MARK(1);
         if ((k & 7) == 0 && k < 8 * 60) BSP_TL_MARK(2 + (k >> 3));
+        cur = nxt;
     }
     if (wave == 0) BSP_TL_FLUSH();
 }
@@ -2686,15 +2612,15 @@ hipError_t launch_spmm_stream(const SpmmStreamArgs& a, const SpmmStreamVariant& 
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_spmm_sweep(const SpmmSweepArgs& a, bool out_bf16, bool ax4, int grid, hipStream_t stream) {
+hipError_t launch_spmm_sweep(const SpmmSweepArgs& a, bool out_bf16, int grid, hipStream_t stream) {
     if (grid <= 0) return hipSuccess;
-#define BSP_SWEEP_LAUNCH(OB, AX)                                                                                   \
-    hipLaunchKernelGGL((spmm_sweep_kernel<kSweepStages, OB, AX>), dim3(grid), dim3(64 * kSweepWaves), 0, stream, a)
-    if (out_bf16 && ax4) BSP_SWEEP_LAUNCH(true, true);
-    else if (out_bf16) BSP_SWEEP_LAUNCH(true, false);
-    else if (ax4) BSP_SWEEP_LAUNCH(false, true);
-    else BSP_SWEEP_LAUNCH(false, false);
-#undef BSP_SWEEP_LAUNCH
+    constexpr int NBW = kSweepWaves - 9;
+    if (out_bf16)
+        hipLaunchKernelGGL((spmm_sweep_kernel<kSweepStages, kSweepStages, NBW, true>), dim3(grid),
+                           dim3(64 * kSweepWaves), 0, stream, a);
+    else
+        hipLaunchKernelGGL((spmm_sweep_kernel<kSweepStages, kSweepStages, NBW, false>), dim3(grid),
+                           dim3(64 * kSweepWaves), 0, stream, a);
     return hipGetLastError();
 }
 

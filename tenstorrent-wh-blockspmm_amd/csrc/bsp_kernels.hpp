@@ -73,14 +73,12 @@ struct SpmmSweepArgs {
     int32_t pad;
 };
 
-// Ring stages of the sweep kernel: 14 stages of 10 KB (2 KB of A, 8 KB of
-// B), and per wave two 768-byte chunks of entry words (64 B words and 64 A
-// words each): 152 KB of a compute unit's 160 KB of LDS.
-constexpr int kSweepStages = 14;
-constexpr int kSweepWordChunk = 768;
-constexpr int kSweepWaves = 8;
+// The sweep kernel: rings of 16 stages (A 2 KB and B 8 KB each: all 160 KB
+// of a compute unit's LDS), eight MFMA waves, an A loader and two B loaders.
+constexpr int kSweepStages = 16;
+constexpr int kSweepWaves = 11;
 
-hipError_t launch_spmm_sweep(const SpmmSweepArgs& a, bool out_bf16, bool ax4, int grid, hipStream_t stream);
+hipError_t launch_spmm_sweep(const SpmmSweepArgs& a, bool out_bf16, int grid, hipStream_t stream);
 
 // Whether an SpMM plan takes the sweep kernel: 32x32-multiple blocks, N a
 // multiple of 128, at least 8 units (stripe x 128 columns) per compute unit

@@ -923,36 +923,59 @@ int build_spmm_sweep(const bsp_bsr_desc* a, int64_t N, int num_cus, SpmmSweep& s
                             sr.half[g].row[j] = -1;
                             sr.half[g].n0[j] = 0;
                         }
-                    std::vector<Entry> es;
-                    int slot = 0;
-                    for (size_t ui = (size_t)sw; ui < mine.size(); ui += (size_t)n_sw, ++slot) {
+                    // The sweep's k-th unit (longest first) takes slot
+                    // (k % 2) * 8 + k / 2, so that the two MFMA wave groups
+                    // (slots 0-7 and 8-15) get alternate units and similar
+                    // entry counts.
+                    std::vector<Entry> es[2];
+                    uint32_t used = 0;
+                    int k = 0;
+                    for (size_t ui = (size_t)sw; ui < mine.size(); ui += (size_t)n_sw, ++k) {
                         const Unit& u = mine[ui];
+                        const int slot = (k % 2) * 8 + k / 2;
+                        used |= 1u << slot;
                         sr.half[slot / 8].row[slot % 8] = u.row;
                         sr.half[slot / 8].n0[slot % 8] = u.n0;
                         const int64_t i = u.row / RS, sub = u.row % RS;
                         for (int64_t blk = a->indptr[i]; blk < a->indptr[i + 1]; ++blk)
                             for (int64_t t = 0; t < CS; ++t)
-                                es.push_back({(int64_t)a->indices[blk] * a->C + kSub * t,
-                                              (uint32_t)((blk * a->R * a->C + kSub * sub * a->C + kSub * t) / kSub),
-                                              slot, u.n0});
+                                es[slot / 8].push_back({(int64_t)a->indices[blk] * a->C + kSub * t,
+                                                        (uint32_t)((blk * a->R * a->C + kSub * sub * a->C + kSub * t) / kSub),
+                                                        slot, u.n0});
                     }
-                    if (slot == 0) continue;  // no units left for this sweep
-                    std::stable_sort(es.begin(), es.end(), [](const Entry& p, const Entry& q) { return p.brow < q.brow; });
-                    size_t off = 0;
+                    if (k == 0) continue;  // no units left for this sweep
+                    // The sweep's entries merged by first row of B (rotated to
+                    // start at kcol); each unit's last entry in stream order
+                    // carries the last bit (the kernel stores the unit's tile
+                    // after it); units with no entries are marked in the
+                    // record's empty mask.
+                    std::vector<Entry> e = es[0];
+                    e.insert(e.end(), es[1].begin(), es[1].end());
+                    std::stable_sort(e.begin(), e.end(), [](const Entry& p, const Entry& q) { return p.brow < q.brow; });
                     if (kcol > 0) {
-                        while (off < es.size() && es[off].brow < kcol) ++off;
-                        if (off == es.size()) off = 0;
-                        std::rotate(es.begin(), es.begin() + off, es.end());
+                        size_t off = 0;
+                        while (off < e.size() && e[off].brow < kcol) ++off;
+                        if (off == e.size()) off = 0;
+                        std::rotate(e.begin(), e.begin() + off, e.end());
                     }
-                    for (const Entry& e : es) {
-                        s.bw.push_back(e.brow | ((int64_t)e.n0 << 32) | ((int64_t)e.slot << kSweepSlotShift));
-                        s.aw.push_back(e.aw);
+                    uint32_t has = 0;
+                    std::vector<uint8_t> last(e.size(), 0);
+                    for (size_t i = e.size(); i-- > 0;)
+                        if (!(has & (1u << e[i].slot))) {
+                            has |= 1u << e[i].slot;
+                            last[i] = 1;
+                        }
+                    for (size_t i = 0; i < e.size(); ++i) {
+                        s.bw.push_back(e[i].brow | ((int64_t)e[i].n0 << 32) | ((int64_t)e[i].slot << kSweepSlotShift) |
+                                       (last[i] ? kSweepLast : 0));
+                        s.aw.push_back(e[i].aw);
                     }
-                    if (es.size() % 2) {  // pad to an even count
-                        s.bw.push_back(s.bw.back() | kSweepSkip);
+                    if (e.size() % 2) {  // pad to an even count
+                        s.bw.push_back((s.bw.back() | kSweepSkip) & ~kSweepLast);
                         s.aw.push_back(s.aw.back());
                     }
-                    sr.count = (int32_t)(es.size() + es.size() % 2);
+                    sr.count = (int32_t)(e.size() + e.size() % 2);
+                    sr.empty = (int32_t)(used & ~has);
                     s.sweeps.push_back(sr);
                     ++rec.n_sweeps;
                 }

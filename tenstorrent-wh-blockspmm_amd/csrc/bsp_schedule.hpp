@@ -221,7 +221,8 @@ struct SpmmSweepHalf {
 };
 struct SpmmSweepRec {
     int32_t count;     // entries of the sweep (0: its units are empty stripes, stored as zeros)
-    int32_t pad[3];
+    int32_t empty;     // bit j: the unit of slot j has no entries (its tile is stored as zeros)
+    int32_t pad[2];
     SpmmSweepHalf half[2];
 };
 static_assert(sizeof(SpmmSweepRec) == 144, "SpmmSweepRec layout is shared with the kernels");
@@ -238,11 +239,14 @@ struct SpmmSweepHead {
 static_assert(sizeof(SpmmSweepHead) == 320, "SpmmSweepHead layout is shared with the kernels");
 
 // B word of a sweep entry: first row of B (bits 0-31) | first output column
-// (bits 32-55) | slot (bits 56-59) | skip (bit 60).  Every sweep has an even
-// number of entries: an odd one is padded with a skip entry (a copy of its
-// last entry's words with the skip bit, loaded and not multiplied).
+// (bits 32-55) | slot (bits 56-59) | skip (bit 60) | last (bit 61: the last
+// entry of its unit in stream order).  Every sweep has an even number of
+// entries: an odd one is padded with a skip entry (a copy of its last entry's
+// words with the skip bit and without the last bit, loaded and not
+// multiplied).
 constexpr int kSweepSlotShift = 56;
 constexpr int64_t kSweepSkip = int64_t(1) << 60;
+constexpr int64_t kSweepLast = int64_t(1) << 61;
 constexpr int64_t kSweepMaxN = int64_t(1) << 24;
 
 struct SpmmSweep {

@@ -2,8 +2,9 @@
 every 32x32 sub-block product of every (stripe, 128-column tile) unit appears
 exactly once, each unit sits in exactly one slot of one sweep of one
 workgroup, sweeps hold at most 16 units and an even number of entries (a
-skip entry pads an odd one), entries of a sweep ascend in block column, and
-the entry words agree with the slot records.  The reference's host analysis
+skip entry pads an odd one), entries of a sweep ascend in block column,
+the entry words agree with the slot records, and each unit's last entry in
+stream order (only it) carries the last bit.  The reference's host analysis
 this replaces for such shapes: block_spmm/inc/host_code/
 bsr_spmm_multicore_load_balanced_new_DM.cpp:339-393."""
 import numpy as np
@@ -12,6 +13,7 @@ import pytest
 from helpers import W, bsr_of, capi
 
 SKIP = 1 << 60
+LAST = 1 << 61
 
 
 def _expected(a, N):
@@ -48,6 +50,13 @@ def _check(a, N, num_cus=256, col_groups=0):
             words = bw[e:e + cnt]
             brow = words & 0xFFFFFFFF
             assert np.all(np.diff(brow[(words & SKIP) == 0]) >= 0), "a sweep's entries ascend in block column"
+            # the last bit marks exactly each unit's final entry in stream order, never a skip entry
+            live_words = [int(wd) for wd in words if not wd & SKIP]
+            assert not any(int(wd) & LAST for wd in words if wd & SKIP)
+            final = {}
+            for i, wd in enumerate(live_words):
+                final[(wd >> 56) & 15] = i
+            assert {i for i, wd in enumerate(live_words) if wd & LAST} == set(final.values())
             for wd, av in zip(words, aw[e:e + cnt]):
                 if wd & SKIP:
                     continue
