@@ -14,13 +14,12 @@
  * plus:
  *   - time stamps: wave 0 of every workgroup of the persistent SpMM, sweep
  *     SpMM and one-shot SDDMM kernels records the 100 MHz wall clock
- *     (s_memrealtime) at fixed points of its work: the persistent SpMM
- *     stores each stamp to the caller's buffer at once (its wave 0 waits for
- *     none of its own memory operations, and its LDS is sized to two
- *     workgroups per compute unit with no byte to spare); the sweep SpMM
- *     keeps a log in LDS and the one-shot SDDMM in registers, flushed to the
- *     buffer when the workgroup ends (a scalar clock read per stamp, one
- *     512-byte store per workgroup);
+ *     (s_memrealtime) at fixed points of its work: the persistent and sweep
+ *     SpMM store each stamp to the caller's buffer at once (their wave 0
+ *     waits for none of its own memory operations, and their LDS has no byte
+ *     to spare); the one-shot SDDMM keeps its four stamps in registers and
+ *     writes them when the workgroup ends (a scalar clock read per stamp, one
+ *     store of 8 bytes per stamp);
  *   - skip switches (bsp_timeline_skip), off by default: with none set a
  *     launch does all of the work of the plain library's, bit for bit.
  *

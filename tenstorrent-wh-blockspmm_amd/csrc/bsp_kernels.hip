@@ -27,41 +27,15 @@ namespace bsp {
 
 // ---------------------------------------------------------------------------
 // Per-workgroup timeline (the instrumented build, BSP_TIMELINE; the slots are
-// listed in bsparse_timeline.h).  Lane 0 of wave 0 writes the wall clock
-// into a 64-word LDS log; when wave 0 ends, its lanes copy the log to the
-// attached buffer.  The log stays in LDS while the kernel runs so that no
-// stamp adds a global store, which would sit in the vector-memory queue of a
-// wave whose ring waits count its loads.
+// listed in bsparse_timeline.h).  Wave 0 of a workgroup takes the stamps.
 #ifdef BSP_TIMELINE
 __device__ uint64_t* g_timeline_buf = nullptr;
 __device__ int64_t g_timeline_cap = 0;
 
-// The LDS log (allocated only in the kernels that use it).
-__device__ __forceinline__ uint64_t* timeline_lds() {
-    __shared__ uint64_t log[BSP_TIMELINE_SLOTS];
-    return log;
-}
-
-struct TimelineLog {
-    uint64_t* log;
-    __device__ __forceinline__ TimelineLog() : log(timeline_lds()) {
-        if (threadIdx.x < BSP_TIMELINE_SLOTS) log[threadIdx.x] = 0;
-        mark(0);
-    }
-    __device__ __forceinline__ void mark(int i) {
-        if (threadIdx.x == 0 && i >= 0 && i < BSP_TIMELINE_SLOTS) log[i] = wall_clock64();
-    }
-    // Wave 0 only (its lanes copy the log; other waves never call it).
-    __device__ __forceinline__ void flush() {
-        mark(BSP_TIMELINE_SLOTS - 1);
-        uint64_t* buf = g_timeline_buf;
-        if (threadIdx.x < BSP_TIMELINE_SLOTS && buf && (int64_t)blockIdx.x < g_timeline_cap)
-            buf[(int64_t)blockIdx.x * BSP_TIMELINE_SLOTS + threadIdx.x] = log[threadIdx.x];
-    }
-};
-// The same with slots 0, 1, 2 and 63 held in registers, for a kernel whose
-// LDS is sized to an exact occupancy (the one-shot SDDMM: two workgroups of
-// 80 KB per compute unit, which a 512-byte log would halve).
+// Slots 0, 1, 2 and 63 held in registers and written when wave 0 ends, for a
+// kernel whose wave 0 waits for all of its loads at once and whose LDS is
+// sized to an exact occupancy (the one-shot SDDMM: two workgroups of 80 KB per
+// compute unit, which a log in LDS would halve).
 struct TimelineRegs {
     uint64_t t0 = 0, t1 = 0, t2 = 0;  // (scalars: a lane-indexed array would go to scratch)
     __device__ __forceinline__ TimelineRegs() { t0 = wall_clock64(); }
@@ -80,10 +54,11 @@ struct TimelineRegs {
 };
 // Stamps stored straight to the attached buffer by lane 0 of wave 0, for a
 // kernel whose wave 0 waits for none of its own vector-memory operations
-// (the persistent SpMM, where wave 0 is an MFMA wave: it issues stores and no
-// loads, and waits only for its LDS reads) and whose LDS is sized to an exact
-// occupancy (two 80 KB workgroups per compute unit: an LDS log would leave
-// room for one).  Slots a workgroup does not reach keep what the buffer held.
+// (the persistent and sweep SpMM, where wave 0 is an MFMA wave: it issues
+// stores and no loads, and waits only for its LDS reads; a stamp store in a
+// loader wave's queue would stretch the waits that count its loads) and whose
+// LDS has no bytes to spare (two 80 KB workgroups per compute unit, or one of
+// 160 KB).  Slots a workgroup does not reach keep what the buffer held.
 struct TimelineGlobal {
     uint64_t* row = nullptr;
     __device__ __forceinline__ TimelineGlobal() {
@@ -96,22 +71,6 @@ struct TimelineGlobal {
     }
     __device__ __forceinline__ void flush() { mark(BSP_TIMELINE_SLOTS - 1); }
 };
-// No log (kernels with no LDS to spare whose stamps sit in lambdas: the
-// two-pipeline persistent variants, which no plan takes by default).
-struct TimelineNone {
-    __device__ __forceinline__ void mark(int) {}
-    __device__ __forceinline__ void flush() {}
-};
-template <bool LDS_LOG>
-struct TimelinePick {
-    using type = TimelineNone;
-};
-template <>
-struct TimelinePick<true> {
-    using type = TimelineLog;
-};
-// LDS_LOG: the kernel has 512 bytes of LDS to spare.
-#define BSP_TL_DECL(LDS_LOG) typename TimelinePick<(LDS_LOG)>::type bsp_tl
 #define BSP_TL_DECL_REGS() TimelineRegs bsp_tl
 #define BSP_TL_DECL_GLOBAL() TimelineGlobal bsp_tl
 #define BSP_TL_MARK(i) bsp_tl.mark(i)
@@ -120,7 +79,6 @@ struct TimelinePick<true> {
 // kernel arguments, a wave-uniform scalar).
 #define BSP_SKIP(p, bit) (((p).skips & (bit)) != 0)
 #else
-#define BSP_TL_DECL(LDS_LOG) ((void)0)
 #define BSP_TL_DECL_REGS() ((void)0)
 #define BSP_TL_DECL_GLOBAL() ((void)0)
 #define BSP_TL_MARK(i) ((void)0)

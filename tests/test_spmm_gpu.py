@@ -149,7 +149,7 @@ def test_skewed_workload_full_size(monkeypatch, kernel, split):
     assert (info["n_split_rows"] > 0) == bool(split)
     if kernel == "sweep":
         # one workgroup per compute unit, 16 units each, one sweep
-        assert (info["grid"], info["waves"], info["stages"], info["n_items"]) == (256, 8, 14, 4096), info
+        assert (info["grid"], info["waves"], info["stages"], info["n_items"]) == (256, 11, 16, 4096), info
     if kernel == "persistent":
         # eight units per workgroup, the longest (101 entries) above a
         # workgroup's share: one workgroup per compute unit, four B loaders,
