@@ -231,6 +231,30 @@ __device__ __forceinline__ void gl_lds16_s(uint32_t voff_bytes, const void* sbas
         : "memory");
 }
 
+// The same with M0 = lds_base + IMM: one scalar add sets the LDS destination
+// (gl_lds16_s takes an add and a move).  The loader waves of the persistent
+// kernels issue several of these per entry, and a compute unit issues one
+// scalar instruction per cycle across all of its waves.
+template <int IMM>
+__device__ __forceinline__ void gl_lds16_si(uint32_t voff_bytes, const void* sbase, uint32_t lds_base) {
+    const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_base);
+    if constexpr (IMM == 0) {
+        __asm__ volatile(
+            "s_mov_b32 m0, %2\n\t"
+            "global_load_lds_dwordx4 %0, %1"
+            :
+            : "v"(voff_bytes), "s"(sbase), "s"(lds)
+            : "memory");
+    } else {
+        __asm__ volatile(
+            "s_add_u32 m0, %2, %3\n\t"
+            "global_load_lds_dwordx4 %0, %1"
+            :
+            : "v"(voff_bytes), "s"(sbase), "s"(lds), "n"(IMM)
+            : "memory", "scc");
+    }
+}
+
 // The same with 4 bytes per lane (lane i's dword lands at M0 + 4i).
 __device__ __forceinline__ void gl_lds4_s(uint32_t voff_bytes, const void* sbase, uint32_t lds_wave_base) {
     const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_wave_base);
@@ -1059,7 +1083,24 @@ struct BSliceLoader {
             voff[j] = (uint32_t)(2 * ((int64_t)r * ldb + 8 * (slot ^ (4 * (r & 3)))));
         }
     }
+    // Issues pieces J .. BI-1 of the slice at bpan into LDS at dst + 1 KB per piece.
+    template <int J = 0>
+    __device__ __forceinline__ void issue(const uint16_t* bpan, uint32_t dst) const {
+        if constexpr (J < BI) {
+            gl_lds16_si<J * 1024>(voff[J], bpan, dst);
+            issue<J + 1>(bpan, dst);
+        }
+    }
 };
+
+// First element of an entry's B slice: row (low 32 bits of the word) times
+// ldb plus the column (bits 32 .. 32+CB-1).  ldb < 2^26 (checked by the host),
+// so the product is one 32 x 32-bit multiply with a 64-bit result.
+template <int CB = 32>
+__device__ __forceinline__ const uint16_t* b_slice(const uint16_t* b, int64_t ldb, int64_t w) {
+    const uint32_t col = CB == 32 ? (uint32_t)((uint64_t)w >> 32) : (uint32_t)((uint64_t)w >> 32) & ((1u << CB) - 1u);
+    return b + ((uint64_t)(uint32_t)w * (uint32_t)ldb + col);
+}
 
 // One loader wave's side of the ring: issue(e, word) issues entry e's loads
 // (P per wave) into stage e % S; the wave takes part in the n barriers.  The
@@ -1259,10 +1300,10 @@ __global__ __launch_bounds__(64 * (4 * SR + 1 + NBW) * PIPES) void spmm_stream_k
         }
         auto issue_a = [&](int e, uint32_t w) {
             if (BSP_SKIP(p, kSkipSparseRead)) return;  // left out: the wave's waits pass at once
-            const uint16_t* ablk = p.a + (int64_t)w * 32;
+            const uint16_t* ablk = p.a + (uint64_t)w * 32;
             const uint32_t dst = lds0 + (uint32_t)(e % SA) * A_STAGE;
-            gl_lds16_s(a_voff[0], ablk, dst);
-            gl_lds16_s(a_voff[1], ablk, dst + 1024);
+            gl_lds16_si<0>(a_voff[0], ablk, dst);
+            gl_lds16_si<1024>(a_voff[1], ablk, dst);
         };
         if constexpr (EPS == 2)
             stream_loader2<SA, 2>(n, head->aw, p.aw + wg.w_begin, issue_a);
@@ -1277,10 +1318,7 @@ __global__ __launch_bounds__(64 * (4 * SR + 1 + NBW) * PIPES) void spmm_stream_k
         const uint32_t b_lds = lds0 + A_RING + wb * Loader::BI * 1024;
         auto issue_b = [&](int e, int64_t w) {
             if (BSP_SKIP(p, kSkipDenseRead)) return;  // left out: the wave's waits pass at once
-            const uint16_t* bpan = p.b + (int64_t)(uint32_t)w * p.ldb + (int32_t)(w >> 32);
-            const uint32_t dst = b_lds + (uint32_t)(e % SB) * Loader::BYTES;
-#pragma unroll
-            for (int j = 0; j < Loader::BI; ++j) gl_lds16_s(ld.voff[j], bpan, dst + j * 1024);
+            ld.issue(b_slice(p.b, p.ldb, w), b_lds + (uint32_t)(e % SB) * Loader::BYTES);
         };
         if constexpr (EPS == 2)
             stream_loader2<SB, Loader::BI>(n, head->bw, p.bw + wg.w_begin, issue_b);
@@ -1549,10 +1587,10 @@ __global__ __launch_bounds__(64 * (8 + 1 + NBW), 1) void spmm_sweep_kernel(SpmmS
         for (int j = 0; j < 2; ++j) a_voff[j] = 2 * a_row_load_offset(j, lane, p.lda);
         auto issue_a = [&](int e, uint32_t w) {
             if (BSP_SKIP(p, kSkipSparseRead)) return;  // left out: the wave's waits pass at once
-            const uint16_t* ablk = p.a + (int64_t)w * 32;
+            const uint16_t* ablk = p.a + (uint64_t)w * 32;
             const uint32_t dst = lds0 + (uint32_t)(e % SA) * kA_BYTES;
-            gl_lds16_s(a_voff[0], ablk, dst);
-            gl_lds16_s(a_voff[1], ablk, dst + 1024);
+            gl_lds16_si<0>(a_voff[0], ablk, dst);
+            gl_lds16_si<1024>(a_voff[1], ablk, dst);
         };
         stream_loader2<SA, 2>(n, head->aw, p.aw + wg.w_begin, issue_a);
         return;
@@ -1563,10 +1601,7 @@ __global__ __launch_bounds__(64 * (8 + 1 + NBW), 1) void spmm_sweep_kernel(SpmmS
         const uint32_t b_lds = lds0 + A_RING + wb * Loader::BI * 1024;
         auto issue_b = [&](int e, int64_t w) {
             if (BSP_SKIP(p, kSkipDenseRead)) return;  // left out: the wave's waits pass at once
-            const uint16_t* bpan = p.b + (int64_t)(uint32_t)w * p.ldb + (int32_t)((w >> 32) & 0xffffff);
-            const uint32_t dst = b_lds + (uint32_t)(e % SB) * Loader::BYTES;
-#pragma unroll
-            for (int j = 0; j < Loader::BI; ++j) gl_lds16_s(ld.voff[j], bpan, dst + j * 1024);
+            ld.issue(b_slice<24>(p.b, p.ldb, w), b_lds + (uint32_t)(e % SB) * Loader::BYTES);
         };
         stream_loader2<SB, Loader::BI>(n, head->bw, p.bw + wg.w_begin, issue_b);
         return;
