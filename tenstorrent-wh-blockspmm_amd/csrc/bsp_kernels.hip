@@ -285,6 +285,18 @@ __device__ __forceinline__ void wait_vmcnt() {
     __asm__ volatile("" ::: "memory");
 }
 
+// Waits until this wave's LDS accesses (and scalar loads) have completed.
+// The builtin, not inline asm: the compiler's own wait insertion then knows
+// that the LDS reads before it have returned, and adds no waits of its own
+// before later uses of the registers they wrote (with the asm form it kept
+// them pending and made the products of a step wait for the reads of the
+// next).
+__device__ __forceinline__ void wait_lgkm0() {
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __asm__ volatile("" ::: "memory");
+}
+
 // Waits until at most PER*n + EXTRA vector loads of this wave are
 // outstanding, n <= NMAX.
 template <int PER, int NMAX, int EXTRA = 0>
@@ -401,7 +413,7 @@ __device__ __forceinline__ void run_ring(int n, Issue&& issue, Read&& read, Mult
     landed();
     auto xchg = [] {
         if constexpr (XCHG) {
-            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            spmm_detail::wait_lgkm0();
             barrier_no_fence();
         }
     };
@@ -413,7 +425,7 @@ __device__ __forceinline__ void run_ring(int n, Issue&& issue, Read&& read, Mult
     // wave's; the compiler would otherwise wait for them only at their first
     // use, after the barrier and the next issue).
     auto sync = [&](int k) {
-        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        spmm_detail::wait_lgkm0();
         if (k <= n - S)
             wait_vmcnt<PER * (S - 2)>();         // entry k+1 landed
         else
@@ -426,7 +438,7 @@ __device__ __forceinline__ void run_ring(int n, Issue&& issue, Read&& read, Mult
     // issue, so the steady state carries no branches for the ring's tail
     // (scalar instructions are the per-entry cost of this loop).
     auto sync_full = [&](int k) {
-        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        spmm_detail::wait_lgkm0();
         wait_vmcnt<PER * (S - 2)>();
         barrier_no_fence();
         issue(k + S, stage);
@@ -540,7 +552,7 @@ __device__ __forceinline__ void run_ring_halves(int n, Issue&& issue, Read&& rea
         read(k, stage, o, 1);
         interleave();
         fence_sched();
-        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        spmm_detail::wait_lgkm0();
         // Entry k+1 landed: at most the loads of the entries after it are outstanding.
         if constexpr (EXTRA == 0 || S % 2 == 0) {
             if (full || k <= n - S)
@@ -1445,7 +1457,7 @@ __global__ __launch_bounds__(64 * (4 * SR + 1 + NBW) * PIPES) void spmm_stream_k
         }
     };
     auto fence_sched = [] { __builtin_amdgcn_sched_barrier(0); };
-    auto lds_done = [] { __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); };
+    auto lds_done = [] { wait_lgkm0(); };
     if constexpr (EPS == 2) {
         struct Pair {
             Operands e0, e1;
@@ -1740,7 +1752,7 @@ __global__ __launch_bounds__(64 * (8 + 1 + NBW), 1) void spmm_sweep_kernel(SpmmS
             : "v"(o.a[0]), "v"(o.a[1]), "v"(o.b[0][0]), "v"(o.b[1][0]), "s"(slot)
             : "scc");
     };
-    auto lds_done = [] { __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); };
+    auto lds_done = [] { wait_lgkm0(); };
     // Step k (k = 0, 2, 4, ...; the loaders' barrier for entries k and k+1):
     // read and multiply this group's entries among k and k+1.
     // This group's entry among a step's two: its slot, or -1.
@@ -2145,12 +2157,12 @@ __global__ __launch_bounds__(256) void sddmm_kernel(SddmmArgs p) {
             // reads of the previous entry; the waits before each barrier make
             // the LDS accesses complete without a fence (a fence would also
             // wait for the next unit's loads, which stay in flight).
-            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            spmm_detail::wait_lgkm0();
             spmm_detail::barrier_no_fence();
             float* mine = red[wave];
 #pragma unroll
             for (int v = 0; v < 16; ++v) mine[v * 64 + lane] = acc[v];
-            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            spmm_detail::wait_lgkm0();
             spmm_detail::barrier_no_fence();
             const int64_t off = entry_off(eu);
 #pragma unroll
@@ -2474,7 +2486,7 @@ __global__ __launch_bounds__(256) void spgemm_kernel(SpgemmArgs p) {
             // reads of it are complete once lgkmcnt is 0 (no scalar loads are
             // in flight here, so the wait covers only those reads).
             if (k + S - 1 < n) {
-                __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                spmm_detail::wait_lgkm0();
                 issue(k + S - 1, stage == 0 ? S - 1 : stage - 1);
             }
             // Product k landed (stores in flight only make this wait longer:
