@@ -1756,11 +1756,14 @@ __global__ __launch_bounds__(64 * (8 + 1 + NBW), 1) void spmm_sweep_kernel(SpmmS
     // Step k (k = 0, 2, 4, ...; the loaders' barrier for entries k and k+1):
     // read and multiply this group's entries among k and k+1.
     // This group's entry among a step's two: its slot, or -1.
-    auto mine = [&](int64_t w) __attribute__((always_inline)) {
-        const uint32_t code = (uint32_t)((uint64_t)w >> kSweepSlotShift) & 31u;
+    // (w: the high half of the entry's word, which holds the slot code and
+    // the last bit.)
+    auto mine = [&](uint32_t w) __attribute__((always_inline)) {
+        const uint32_t code = (w >> (kSweepSlotShift - 32)) & 31u;
         return (code & 16u) == 0 && (int)(code >> 3) == group ? (int)(code & 7u) : -1;
     };
-    auto step = [&](int k, int64_t w0, int64_t w1) __attribute__((always_inline)) {
+    constexpr uint32_t kLastHi = (uint32_t)((uint64_t)kSweepLast >> 32);
+    auto step = [&](int k, uint32_t w0, uint32_t w1) __attribute__((always_inline)) {
         barrier_no_fence();
         const int s0 = mine(w0), s1 = mine(w1);
         Ops o;
@@ -1768,13 +1771,13 @@ __global__ __launch_bounds__(64 * (8 + 1 + NBW), 1) void spmm_sweep_kernel(SpmmS
             read(k, o);
             lds_done();
             multiply(o, s0);
-            if (w0 & kSweepLast) store_slot(s0);  // the unit's last entry
+            if (w0 & kLastHi) store_slot(s0);  // the unit's last entry
         }
         if (s1 >= 0) {
             read(k + 1, o);
             lds_done();
             multiply(o, s1);
-            if (w1 & kSweepLast) store_slot(s1);
+            if (w1 & kLastHi) store_slot(s1);
         }
         left -= 2;
         if (left == 0) {
@@ -1783,20 +1786,22 @@ __global__ __launch_bounds__(64 * (8 + 1 + NBW), 1) void spmm_sweep_kernel(SpmmS
             open();
         }
     };
-    // The stream's B words, two (a step's) at a time by a scalar load one step
-    // ahead, waited for with the step's LDS reads (the arrays are padded past
-    // every stream's end).
-    struct W2 {
-        int64_t w[2];
-    };
-    const W2* wp = (const W2*)(p.bw + wg.w_begin);
-    W2 cur = load_const(wp);
+    // The high halves of the stream's B words, a step's two by scalar loads
+    // one step ahead, waited for with the step's LDS reads (the arrays are
+    // padded past every stream's end).  Only the high halves: with whole
+    // words, the compiler reused the registers of the unused low halves
+    // while their load was in flight, and so waited for the load at once,
+    // at the top of every step.
+    const uint32_t* wh = (const uint32_t*)(p.bw + wg.w_begin) + 1;
+    uint32_t c0 = load_const(wh), c1 = load_const(wh + 2);
+    wait_lgkm0();
     for (int k = 0; k < n; k += 2) {
-        const W2 nxt = load_const(wp + k / 2 + 1);
-        step(k, cur.w[0], cur.w[1]);
+        const uint32_t n0 = load_const(wh + 2 * k + 4), n1 = load_const(wh + 2 * k + 6);
+        step(k, c0, c1);
         if (k == 0) BSP_TL_MARK(1);
         if ((k & 7) == 0 && k < 8 * 60) BSP_TL_MARK(2 + (k >> 3));
-        cur = nxt;
+        c0 = n0;
+        c1 = n1;
     }
     if (wave == 0) BSP_TL_FLUSH();
 }
